@@ -1,0 +1,279 @@
+#!/usr/bin/env python3
+"""Benchmark: one full Muon optimizer step over the Llama-3-8B-shaped matrix set on one MI355X.
+
+Workload (BASELINE config c5): 32 layers x {q, o 4096x4096; k, v 1024x4096; gate, up
+14336x4096; down 4096x14336} = 224 matrices, bf16 weights and gradients ~N(0, 0.02^2), fp32
+momentum, all owned by the single rank; dmuon_amd.Muon(lr=0.02, momentum=0.95 Nesterov,
+weight_decay=0.1) with 5 direct Newton-Schulz steps of Keller's (3.4445, -4.7750, 2.0315).
+A "step" is one optimizer.step() over the set (momentum, normalisation, 5 NS steps, update).
+Synthetic data is generated on the GPU (values do not affect timing).
+
+Prints ONE JSON line. Extra fields: per-kernel-class breakdown from the library's hipEvent
+profiler (a second, separately timed pass), the roofline of the dominant kernel family (the
+bf16 MFMA NT kernels: SYRK, SYRK-poly, GEMM) and of the fused momentum kernel, the AdamW
+step for the embeddings/norms (reported separately), and a CPU baseline: the numpy restatement
+of the reference math on the host cores, over a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+LLAMA3_8B_LAYER = {  # name: (rows, cols)
+    "q": (4096, 4096), "k": (1024, 4096), "v": (1024, 4096), "o": (4096, 4096),
+    "gate": (14336, 4096), "up": (14336, 4096), "down": (4096, 14336),
+}
+N_LAYERS = 32
+KELLER = [(3.4445, -4.7750, 2.0315)] * 5
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+
+
+def ns_useful_flops(rows, cols, steps=5):
+    m, n = min(rows, cols), max(rows, cols)
+    return float(steps) * (m * (m + 1) * n + m * (m + 1) * m + 2.0 * m * m * n)
+
+
+def build_matrix_set(torch, device, dtype, n_layers):
+    from torch import nn
+
+    class MatrixSet(nn.Module):
+        def __init__(self):
+            super().__init__()
+            gen = torch.Generator(device=device).manual_seed(0)
+            self.mats = nn.ParameterList()
+            for _ in range(n_layers):
+                for _name, shape in LLAMA3_8B_LAYER.items():
+                    w = torch.empty(shape, device=device, dtype=dtype)
+                    w.normal_(0.0, 0.02, generator=gen)
+                    self.mats.append(nn.Parameter(w))
+
+    m = MatrixSet()
+    gen = torch.Generator(device=device).manual_seed(1)
+    for p in m.parameters():
+        g = torch.empty_like(p)
+        g.normal_(0.0, 0.02, generator=gen)
+        p.grad = g
+    return m
+
+
+def cpu_baseline(budget_s: float = 25.0) -> dict:
+    """Times the oracle (numpy restatement of the reference math, fp32 compute) on the host:
+    momentum + Nesterov + direct NS x5 + update, for layer-0's k, q and down matrices; the full
+    step is extrapolated by matrix counts (v, o, gate, up share those NS costs)."""
+    import numpy as np
+
+    from oracle import ns_oracle as o
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    per = {}
+    spent = 0.0
+    for name, count in (("k", 2), ("q", 2), ("down", 3)):
+        rows, cols = LLAMA3_8B_LAYER[name]
+        W = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
+        g = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
+        buf = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
+        t0 = time.perf_counter()
+        o.muon_step(W, g, buf, lr=0.02, mu=0.95, wd=0.1, coefficients=o.KELLER, ns="direct",
+                    dtype="fp32")
+        dt = time.perf_counter() - t0
+        spent += dt
+        per[name] = (dt, count)
+        if spent > budget_s and name != "down":
+            break
+    # per-layer time: k,v share the k cost; q,o the q cost; gate, up, down the down cost
+    layer_s = sum(dt * count for dt, count in per.values())
+    missing = {"k", "q", "down"} - set(per)
+    if missing:
+        return {"value": None, "unit": "ms", "cores": threads, "kind": "port",
+                "sample": f"incomplete: budget exhausted before {sorted(missing)}"}
+    return {
+        "value": round(layer_s * N_LAYERS * 1e3, 1),
+        "unit": "ms",
+        "cores": threads,
+        "kind": "port",
+        "sample": ("oracle/ns_oracle.muon_step (numpy, fp32 compute; the reference's fp16 "
+                   "casts are not emulated) on one k (1024x4096), one q (4096x4096) and one down "
+                   f"(4096x14336) matrix = {spent:.1f} s of CPU work; full 224-matrix step "
+                   "extrapolated as 32 layers x (2k + 2q + 3down)"),
+        "per_matrix_s": {k: round(v[0], 3) for k, v in per.items()},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--layers", type=int, default=N_LAYERS, help="layers of the matrix set")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-adamw", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=25.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures the single-GPU owner path only: "
+                          "run bench.py with --gpus 1 (multi-GPU sharding is described in "
+                          "DESIGN.md, not benchmarked)"}))
+        sys.exit(2)
+
+    import torch
+
+    import dmuon_amd as dmuon
+    from dmuon_amd import _C
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    model = build_matrix_set(torch, dev, torch.bfloat16, args.layers)
+    dmuon.dedicate_params(model, None, lambda n, p: p.dim() == 2)
+    dmuon.replicate(model)
+    opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1,
+                     ns_backend=dmuon.NewtonSchulz("direct", coefficients=KELLER))
+    n_mats = sum(1 for _ in model.parameters())
+    n_elems = sum(p.numel() for p in model.parameters())
+    flops = sum(ns_useful_flops(*p.shape) for p in model.parameters())
+
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+
+    # ---- timed region: exactly K optimizer steps ---------------------------------------------
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        opt.step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+
+    # ---- kernel breakdown: the same steps with the library's per-launch hipEvents -------------
+    prof_steps = max(1, min(3, args.steps))
+    _C.profile_collect()
+    _C.profile_enable(True)
+    for _ in range(prof_steps):
+        opt.step()
+    torch.cuda.synchronize()
+    _C.profile_enable(False)
+    prof = _C.profile_collect()
+    classes = {}
+    for name, r in prof.items():
+        if r["launches"] == 0:
+            continue
+        ms = r["ms"] / prof_steps
+        ent = {"ms_per_step": round(ms, 3), "launches_per_step": r["launches"] // prof_steps,
+               "avg_launch_us": round(1e3 * r["ms"] / r["launches"], 2)}
+        if r["flops"] > 0:
+            ent["tflops"] = round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1)
+        if r["bytes"] > 0 and r["flops"] == 0:
+            ent["gbs"] = round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)
+        classes[name] = ent
+    mf = [prof[c] for c in ("syrk", "poly", "gemm", "final")]
+    mf_ms = sum(r["ms"] for r in mf)
+    mf_launch = sum(r["launches"] for r in mf)
+    mf_flops = sum(r["flops"] for r in mf)
+    achieved_tf = mf_flops / (mf_ms * 1e-3) / 1e12
+    pre = prof["pre"]
+    pre_gbs = pre["bytes"] / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
+
+    # ---- AdamW-routed params of the c5 config (embeddings, lm_head, norms), reported apart ----
+    adamw = None
+    if not args.no_adamw:
+        from torch import nn
+
+        class Rest(nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.embed = nn.Parameter(torch.zeros(128256, 4096, device=dev, dtype=torch.bfloat16))
+                self.lm_head = nn.Parameter(torch.zeros(128256, 4096, device=dev, dtype=torch.bfloat16))
+                self.norms = nn.ParameterList(
+                    [nn.Parameter(torch.ones(4096, device=dev, dtype=torch.bfloat16)) for _ in range(65)])
+                self.proj = nn.Parameter(torch.zeros(256, 256, device=dev, dtype=torch.bfloat16))
+
+        del opt
+        rest = Rest()
+        for p in rest.parameters():
+            p.grad = torch.randn_like(p) * 0.02
+        dmuon.dedicate_params(rest, None, lambda n, p: n == "proj")
+        dmuon.replicate(rest)
+        opt2 = dmuon.Muon(rest, adamw_lr=1e-3)
+        adam_groups = [g for g in opt2.param_groups if not g["use_muon"]]
+
+        def adamw_step():
+            for g in adam_groups:
+                opt2._step_adamw_group(g)
+
+        adamw_step()
+        torch.cuda.synchronize()
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record()
+        for _ in range(3):
+            adamw_step()
+        a1.record()
+        torch.cuda.synchronize()
+        adamw = {"ms_per_step": round(a0.elapsed_time(a1) / 3, 3),
+                 "params": int(sum(p.numel() for n, p in rest.named_parameters() if n != "proj")),
+                 "impl": "torch._foreach (reference muon.py:1857-1916 semantics)"}
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
+
+    out = {
+        "metric": "Muon step ms (8B matrix set, 1 GPU); NS TFLOPS + % bf16 MFMA peak",
+        "value": round(ms_per_step, 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"Llama-3-8B matrix set: {args.layers} layers x 7 matrices "
+                               f"({n_mats} bf16 matrices, {n_elems / 1e9:.2f} G elements), "
+                               "fp32 momentum, 5 direct NS steps (Keller)",
+                   "matrices": n_mats, "useful_ns_tflop_per_step": round(flops / 1e12, 2),
+                   "parallelism": "single GPU (world_size=1 owner)"},
+        "ns_tflops": round(flops / (ms_per_step * 1e-3) / 1e12, 1),
+        "ns_frac_mfma_peak_step": round(flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "roofline": {
+            "kernel": "nt_mfma_kernel (SYRK X X^T, SYRK-poly, NS GEMM, final GEMM+update)",
+            "bound": "mfma", "achieved": round(achieved_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(1e3 * mf_ms / max(mf_launch, 1), 2),
+            "launches_per_step": mf_launch // prof_steps,
+        },
+        "roofline_elementwise": {
+            "kernel": "muon_pre_kernel (momentum + Nesterov + bf16 staging + norm partials)",
+            "bound": "hbm", "achieved": None if pre_gbs is None else round(pre_gbs, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": None if pre_gbs is None else round(pre_gbs / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_elem": 12,
+        },
+        "kernel_classes": classes,
+        "adamw_rest": adamw,
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 3),
+        "device": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

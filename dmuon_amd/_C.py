@@ -1,0 +1,109 @@
+"""ctypes binding of libdmuon_amd.so (the C ABI declared in include/dmuon_amd.h).
+
+There is no fallback: if the library is missing or fails to load, importing the compute
+entry points raises. Build it with ``python -m dmuon_amd.csrc.build`` (``__graft_entry__.build``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional
+
+_LIB_PATH = Path(__file__).resolve().parent / "csrc" / "libdmuon_amd.so"
+_lib: Optional[ctypes.CDLL] = None
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+c_int, c_i64, c_f, c_d, c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
+c_fp = ctypes.POINTER(ctypes.c_float)
+
+# name -> (restype, argtypes); mirrors include/dmuon_amd.h
+_SIGNATURES = {
+    "dmuon_last_error": (ctypes.c_char_p, []),
+    "dmuon_abi_version": (c_int, []),
+    "dmuon_profile_enable": (c_int, [c_int]),
+    "dmuon_profile_collect": (c_int, [ctypes.POINTER(c_d), ctypes.POINTER(c_i64),
+                                      ctypes.POINTER(c_d), ctypes.POINTER(c_d), c_int]),
+    "dmuon_syrk_bf16": (c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp,
+                                c_i64, c_i64, c_int, c_int, c_int, c_f, c_f, c_f, c_vp, c_int, c_vp]),
+    "dmuon_ns_gemm_bf16": (c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
+                                   c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_int, c_int, c_int,
+                                   c_f, c_f, c_vp, c_int, c_vp]),
+    "dmuon_ns_gemm_final_bf16": (c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64,
+                                         c_i64, c_int, c_int, c_int, c_f, c_f, c_vp, c_int, c_int,
+                                         c_int, c_vp, c_int, c_vp, c_int, c_f, c_f, c_int, c_vp]),
+    "dmuon_muon_pre_partials": (c_int, [c_int, c_int]),
+    "dmuon_muon_pre": (c_int, [c_vp, c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp,
+                               c_int, c_int, c_int, c_int, c_int, c_f, c_int, c_int, c_vp]),
+    "dmuon_norm_finalize": (c_int, [c_vp, c_int, c_int, c_f, c_vp, c_vp, c_vp]),
+    "dmuon_muon_update": (c_int, [c_vp, c_int, c_vp, c_int, c_i64, c_int, c_f, c_f, c_vp]),
+    "dmuon_ns_plan": (c_int, [c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int),
+                              ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_i64)]),
+    "dmuon_muon_step_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int, c_d,
+                                      c_d, c_d, c_int, c_int, c_fp, c_int, c_f, c_vp, c_i64,
+                                      c_int, c_vp]),
+    "dmuon_newton_schulz_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_fp,
+                                          c_int, c_f, c_vp, c_i64, c_int, c_vp]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+def lib_path() -> Path:
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """Loads (once) and returns the library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not _LIB_PATH.exists():
+        raise RuntimeError(
+            f"{_LIB_PATH} is missing: build the HIP kernels first "
+            "(python -m dmuon_amd.csrc.build). dmuon_amd has no CPU fallback."
+        )
+    handle = ctypes.CDLL(os.fspath(_LIB_PATH))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = handle
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = lib().dmuon_last_error().decode(errors="replace")
+        raise RuntimeError(f"dmuon_amd: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))
+
+
+PROFILE_CLASSES = ("pre", "norm", "syrk", "poly", "gemm", "final")
+
+
+def profile_enable(on: bool) -> None:
+    check(lib().dmuon_profile_enable(1 if on else 0))
+
+
+def profile_collect() -> dict:
+    """Per kernel class: {"ms", "launches", "flops", "bytes"} since the last collect."""
+    n = 8
+    ms, cnt = (c_d * n)(), (c_i64 * n)()
+    fl, by = (c_d * n)(), (c_d * n)()
+    check(lib().dmuon_profile_collect(ms, cnt, fl, by, n))
+    return {name: {"ms": ms[i], "launches": cnt[i], "flops": fl[i], "bytes": by[i]}
+            for i, name in enumerate(PROFILE_CLASSES)}
+
+
+def plan(rows: int, cols: int, batch: int, tile: int = 0, num_cus: int = 0):
+    """(tile, m_pad, n_pad, workspace_bytes) for a group of same-shape matrices."""
+    t, mp, np_, ws = c_int(), c_int(), c_int(), c_i64()
+    check(lib().dmuon_ns_plan(rows, cols, batch, tile, num_cus, ctypes.byref(t), ctypes.byref(mp),
+                              ctypes.byref(np_), ctypes.byref(ws)))
+    return t.value, mp.value, np_.value, ws.value

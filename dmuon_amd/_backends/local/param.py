@@ -1,0 +1,88 @@
+"""world_size=1 data contract of the reference's dedicated-parameter runtime.
+
+At one rank every dedicated parameter is owned locally, the grad reduce-to-owner is the
+identity and the post-step publish has no peer, so the objects below keep only the fields the
+optimizer reads and writes (reference: ``dmuon/_backends/fsdp2/param.py:116-628``,
+``fsdp2/group.py:276-2177``, ``dmuon/_core/comm.py:24-110``):
+
+* ``_owned_data``  -- the owner's copy of the weight; here the live parameter storage itself,
+  so an in-place update is what the next forward reads (no packed-buffer publish).
+* ``_reduced_grad`` -- the reduced gradient the Muon step consumes (``group.py:1348-1352``);
+  here the parameter's ``.grad``, set by :func:`dmuon_amd.prepare_muon_grads` or read directly
+  by the optimizer; cleared after the update (``muon.py:1746-1747``).
+* ``is_owner``, ``full_shape``, ``tp_group`` (always None: no tensor parallelism here).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import nn
+
+
+class DedicatedParam:
+    def __init__(self, param: nn.Parameter, name: str, owner_rank: int = 0):
+        self.param = param
+        self._orig_param = param
+        self.param_name = name
+        self.owner_rank = owner_rank
+        self.is_owner = True
+        self.full_shape = tuple(param.shape)
+        self.tp_group = None
+        self.is_dtensor = False
+        self.is_tp_owner = False
+        self._reduced_grad: Optional[torch.Tensor] = None
+        self._accumulated_grad: Optional[torch.Tensor] = None
+
+    @property
+    def _owned_data(self) -> torch.Tensor:
+        return self.param.data
+
+    def current_grad(self) -> Optional[torch.Tensor]:
+        g = self._reduced_grad
+        return self.param.grad if g is None else g
+
+    def uses_sharded_muon_forward(self) -> bool:
+        return False
+
+    def __repr__(self) -> str:
+        return f"DedicatedParam({self.param_name}, shape={self.full_shape}, owner={self.owner_rank})"
+
+
+class DedicatedParamGroup:
+    def __init__(self, params: list[DedicatedParam]):
+        self.params = params
+        self.replicate_group = None
+
+    # reduce / publish hooks are identities at world_size=1 (group.py:1727-1729, :1792-1794)
+    def wait_for_reduce(self) -> None:
+        for dp in self.params:
+            if dp._reduced_grad is None and dp.param.grad is not None:
+                dp._reduced_grad = dp.param.grad
+
+    def replicate_broadcast_async(self) -> None:
+        return None
+
+
+class DedicatedState:
+    def __init__(self, group: DedicatedParamGroup):
+        self.group = group
+
+
+class ReplicatedGroup:
+    """Non-dedicated parameters updated by AdamW (``ddp/replicate.py:87-282`` at one rank)."""
+
+    def __init__(self, params: list[nn.Parameter]):
+        self.params = params
+
+
+class LocalCommContext:
+    """Stand-in for ``DedicatedCommContext`` (``_core/comm.py:24-110``) at world_size=1: no
+    collectives, no side streams; everything runs on the caller's current stream."""
+
+    def __init__(self) -> None:
+        self.world_size = 1
+        self.rank = 0
+        self.replicate_group = None
+        self.forward_prefetch_depth = 1
+        self.sharded_adamw_unshard_separate_stream_enabled = False

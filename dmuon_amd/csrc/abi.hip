@@ -1,0 +1,492 @@
+// extern "C" entry points of libdmuon_amd.so (declared in include/dmuon_amd.h): argument
+// validation, workspace planning and the launch sequence of one Muon group step.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/dmuon_amd.h"
+#include "dmuon_amd_internal.h"
+
+using namespace dmuon;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return 1;
+}
+
+int check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail("%s: launch failed: %s", what, hipGetErrorString(e));
+  return 0;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool ld_ok(int64_t ld) { return ld > 0 && (ld % 8) == 0; }
+bool stride_ok(int64_t s, int batch) { return batch <= 1 || (s >= 0 && (s % 8) == 0); }
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+int64_t align256(int64_t b) { return round_up(b, 256); }
+
+struct Workspace {
+  uint16_t *X, *XT0, *XT1, *Am, *Pm;
+  float *partials, *scale, *scale_sq;
+  int nparts;
+  int64_t bytes;
+};
+
+// Carves the workspace of a group; base == nullptr only computes the size.
+Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch) {
+  Workspace w{};
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  const int64_t L = batch;
+  const int64_t xs = (int64_t)m_pad * n_pad * 2;
+  const int64_t as = (int64_t)m_pad * m_pad * 2;
+  w.X = reinterpret_cast<uint16_t*>(take(L * xs));
+  w.XT0 = reinterpret_cast<uint16_t*>(take(L * xs));
+  w.XT1 = reinterpret_cast<uint16_t*>(take(L * xs));
+  w.Am = reinterpret_cast<uint16_t*>(take(L * as));
+  w.Pm = reinterpret_cast<uint16_t*>(take(L * as));
+  w.nparts = pre_blocks_per_mat(Rp, Cp);
+  w.partials = reinterpret_cast<float*>(take(L * w.nparts * 4));
+  w.scale = reinterpret_cast<float*>(take(L * 4));
+  w.scale_sq = reinterpret_cast<float*>(take(L * 4));
+  w.bytes = off;
+  return w;
+}
+
+// ---- launch profiler: optional hipEvent pairs around every kernel of run_group ----------------
+// Single-threaded use only (like the launch path itself). Events are host objects; no device
+// memory is allocated.
+enum ProfClass { PC_PRE = 0, PC_NORM, PC_SYRK, PC_POLY, PC_GEMM, PC_FINAL, PC_COUNT };
+struct ProfRec {
+  int cls;
+  hipEvent_t a, b;
+  double flops, bytes;
+};
+struct Profiler {
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  std::vector<ProfRec> recs;
+  hipEvent_t take() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+};
+Profiler g_prof;
+
+template <class F>
+int timed(int cls, double flops, double bytes, hipStream_t stream, const char* who, F&& launch) {
+  if (!g_prof.on) return check_launch(launch(), who);
+  hipEvent_t a = g_prof.take(), b = g_prof.take();
+  if (!a || !b) return fail("%s: hipEventCreate failed", who);
+  if (hipEventRecord(a, stream) != hipSuccess) return fail("%s: hipEventRecord failed", who);
+  const int rc = check_launch(launch(), who);
+  if (hipEventRecord(b, stream) != hipSuccess) return fail("%s: hipEventRecord failed", who);
+  g_prof.recs.push_back({cls, a, b, flops, bytes});
+  return rc;
+}
+
+int tri_tiles(int m_pad, int tile) {
+  const int mt = m_pad / tile;
+  return mt * (mt + 1) / 2;
+}
+
+int plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, int* m_pad,
+         int* n_pad, int64_t* bytes) {
+  if (rows <= 0 || cols <= 0 || batch <= 0)
+    return fail("dmuon_ns_plan: rows, cols and batch must be positive (got %d, %d, %d)", rows,
+                cols, batch);
+  if (tile_req != 0 && tile_req != 128 && tile_req != 256)
+    return fail("dmuon_ns_plan: tile must be 0 (auto), 128 or 256, got %d", tile_req);
+  const int m = rows < cols ? rows : cols;
+  const int n = rows < cols ? cols : rows;
+  if (num_cus <= 0) num_cus = 256;
+  int t = tile_req;
+  if (t == 0) {
+    // 256x256 tiles when they add no padding over 128 and fill the machine at least once.
+    const bool same_pad = round_up(m, 256) == round_up(m, 128) && round_up(n, 256) == round_up(n, 128);
+    const int64_t tiles = (int64_t)batch * tri_tiles((int)round_up(m, 256), 256);
+    t = (same_pad && tiles >= num_cus) ? 256 : 128;
+  }
+  const int mp = (int)round_up(m, t), np = (int)round_up(n, t);
+  const bool tall = rows > cols;
+  const int Rp = tall ? np : mp, Cp = tall ? mp : np;
+  Workspace w = carve(nullptr, mp, np, Rp, Cp, batch);
+  *tile = t;
+  *m_pad = mp;
+  *n_pad = np;
+  *bytes = w.bytes;
+  return 0;
+}
+
+// The whole Newton-Schulz + optional update sequence of one group; see dmuon_muon_step_group.
+int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* const* w_ptrs,
+              int w_dtype, void* const* out_ptrs, int out_dtype, int rows, int cols, int batch,
+              float mu, int nesterov, int first_step, float decay, float lrs, const float* coeffs,
+              int T, float eps, void* workspace, int64_t workspace_bytes, int tile_req,
+              hipStream_t stream, const char* who) {
+  if (!g_ptrs) return fail("%s: g_ptrs is NULL", who);
+  if (g_dtype != DMUON_DTYPE_F32 && g_dtype != DMUON_DTYPE_BF16)
+    return fail("%s: unsupported gradient dtype code %d", who, g_dtype);
+  if (w_ptrs && w_dtype != DMUON_DTYPE_F32 && w_dtype != DMUON_DTYPE_BF16)
+    return fail("%s: unsupported weight dtype code %d", who, w_dtype);
+  if (out_ptrs && out_dtype != DMUON_DTYPE_F32 && out_dtype != DMUON_DTYPE_BF16)
+    return fail("%s: unsupported output dtype code %d", who, out_dtype);
+  if (!coeffs || T <= 0) return fail("%s: need at least one (a, b, c) coefficient triple", who);
+  if (!workspace || !aligned16(workspace)) return fail("%s: workspace NULL or misaligned", who);
+  int tile, m_pad, n_pad;
+  int64_t need;
+  if (plan(rows, cols, batch, tile_req, 0, &tile, &m_pad, &n_pad, &need)) return 1;
+  if (workspace_bytes < need)
+    return fail("%s: workspace of %lld bytes is smaller than the %lld bytes planned", who,
+                (long long)workspace_bytes, (long long)need);
+  const bool tall = rows > cols;
+  const int m = tall ? cols : rows, n = tall ? rows : cols;
+  const int Rp = tall ? n_pad : m_pad, Cp = tall ? m_pad : n_pad;
+  Workspace w = carve(static_cast<char*>(workspace), m_pad, n_pad, Rp, Cp, batch);
+  const long long xs = (long long)m_pad * n_pad, as = (long long)m_pad * m_pad;
+
+  PreArgs p{};
+  p.g_ptrs = g_ptrs;
+  p.g_dtype = g_dtype;
+  p.buf_ptrs = buf_ptrs;
+  p.Y = tall ? w.XT0 : w.X;
+  p.ldy = tall ? m_pad : n_pad;
+  p.sY = xs;
+  p.YT = tall ? w.X : w.XT0;
+  p.ldyt = tall ? n_pad : m_pad;
+  p.sYT = xs;
+  p.partials = w.partials;
+  p.rows = rows;
+  p.cols = cols;
+  p.Rp = Rp;
+  p.Cp = Cp;
+  p.L = batch;
+  p.mu = mu;
+  p.first_step = first_step;
+  p.nesterov = nesterov;
+  const double Ld = batch, md = m, nd = n, elems = (double)rows * cols * batch;
+  const double gbytes = g_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0;
+  // algorithmic bytes: gradient read, fp32 momentum read (not on the first step) and write,
+  // one bf16 copy of ns_in
+  const double pre_bytes = elems * (gbytes + (buf_ptrs ? (first_step ? 4.0 : 8.0) : 0.0) + 2.0);
+  if (timed(PC_PRE, 0.0, pre_bytes, stream, who, [&] { return launch_pre(p, stream); })) return 1;
+  if (timed(PC_NORM, 0.0, (double)batch * w.nparts * 4, stream, who, [&] {
+        return launch_norm_finalize(w.partials, w.nparts, batch, eps, w.scale, w.scale_sq, stream);
+      }))
+    return 1;
+  const double syrk_flops = Ld * md * (md + 1) * nd, poly_flops = Ld * md * (md + 1) * md;
+  const double gemm_flops = 2.0 * Ld * md * md * nd;
+  const double wbytes = w_ptrs ? 2.0 * elems * (w_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0) : 0.0;
+  const double obytes = out_ptrs ? elems * (out_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0) : 0.0;
+
+  uint16_t* xt_cur = w.XT0;
+  uint16_t* xt_nxt = w.XT1;
+  for (int it = 0; it < T; ++it) {
+    const float ca = coeffs[3 * it], cb = coeffs[3 * it + 1], cc = coeffs[3 * it + 2];
+    // A = s^2 X X^T (s only on the first step: X holds the un-normalised ns_in)
+    NtArgs s{};
+    s.A = w.X; s.lda = n_pad; s.sA = xs;
+    s.B = w.X; s.ldb = n_pad; s.sB = xs;
+    s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch;
+    s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
+    s.mode = EPI_SYM; s.alpha = 1.f; s.beta = 0.f; s.diag = 0.f;
+    s.alpha_dev = it == 0 ? w.scale_sq : nullptr;
+    s.D = w.Am; s.ldd = m_pad; s.sD = as;
+    if (timed(PC_SYRK, syrk_flops, 0.0, stream, who, [&] { return launch_nt(s, tile, stream); }))
+      return 1;
+    // P = c A A^T + b A
+    NtArgs q{};
+    q.A = w.Am; q.lda = m_pad; q.sA = as;
+    q.B = w.Am; q.ldb = m_pad; q.sB = as;
+    q.M = m_pad; q.N = m_pad; q.K = m_pad; q.L = batch;
+    q.mt = q.nt = m_pad / tile; q.tiles_per_mat = s.tiles_per_mat; q.tri = 1;
+    q.mode = EPI_SYM; q.alpha = cc; q.beta = cb; q.diag = 0.f;
+    q.C = w.Am; q.ldc = m_pad; q.sC = as;
+    q.D = w.Pm; q.ldd = m_pad; q.sD = as;
+    if (timed(PC_POLY, poly_flops, 0.0, stream, who, [&] { return launch_nt(q, tile, stream); }))
+      return 1;
+    // X' = s (P X + a X)
+    NtArgs g{};
+    g.A = w.Pm; g.lda = m_pad; g.sA = as;
+    g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
+    g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch;
+    g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
+    g.alpha = 1.f; g.beta = ca; g.alpha_dev = it == 0 ? w.scale : nullptr;
+    g.C = w.X; g.ldc = n_pad; g.sC = xs;
+    if (it + 1 < T) {
+      g.mode = EPI_NS;
+      g.D = w.X; g.ldd = n_pad; g.sD = xs;
+      g.DT = xt_nxt; g.lddt = m_pad; g.sDT = xs;
+      if (timed(PC_GEMM, gemm_flops, 0.0, stream, who, [&] { return launch_nt(g, tile, stream); }))
+        return 1;
+      uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
+    } else {
+      g.mode = EPI_FINAL;
+      g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;
+      g.w_ptrs = w_ptrs; g.w_dtype = w_dtype; g.decay = decay; g.lrs = lrs;
+      g.m_real = m; g.n_real = n; g.transposed = tall ? 1 : 0;
+      if (timed(PC_FINAL, gemm_flops, wbytes + obytes, stream, who,
+                [&] { return launch_nt(g, tile, stream); }))
+        return 1;
+    }
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dmuon_last_error(void) { return g_last_error.c_str(); }
+
+int dmuon_profile_enable(int on) {
+  g_prof.on = on != 0;
+  return 0;
+}
+
+int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* bytes,
+                          int n_classes) {
+  if (n_classes < PC_COUNT || !ms || !launches || !flops || !bytes)
+    return fail("dmuon_profile_collect: need arrays of at least %d classes", (int)PC_COUNT);
+  for (int c = 0; c < n_classes; ++c) {
+    ms[c] = 0.0;
+    launches[c] = 0;
+    flops[c] = 0.0;
+    bytes[c] = 0.0;
+  }
+  int rc = 0;
+  for (const ProfRec& r : g_prof.recs) {
+    float t = 0.f;
+    if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&t, r.a, r.b) != hipSuccess)
+      rc = fail("dmuon_profile_collect: event query failed");
+    ms[r.cls] += t;
+    launches[r.cls] += 1;
+    flops[r.cls] += r.flops;
+    bytes[r.cls] += r.bytes;
+    g_prof.pool.push_back(r.a);
+    g_prof.pool.push_back(r.b);
+  }
+  g_prof.recs.clear();
+  return rc;
+}
+
+int dmuon_abi_version(void) { return 100; }
+
+int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
+                    int64_t strideB, const void* C, int64_t ldc, int64_t strideC, void* D,
+                    int64_t ldd, int64_t strideD, int M, int K, int batch, float alpha, float beta,
+                    float diag_add, const float* alpha_dev, int tile, void* stream) {
+  const char* who = "dmuon_syrk_bf16";
+  if (batch == 0 || M == 0) return 0;
+  if (tile != 128 && tile != 256) return fail("%s: tile must be 128 or 256, got %d", who, tile);
+  if (M < 0 || K <= 0 || batch < 0) return fail("%s: bad sizes M=%d K=%d batch=%d", who, M, K, batch);
+  if (M % tile) return fail("%s: M=%d is not a multiple of the tile %d", who, M, tile);
+  if (K % 64) return fail("%s: K=%d is not a multiple of 64", who, K);
+  if (!B) { B = A; ldb = lda; strideB = strideA; }
+  if (!A || !D) return fail("%s: A and D must be non-NULL", who);
+  if (!aligned16(A) || !aligned16(B) || !aligned16(D) || (C && !aligned16(C)))
+    return fail("%s: operands must be 16-byte aligned", who);
+  if (!ld_ok(lda) || !ld_ok(ldb) || !ld_ok(ldd) || (C && !ld_ok(ldc)))
+    return fail("%s: leading dimensions must be positive multiples of 8", who);
+  if (lda < K || ldb < K || ldd < M || (C && ldc < M))
+    return fail("%s: leading dimension smaller than the row length", who);
+  if (!stride_ok(strideA, batch) || !stride_ok(strideB, batch) || !stride_ok(strideD, batch) ||
+      (C && !stride_ok(strideC, batch)))
+    return fail("%s: batch strides must be non-negative multiples of 8", who);
+  if (D == A || D == B || (C && D == C)) return fail("%s: D must not alias A, B or C", who);
+  NtArgs s{};
+  s.A = static_cast<const uint16_t*>(A); s.lda = lda; s.sA = strideA;
+  s.B = static_cast<const uint16_t*>(B); s.ldb = ldb; s.sB = strideB;
+  s.M = M; s.N = M; s.K = K; s.L = batch;
+  s.mt = s.nt = M / tile; s.tiles_per_mat = tri_tiles(M, tile); s.tri = 1;
+  s.mode = EPI_SYM; s.alpha = alpha; s.beta = C ? beta : 0.f; s.diag = diag_add;
+  s.alpha_dev = alpha_dev;
+  s.C = static_cast<const uint16_t*>(C); s.ldc = ldc; s.sC = strideC;
+  s.D = static_cast<uint16_t*>(D); s.ldd = ldd; s.sD = strideD;
+  return check_launch(launch_nt(s, tile, static_cast<hipStream_t>(stream)), who);
+}
+
+static int gemm_common_checks(const char* who, const void* P, int64_t ldp, int64_t strideP,
+                              const void* XT, int64_t ldxt, int64_t strideXT, const void* X,
+                              int64_t ldx, int64_t strideX, int M, int N, int batch, int tile) {
+  if (tile != 128 && tile != 256) return fail("%s: tile must be 128 or 256, got %d", who, tile);
+  if (M <= 0 || N <= 0 || batch < 0) return fail("%s: bad sizes M=%d N=%d batch=%d", who, M, N, batch);
+  if (M % tile || N % tile) return fail("%s: M=%d and N=%d must be multiples of the tile %d", who, M, N, tile);
+  if (!P || !XT) return fail("%s: P and XT must be non-NULL", who);
+  if (!aligned16(P) || !aligned16(XT) || (X && !aligned16(X)))
+    return fail("%s: operands must be 16-byte aligned", who);
+  if (!ld_ok(ldp) || !ld_ok(ldxt) || (X && !ld_ok(ldx)) || ldp < M || ldxt < M || (X && ldx < N))
+    return fail("%s: bad leading dimensions", who);
+  if (!stride_ok(strideP, batch) || !stride_ok(strideXT, batch) || (X && !stride_ok(strideX, batch)))
+    return fail("%s: batch strides must be non-negative multiples of 8", who);
+  return 0;
+}
+
+int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT, int64_t ldxt,
+                       int64_t strideXT, const void* X, int64_t ldx, int64_t strideX, void* Xout,
+                       int64_t ldxo, int64_t strideXo, void* XTout, int64_t ldxto,
+                       int64_t strideXTo, int M, int N, int batch, float alpha, float beta,
+                       const float* alpha_dev, int tile, void* stream) {
+  const char* who = "dmuon_ns_gemm_bf16";
+  if (batch == 0) return 0;
+  if (gemm_common_checks(who, P, ldp, strideP, XT, ldxt, strideXT, X, ldx, strideX, M, N, batch, tile))
+    return 1;
+  if (!Xout || !aligned16(Xout) || !ld_ok(ldxo) || ldxo < N || !stride_ok(strideXo, batch))
+    return fail("%s: bad Xout", who);
+  if (XTout && (!aligned16(XTout) || !ld_ok(ldxto) || ldxto < M || !stride_ok(strideXTo, batch)))
+    return fail("%s: bad XTout", who);
+  if (XTout == XT) return fail("%s: XTout must not alias XT", who);
+  if (Xout == P || Xout == XT) return fail("%s: Xout must not alias P or XT", who);
+  NtArgs g{};
+  g.A = static_cast<const uint16_t*>(P); g.lda = ldp; g.sA = strideP;
+  g.B = static_cast<const uint16_t*>(XT); g.ldb = ldxt; g.sB = strideXT;
+  g.M = M; g.N = N; g.K = M; g.L = batch;
+  g.mt = M / tile; g.nt = N / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
+  g.mode = EPI_NS; g.alpha = alpha; g.beta = X ? beta : 0.f; g.alpha_dev = alpha_dev;
+  g.C = static_cast<const uint16_t*>(X); g.ldc = ldx; g.sC = strideX;
+  g.D = static_cast<uint16_t*>(Xout); g.ldd = ldxo; g.sD = strideXo;
+  g.DT = static_cast<uint16_t*>(XTout); g.lddt = ldxto; g.sDT = strideXTo;
+  return check_launch(launch_nt(g, tile, static_cast<hipStream_t>(stream)), who);
+}
+
+int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT,
+                             int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx,
+                             int64_t strideX, int M, int N, int batch, float alpha, float beta,
+                             const float* alpha_dev, int m_real, int n_real, int transposed,
+                             void* const* out_ptrs, int out_dtype, void* const* w_ptrs,
+                             int w_dtype, float decay, float lrs, int tile, void* stream) {
+  const char* who = "dmuon_ns_gemm_final_bf16";
+  if (batch == 0) return 0;
+  if (gemm_common_checks(who, P, ldp, strideP, XT, ldxt, strideXT, X, ldx, strideX, M, N, batch, tile))
+    return 1;
+  if (m_real <= 0 || n_real <= 0 || m_real > M || n_real > N)
+    return fail("%s: real extent %dx%d outside the padded %dx%d", who, m_real, n_real, M, N);
+  if (!out_ptrs && !w_ptrs) return fail("%s: nothing to write (out_ptrs and w_ptrs NULL)", who);
+  if (out_ptrs && out_dtype != DMUON_DTYPE_F32 && out_dtype != DMUON_DTYPE_BF16)
+    return fail("%s: unsupported output dtype %d", who, out_dtype);
+  if (w_ptrs && w_dtype != DMUON_DTYPE_F32 && w_dtype != DMUON_DTYPE_BF16)
+    return fail("%s: unsupported weight dtype %d", who, w_dtype);
+  NtArgs g{};
+  g.A = static_cast<const uint16_t*>(P); g.lda = ldp; g.sA = strideP;
+  g.B = static_cast<const uint16_t*>(XT); g.ldb = ldxt; g.sB = strideXT;
+  g.M = M; g.N = N; g.K = M; g.L = batch;
+  g.mt = M / tile; g.nt = N / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
+  g.mode = EPI_FINAL; g.alpha = alpha; g.beta = X ? beta : 0.f; g.alpha_dev = alpha_dev;
+  g.C = static_cast<const uint16_t*>(X); g.ldc = ldx; g.sC = strideX;
+  g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;
+  g.w_ptrs = w_ptrs; g.w_dtype = w_dtype; g.decay = decay; g.lrs = lrs;
+  g.m_real = m_real; g.n_real = n_real; g.transposed = transposed ? 1 : 0;
+  return check_launch(launch_nt(g, tile, static_cast<hipStream_t>(stream)), who);
+}
+
+int dmuon_muon_pre_partials(int Rp, int Cp) { return pre_blocks_per_mat(Rp, Cp); }
+
+int dmuon_muon_pre(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* Y, int64_t ldy,
+                   int64_t strideY, void* YT, int64_t ldyt, int64_t strideYT, float* partials,
+                   int rows, int cols, int Rp, int Cp, int batch, float mu, int first_step,
+                   int nesterov, void* stream) {
+  const char* who = "dmuon_muon_pre";
+  if (batch == 0) return 0;
+  if (!g_ptrs || !Y || !YT || !partials) return fail("%s: NULL argument", who);
+  if (g_dtype != DMUON_DTYPE_F32 && g_dtype != DMUON_DTYPE_BF16)
+    return fail("%s: unsupported gradient dtype %d", who, g_dtype);
+  if (rows <= 0 || cols <= 0 || batch < 0) return fail("%s: bad sizes", who);
+  if (Rp % 64 || Cp % 64 || Rp < rows || Cp < cols)
+    return fail("%s: padded extent %dx%d must be multiples of 64 covering %dx%d", who, Rp, Cp, rows, cols);
+  if (!aligned16(Y) || !aligned16(YT) || !ld_ok(ldy) || !ld_ok(ldyt) || ldy < Cp || ldyt < Rp ||
+      !stride_ok(strideY, batch) || !stride_ok(strideYT, batch))
+    return fail("%s: bad Y/YT layout", who);
+  PreArgs p{};
+  p.g_ptrs = g_ptrs; p.g_dtype = g_dtype; p.buf_ptrs = buf_ptrs;
+  p.Y = static_cast<uint16_t*>(Y); p.ldy = ldy; p.sY = strideY;
+  p.YT = static_cast<uint16_t*>(YT); p.ldyt = ldyt; p.sYT = strideYT;
+  p.partials = partials;
+  p.rows = rows; p.cols = cols; p.Rp = Rp; p.Cp = Cp; p.L = batch;
+  p.mu = mu; p.first_step = first_step; p.nesterov = nesterov;
+  return check_launch(launch_pre(p, static_cast<hipStream_t>(stream)), who);
+}
+
+int dmuon_norm_finalize(const float* partials, int nparts, int batch, float eps, float* scale,
+                        float* scale_sq, void* stream) {
+  const char* who = "dmuon_norm_finalize";
+  if (batch == 0) return 0;
+  if (!partials || !scale || !scale_sq || nparts <= 0 || batch < 0) return fail("%s: bad arguments", who);
+  return check_launch(launch_norm_finalize(partials, nparts, batch, eps, scale, scale_sq,
+                                           static_cast<hipStream_t>(stream)),
+                      who);
+}
+
+int dmuon_muon_update(void* const* w_ptrs, int w_dtype, const void* const* u_ptrs, int u_dtype,
+                      int64_t numel, int batch, float decay, float lrs, void* stream) {
+  const char* who = "dmuon_muon_update";
+  if (batch == 0 || numel == 0) return 0;
+  if (!w_ptrs || !u_ptrs || numel < 0 || batch < 0) return fail("%s: bad arguments", who);
+  if ((w_dtype != DMUON_DTYPE_F32 && w_dtype != DMUON_DTYPE_BF16) ||
+      (u_dtype != DMUON_DTYPE_F32 && u_dtype != DMUON_DTYPE_BF16))
+    return fail("%s: unsupported dtype", who);
+  UpdateArgs u{};
+  u.w_ptrs = w_ptrs; u.w_dtype = w_dtype; u.u_ptrs = u_ptrs; u.u_dtype = u_dtype;
+  u.numel = numel; u.L = batch; u.decay = decay; u.lrs = lrs;
+  return check_launch(launch_update(u, static_cast<hipStream_t>(stream)), who);
+}
+
+int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, int* m_pad,
+                  int* n_pad, int64_t* workspace_bytes) {
+  if (!tile || !m_pad || !n_pad || !workspace_bytes) return fail("dmuon_ns_plan: NULL output");
+  return plan(rows, cols, batch, tile_req, num_cus, tile, m_pad, n_pad, workspace_bytes);
+}
+
+int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
+                          void* const* w_ptrs, int w_dtype, int rows, int cols, int batch,
+                          double lr, double mu, double wd, int nesterov, int first_step,
+                          const float* coeffs, int T, float eps, void* workspace,
+                          int64_t workspace_bytes, int tile, void* stream) {
+  const char* who = "dmuon_muon_step_group";
+  if (batch == 0) return 0;
+  if (!buf_ptrs || !w_ptrs) return fail("%s: buf_ptrs and w_ptrs must be non-NULL", who);
+  // host scalars in double, rounded once to fp32, as torch does with Python-float arguments
+  const double scale = 0.2 * sqrt((double)(rows > cols ? rows : cols));
+  const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
+  const float lrs = (float)(lr * scale);
+  return run_group(g_ptrs, g_dtype, buf_ptrs, w_ptrs, w_dtype, nullptr, 0, rows, cols, batch,
+                   (float)mu, nesterov, first_step, decay, lrs, coeffs, T, eps, workspace,
+                   workspace_bytes, tile, static_cast<hipStream_t>(stream), who);
+}
+
+int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,
+                              int out_dtype, int rows, int cols, int batch, const float* coeffs,
+                              int T, float eps, void* workspace, int64_t workspace_bytes, int tile,
+                              void* stream) {
+  const char* who = "dmuon_newton_schulz_group";
+  if (batch == 0) return 0;
+  if (!out_ptrs) return fail("%s: out_ptrs must be non-NULL", who);
+  return run_group(g_ptrs, g_dtype, nullptr, nullptr, 0, out_ptrs, out_dtype, rows, cols, batch,
+                   0.f, 0, 1, 1.f, 0.f, coeffs, T, eps, workspace, workspace_bytes, tile,
+                   static_cast<hipStream_t>(stream), who);
+}
+
+}  // extern "C"

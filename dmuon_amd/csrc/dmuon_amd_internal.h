@@ -1,0 +1,63 @@
+// Internal declarations shared by the HIP translation units of libdmuon_amd.
+// Not part of the public C-ABI (that is include/dmuon_amd.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dmuon {
+
+// dtype codes used across the C-ABI (mirrors DMUON_DTYPE_* in dmuon_amd.h).
+enum DType : int { DT_F32 = 0, DT_BF16 = 1 };
+
+// Epilogue of the NT-form MFMA product  acc[i][j] = sum_k A[i][k] * B[j][k].
+//   EPI_SYM   D = s*acc + beta*C + diag*I          (symmetric result, upper tiles + mirror)
+//   EPI_NS    D = s*(acc + beta*C), also D^T        (Newton-Schulz X <- a*X + B*X step)
+//   EPI_FINAL U = s*(acc + beta*C) -> out[] and/or W <- W*decay - lrs*U, original orientation
+enum EpiMode : int { EPI_SYM = 0, EPI_NS = 1, EPI_FINAL = 2 };
+
+struct NtArgs {
+  const uint16_t* A; long long lda, sA;   // bf16 [L][M][K], row stride lda, batch stride sA
+  const uint16_t* B; long long ldb, sB;   // bf16 [L][N][K]
+  int M, N, K, L;                         // multiples of the tile sizes (host pads)
+  int mt, nt, tiles_per_mat, tri;         // tile grid; tri: upper-triangle tiles of an MxM result
+  int mode;
+  float alpha, beta, diag;
+  const float* alpha_dev;                 // optional per-matrix multiplier of alpha
+  const uint16_t* C; long long ldc, sC;   // optional bf16 [L][M][N] addend
+  uint16_t* D; long long ldd, sD;         // bf16 [L][M][N]
+  uint16_t* DT; long long lddt, sDT;      // bf16 [L][N][M] (EPI_NS, optional)
+  void* const* out_ptrs; int out_dtype;   // EPI_FINAL: per-matrix U outputs (original shape)
+  void* const* w_ptrs; int w_dtype;       // EPI_FINAL: per-matrix weights updated in place
+  float decay, lrs;                       // W <- round(W*decay) - lrs*U   (decay==1: no decay rounding)
+  int m_real, n_real, transposed;         // true NS dims; transposed: original = X^T (n_real x m_real)
+};
+
+// Launches the NT MFMA kernel; picks the tile configuration from args (tile = 256 or 128).
+hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream);
+
+struct PreArgs {
+  void* const* g_ptrs; int g_dtype;       // per-matrix gradient (rows x cols, row-major)
+  float* const* buf_ptrs;                 // per-matrix fp32 momentum buffer (rows x cols)
+  uint16_t* Y; long long ldy, sY;         // bf16 ns_in in the gradient's layout, padded [L][Rp][Cp]
+  uint16_t* YT; long long ldyt, sYT;      // bf16 ns_in transposed, padded [L][Cp][Rp]
+  float* partials;                        // [L][blocks_per_mat] sum of squares of ns_in
+  int rows, cols, Rp, Cp, L;
+  float mu; int first_step, nesterov;
+};
+hipError_t launch_pre(const PreArgs& a, hipStream_t stream);
+int pre_blocks_per_mat(int Rp, int Cp);
+
+// scale[l] = 1/(sqrt(sum partials[l]) + eps), scale_sq[l] = scale^2
+hipError_t launch_norm_finalize(const float* partials, int nparts, int L, float eps,
+                                float* scale, float* scale_sq, hipStream_t stream);
+
+struct UpdateArgs {
+  void* const* w_ptrs; int w_dtype;
+  const void* const* u_ptrs; int u_dtype;
+  long long numel; int L;
+  float decay, lrs;
+};
+hipError_t launch_update(const UpdateArgs& a, hipStream_t stream);
+
+}  // namespace dmuon

@@ -1,0 +1,208 @@
+// Bandwidth-bound kernels of the Muon step on gfx950.
+//
+//  pre      buf <- mu*buf + g (first step: buf <- g); ns_in = g + mu*buf (Nesterov) or buf;
+//           writes bf16(ns_in) twice -- in the gradient's own layout and transposed (LDS-tiled
+//           64x64 transpose) -- into zero-padded NS operands, plus per-block partial sums of
+//           ns_in^2 for the Frobenius norm. One pass: 2 (g) + 4 + 4 (buf) + 2 + 2 (copies) B/elt.
+//  finalize scale = 1/(||ns_in||_F + eps) per matrix, fixed-order (deterministic) reduction.
+//  update   W <- W*(1 - lr*wd) - lr*scale*U   for callers holding a materialised U.
+#include "dmuon_amd_internal.h"
+
+namespace dmuon {
+namespace {
+
+constexpr int kTile = 64;
+constexpr int kPad = 8;  // u16 of padding per LDS row (keeps 16-byte alignment)
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+__device__ __forceinline__ float bf2f(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ float load_any(const void* p, int dtype, long long idx) {
+  return dtype == DT_F32 ? static_cast<const float*>(p)[idx]
+                         : bf2f(static_cast<const uint16_t*>(p)[idx]);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t tileT[kTile][kTile + kPad];
+  __shared__ float red[4];
+
+  const int l = blockIdx.z;
+  const int r0 = blockIdx.y * kTile, c0 = blockIdx.x * kTile;
+  const int tid = threadIdx.x;
+  const int tc = tid & 15, tr = tid >> 4;
+
+  const void* g = a.g_ptrs[l];
+  float* buf = a.buf_ptrs ? a.buf_ptrs[l] : nullptr;  // null: plain NS input, no momentum
+  uint16_t* Y = a.Y + (long long)l * a.sY;
+  uint16_t* YT = a.YT + (long long)l * a.sYT;
+  const float mu = a.mu;
+  const bool vec = (a.cols & 3) == 0;
+
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rl = tr + 16 * q;
+    const int row = r0 + rl;
+    const int col = c0 + 4 * tc;
+    float gv[4] = {0.f, 0.f, 0.f, 0.f}, bv[4] = {0.f, 0.f, 0.f, 0.f};
+    bool in[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) in[e] = (row < a.rows) && (col + e < a.cols);
+    const long long base = (long long)row * a.cols + col;
+    if (vec && in[3]) {
+      if (a.g_dtype == DT_F32) {
+        const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(g) + base);
+        gv[0] = t.x; gv[1] = t.y; gv[2] = t.z; gv[3] = t.w;
+      } else {
+        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(g) + base);
+        gv[0] = bf2f(t.x & 0xffff); gv[1] = bf2f(t.x >> 16);
+        gv[2] = bf2f(t.y & 0xffff); gv[3] = bf2f(t.y >> 16);
+      }
+      if (buf && !a.first_step) {
+        const float4 t = *reinterpret_cast<const float4*>(buf + base);
+        bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (in[e]) {
+          gv[e] = load_any(g, a.g_dtype, base + e);
+          if (buf && !a.first_step) bv[e] = buf[base + e];
+        }
+      }
+    }
+    float nb[4], ns[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // buf.mul_(mu).add_(g): two roundings, as the reference does them
+      if (buf) {
+        nb[e] = a.first_step ? gv[e] : __fadd_rn(__fmul_rn(bv[e], mu), gv[e]);
+        ns[e] = a.nesterov ? __fadd_rn(gv[e], __fmul_rn(mu, nb[e])) : nb[e];
+      } else {
+        nb[e] = gv[e];
+        ns[e] = gv[e];
+      }
+      if (!in[e]) ns[e] = 0.f;
+      ss += ns[e] * ns[e];
+    }
+    if (buf) {
+      if (vec && in[3]) {
+        *reinterpret_cast<float4*>(buf + base) = make_float4(nb[0], nb[1], nb[2], nb[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (in[e]) buf[base + e] = nb[e];
+      }
+    }
+    uint16_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = f2bf(ns[e]);
+    if (row < a.Rp) {
+      uint2 p;
+      p.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+      p.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+      *reinterpret_cast<uint2*>(Y + (long long)row * a.ldy + col) = p;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tileT[4 * tc + e][rl] = o[e];
+  }
+  __syncthreads();
+  {
+    // transposed write: row cl of YT gets 64 consecutive source rows (128 B)
+    const int cl = tid >> 2, seg = tid & 3;
+    const int col = c0 + cl;
+    if (col < a.Cp) {
+      const uint4* src = reinterpret_cast<const uint4*>(&tileT[cl][16 * seg]);
+      uint4* dst = reinterpret_cast<uint4*>(YT + (long long)col * a.ldyt + r0 + 16 * seg);
+      dst[0] = src[0];
+      dst[1] = src[1];
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  if (tid == 0) {
+    const int nparts = gridDim.x * gridDim.y;
+    a.partials[(long long)l * nparts + blockIdx.y * gridDim.x + blockIdx.x] =
+        (red[0] + red[1]) + (red[2] + red[3]);
+  }
+}
+
+__global__ __launch_bounds__(256) void norm_finalize_kernel(const float* partials, int nparts,
+                                                            float eps, float* scale,
+                                                            float* scale_sq) {
+  __shared__ double red[256];
+  const int l = blockIdx.x;
+  double s = 0.0;
+  for (int p = threadIdx.x; p < nparts; p += 256) s += (double)partials[(long long)l * nparts + p];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float nrm = (float)sqrt(red[0]);
+    const float sc = 1.0f / (nrm + eps);
+    scale[l] = sc;
+    scale_sq[l] = sc * sc;
+  }
+}
+
+__global__ __launch_bounds__(256) void muon_update_kernel(const UpdateArgs a) {
+  const int l = blockIdx.y;
+  void* w = a.w_ptrs[l];
+  const void* u = a.u_ptrs[l];
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < a.numel; i += stride) {
+    const float uv = load_any(u, a.u_dtype, i);
+    if (a.w_dtype == DT_F32) {
+      float* wp = static_cast<float*>(w) + i;
+      float wv = *wp;
+      if (a.decay != 1.f) wv = __fmul_rn(wv, a.decay);
+      *wp = __fadd_rn(wv, -a.lrs * uv);
+    } else {
+      uint16_t* wp = static_cast<uint16_t*>(w) + i;
+      float wv = bf2f(*wp);
+      if (a.decay != 1.f) wv = bf2f(f2bf(__fmul_rn(wv, a.decay)));
+      *wp = f2bf(__fadd_rn(wv, -a.lrs * uv));
+    }
+  }
+}
+
+}  // namespace
+
+int pre_blocks_per_mat(int Rp, int Cp) { return (Rp / kTile) * (Cp / kTile); }
+
+hipError_t launch_pre(const PreArgs& a, hipStream_t stream) {
+  dim3 grid(a.Cp / kTile, a.Rp / kTile, a.L), block(256);
+  hipLaunchKernelGGL(muon_pre_kernel, grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_norm_finalize(const float* partials, int nparts, int L, float eps, float* scale,
+                                float* scale_sq, hipStream_t stream) {
+  hipLaunchKernelGGL(norm_finalize_kernel, dim3(L), dim3(256), 0, stream, partials, nparts, eps,
+                     scale, scale_sq);
+  return hipGetLastError();
+}
+
+hipError_t launch_update(const UpdateArgs& a, hipStream_t stream) {
+  long long blocks = (a.numel + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(muon_update_kernel, dim3((unsigned)blocks, a.L), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace dmuon

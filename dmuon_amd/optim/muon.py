@@ -1,0 +1,335 @@
+"""``Muon`` optimizer, world_size=1 owner path on MI355X (reference: ``dmuon/optim/muon.py``).
+
+Constructor, ``step()`` and ``zero_grad()`` keep the reference's signature and error behaviour
+(``muon.py:127-314``, ``:1354-1444``, ``:1918``). The per-parameter Muon math of
+``_step_muon_params`` (``muon.py:1582-1747``)::
+
+    buf = mu*buf + g            (first step: buf = g)             muon.py:1683-1691
+    ns_in = g + mu*buf          (Nesterov; else buf)               muon.py:1693-1694
+    U = NS(ns_in)                                                   muon.py:1704
+    W *= 1 - lr*wd  (wd > 0);  W += -lr*0.2*sqrt(max(m, n)) * U     muon.py:1728-1740
+
+runs on the GPU as one C-ABI call per bucket of same-shape parameters
+(``dmuon_muon_step_group``): a fused momentum/Nesterov/staging kernel, a norm finalise, and
+per NS step three bf16 MFMA kernels (SYRK, SYRK-polynomial, GEMM), the last GEMM applying the
+weight update in its epilogue. The momentum buffer is fp32 and lives in
+``optimizer.state[id(dp)]["momentum_buffer"]`` shaped ``(rows, cols)`` like the reference's.
+
+Parameters that are not dedicated (and 1-D dedicated ones) get the reference's decoupled AdamW
+(``muon.py:1857-1916``) through ``torch._foreach`` ops.
+"""
+from __future__ import annotations
+
+import logging
+import math
+from collections import OrderedDict
+from typing import Optional, Union
+
+import torch
+from torch import Tensor, nn
+
+from dmuon_amd import _C
+from dmuon_amd.api import iter_dedicated_states
+from dmuon_amd.optim.newton_schulz import NewtonSchulz, _coeff_array, _float_dtype_code
+
+logger = logging.getLogger(__name__)
+
+_MUON_KEYS = ("lr", "momentum", "weight_decay")
+
+
+def _pinned_ptrs(ptrs: list[int], device: torch.device) -> Tensor:
+    host = torch.tensor(ptrs, dtype=torch.int64, pin_memory=True)
+    return host.to(device, non_blocking=True)
+
+
+class Muon(torch.optim.Optimizer):
+    """Muon for dedicated matrix parameters + AdamW for the rest (``muon.py:127-153``).
+
+    Extra keyword arguments of the reference that concern multi-rank scheduling
+    (``replicate_async``, ``group_prepare_ahead``, ``tp_distributed_gram*``,
+    ``post_step_prefetch_*``, ``forward_prefetch_depth``, ...) are accepted and have no effect
+    at world_size=1. ``workspace_limit_bytes`` bounds the NS scratch (a bucket of same-shape
+    matrices is processed in chunks that fit).
+    """
+
+    def __init__(
+        self,
+        model: nn.Module,
+        lr: float = 0.02,
+        momentum: float = 0.95,
+        weight_decay: float = 0.0,
+        ns_steps: int = 5,
+        adamw_lr: float = 1e-3,
+        adamw_betas: tuple[float, float] = (0.9, 0.999),
+        adamw_weight_decay: float = 0.01,
+        adamw_eps: float = 1e-8,
+        param_groups: Optional[list[dict]] = None,
+        ns_backend: Union[str, NewtonSchulz] = "gram",
+        nesterov: bool = True,
+        record_step_profile: bool = False,
+        workspace_limit_bytes: int = 8 << 30,
+        ns_eps: float = 1e-7,
+        **kwargs,
+    ):
+        if isinstance(ns_backend, str):
+            ns_backend = NewtonSchulz(backend=ns_backend)
+        if not isinstance(ns_backend, NewtonSchulz):
+            raise TypeError(
+                f"ns_backend must be 'gram', 'direct', or a NewtonSchulz instance, "
+                f"got {type(ns_backend).__name__}")
+        comm_ctx = getattr(model, "_dedicated_comm_ctx", None)
+        if comm_ctx is None:
+            raise ValueError(
+                "Model has no _dedicated_comm_ctx. Call dmuon.dedicate_params() first.")
+        self.model = model
+        self._comm_ctx = comm_ctx
+        self._ns = ns_backend
+        self._ns_steps = ns_steps
+        self._nesterov = bool(nesterov)
+        self._ns_eps = float(ns_eps)
+        self._record_step_profile = bool(record_step_profile)
+        self._workspace_limit = int(workspace_limit_bytes)
+        self._workspace: Optional[Tensor] = None
+        self._last_step_profile: dict = {}
+        self._optimizer_step_index = 0
+
+        self._all_dedicated_params = []
+        for st in iter_dedicated_states(model):
+            for dp in st.group.params:
+                self._all_dedicated_params.append(dp)
+        self._dedicated_params = [dp for dp in self._all_dedicated_params if dp.is_owner]
+
+        # Non-dedicated params: FSDP2-managed (if any) or registered through replicate().
+        self._fsdp_params: list[nn.Parameter] = []
+        fsdp_hit = False
+        for module in model.modules():
+            fsdp_state = getattr(module, "_get_fsdp_state", lambda: None)()
+            if fsdp_state is not None and getattr(fsdp_state, "_fsdp_param_group", None) is not None:
+                for fp in fsdp_state._fsdp_param_group.fsdp_params:
+                    self._fsdp_params.append(fp.sharded_param)
+                fsdp_hit = True
+        rep = getattr(model, "_replicated_group", None)
+        if rep is not None:
+            self._fsdp_params.extend(rep.params)
+        non_dedicated_exists = any(
+            not hasattr(p, "_dedicated_owner_rank") and p.requires_grad for p in model.parameters())
+        if self._all_dedicated_params and non_dedicated_exists and not (fsdp_hit or rep is not None):
+            raise RuntimeError(
+                "dmuon.Muon: model has non-dedicated parameters but neither "
+                "fully_shard nor dmuon.replicate was called. Those parameters "
+                "would not be synced across ranks nor updated. Call one of "
+                "fully_shard() or dmuon.replicate(model, mesh=...) before "
+                "constructing Muon.")
+
+        self._dp_by_param = {id(dp.param): dp for dp in self._dedicated_params}
+        groups = self._build_groups(param_groups, lr, momentum, weight_decay, adamw_lr,
+                                    adamw_betas, adamw_weight_decay, adamw_eps)
+        defaults = dict(lr=lr, momentum=momentum, weight_decay=weight_decay)
+        super().__init__(groups, defaults)
+
+    # ------------------------------------------------------------------ groups
+    def _build_groups(self, param_groups, lr, momentum, wd, adamw_lr, betas, adamw_wd, eps):
+        """Lowers user groups into Muon (2-D+ dedicated) and AdamW subgroups."""
+        muon_ids = {id(dp.param) for dp in self._dedicated_params if dp.param.dim() >= 2}
+        adamw_pool = [dp.param for dp in self._dedicated_params if dp.param.dim() < 2]
+        adamw_pool += self._fsdp_params
+        user = param_groups if param_groups is not None else [
+            {"params": [dp.param for dp in self._dedicated_params] + self._fsdp_params}]
+        out = []
+        seen: set[int] = set()
+        for ug in user:
+            params = list(ug["params"])
+            muon_p = [p for p in params if id(p) in muon_ids and id(p) not in seen]
+            adam_p = [p for p in params if id(p) not in muon_ids and id(p) not in seen
+                      and p.requires_grad]
+            seen.update(id(p) for p in params)
+            if muon_p:
+                out.append({"params": muon_p, "use_muon": True,
+                            "lr": ug.get("lr", lr), "momentum": ug.get("momentum", momentum),
+                            "weight_decay": ug.get("weight_decay", wd)})
+            if adam_p:
+                out.append({"params": adam_p, "use_muon": False,
+                            "lr": ug.get("adamw_lr", adamw_lr),
+                            "betas": tuple(ug.get("adamw_betas", betas)),
+                            "weight_decay": ug.get("adamw_weight_decay", adamw_wd),
+                            "eps": ug.get("adamw_eps", eps)})
+        missing = [p for p in adamw_pool if id(p) not in seen and p.requires_grad]
+        if missing:
+            out.append({"params": missing, "use_muon": False, "lr": adamw_lr,
+                        "betas": tuple(betas), "weight_decay": adamw_wd, "eps": eps})
+        if not out:
+            out.append({"params": [], "use_muon": True, "lr": lr, "momentum": momentum,
+                        "weight_decay": wd})
+        return out
+
+    # ------------------------------------------------------------------ step
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        ev = None
+        if self._record_step_profile:
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record()
+        count = numel = 0
+        for group in self.param_groups:
+            if group.get("use_muon", False):
+                c, n = self._step_muon_group(group)
+                count += c
+                numel += n
+        if ev is not None:
+            ev[1].record()
+        for group in self.param_groups:
+            if not group.get("use_muon", False):
+                self._step_adamw_group(group)
+        if ev is not None:
+            self._last_step_profile = {"_events": ev, "ns_matrix_count": count,
+                                       "ns_input_numel": numel}
+        self._optimizer_step_index += 1
+        return loss
+
+    def consume_last_step_profile(self) -> dict:
+        """``muon.py:1287-1309``: timings of the last step (synchronises on its events)."""
+        prof = dict(self._last_step_profile)
+        ev = prof.pop("_events", None)
+        if ev is not None:
+            ev[1].synchronize()
+            prof["ns_compute_ms"] = ev[0].elapsed_time(ev[1])
+        self._last_step_profile = {}
+        return prof
+
+    def _buckets(self, group) -> "OrderedDict[tuple, list]":
+        buckets: OrderedDict[tuple, list] = OrderedDict()
+        for p in group["params"]:
+            dp = self._dp_by_param.get(id(p))
+            if dp is None:
+                continue
+            g = dp.current_grad()
+            if g is None:
+                continue
+            st = self.state[id(dp)]
+            first = "momentum_buffer" not in st
+            rows = p.shape[0]
+            cols = p.numel() // rows
+            key = (rows, cols, g.dtype, p.dtype, g.device, first)
+            buckets.setdefault(key, []).append((dp, g))
+        return buckets
+
+    def _step_muon_group(self, group) -> tuple[int, int]:
+        lr, mu, wd = float(group["lr"]), float(group["momentum"]), float(group["weight_decay"])
+        coeffs, T = _coeff_array(self._ns.resolved_coefficients())
+        count = numel = 0
+        for (rows, cols, gdt, wdt, dev, first), items in self._buckets(group).items():
+            _require_cuda(dev)
+            L_all = len(items)
+            num_cus = torch.cuda.get_device_properties(dev).multi_processor_count
+            chunk = self._chunk_size(rows, cols, L_all, num_cus)
+            for s in range(0, L_all, chunk):
+                part = items[s:s + chunk]
+                L = len(part)
+                tile, _, _, nbytes = _C.plan(rows, cols, L, 0, num_cus)
+                ws = self._get_workspace(dev, nbytes)
+                gs, bufs, ws_ = [], [], []
+                for dp, g in part:
+                    st = self.state[id(dp)]
+                    if "momentum_buffer" not in st:
+                        st["momentum_buffer"] = torch.zeros((rows, cols), dtype=torch.float32,
+                                                            device=dev)
+                    if not g.is_contiguous():
+                        g = g.contiguous()
+                    W = dp._owned_data
+                    if not W.is_contiguous():
+                        raise RuntimeError(f"{dp.param_name}: Muon needs a contiguous weight")
+                    gs.append(g)
+                    bufs.append(st["momentum_buffer"])
+                    ws_.append(W)
+                ptrs = _pinned_ptrs([t.data_ptr() for t in gs] + [t.data_ptr() for t in bufs]
+                                    + [t.data_ptr() for t in ws_], dev)
+                base = ptrs.data_ptr()
+                stream = torch.cuda.current_stream(dev).cuda_stream
+                _C.call("dmuon_muon_step_group", base, _float_dtype_code(gs[0]), base + 8 * L,
+                        base + 16 * L, _float_dtype_code(ws_[0]), rows, cols, L, lr, mu, wd,
+                        int(self._nesterov), int(first), coeffs, T, self._ns_eps,
+                        ws.data_ptr(), ws.numel(), tile, stream)
+                count += L
+                numel += L * rows * cols
+            for dp, _ in items:
+                dp._reduced_grad = None
+        return count, numel
+
+    def _chunk_size(self, rows: int, cols: int, L: int, num_cus: int) -> int:
+        per = _C.plan(rows, cols, 1, 0, num_cus)[3]
+        chunk = max(1, min(L, self._workspace_limit // max(per, 1)))
+        while chunk > 1 and _C.plan(rows, cols, chunk, 0, num_cus)[3] > self._workspace_limit:
+            chunk -= 1
+        return chunk
+
+    def _get_workspace(self, device, nbytes: int) -> Tensor:
+        ws = self._workspace
+        if ws is None or ws.device != device or ws.numel() < nbytes:
+            self._workspace = None
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            self._workspace = ws
+        return ws
+
+    # ------------------------------------------------------------------ AdamW
+    def _step_adamw_group(self, group) -> None:
+        """Decoupled AdamW, bucketed by step (``muon.py:1857-1916``)."""
+        lr = group["lr"]
+        beta1, beta2 = group["betas"]
+        wd = group["weight_decay"]
+        eps = group["eps"]
+        buckets: dict = {}
+        for p in group["params"]:
+            dp = self._dp_by_param.get(id(p))
+            grad = dp.current_grad() if dp is not None else p.grad
+            if grad is None:
+                continue
+            key_obj = id(dp) if dp is not None else p
+            state = self.state[key_obj]
+            if len(state) == 0:
+                state["step"] = 0
+                state["exp_avg"] = torch.zeros_like(p)
+                state["exp_avg_sq"] = torch.zeros_like(p)
+            state["step"] += 1
+            key = (state["step"], p.dtype, p.device, grad.dtype)
+            buckets.setdefault(key, []).append((p.data, grad, state["exp_avg"], state["exp_avg_sq"]))
+            if dp is not None:
+                dp._reduced_grad = None
+        for (step, _pdt, _pdev, _gdt), items in buckets.items():
+            params = [it[0] for it in items]
+            grads = [it[1] for it in items]
+            exp_avgs = [it[2] for it in items]
+            exp_avg_sqs = [it[3] for it in items]
+            if wd > 0:
+                torch._foreach_mul_(params, 1.0 - lr * wd)
+            torch._foreach_mul_(exp_avgs, beta1)
+            torch._foreach_add_(exp_avgs, grads, alpha=1.0 - beta1)
+            torch._foreach_mul_(exp_avg_sqs, beta2)
+            torch._foreach_addcmul_(exp_avg_sqs, grads, grads, value=1.0 - beta2)
+            bc1 = 1.0 - beta1 ** step
+            bc2 = 1.0 - beta2 ** step
+            denom = torch._foreach_sqrt(exp_avg_sqs)
+            torch._foreach_div_(denom, bc2 ** 0.5)
+            torch._foreach_add_(denom, eps)
+            torch._foreach_addcdiv_(params, exp_avgs, denom, value=-(lr / bc1))
+
+    def zero_grad(self, set_to_none: bool = True):
+        for p in self.model.parameters():
+            if p.grad is None:
+                continue
+            if set_to_none:
+                p.grad = None
+            else:
+                p.grad.zero_()
+        for dp in self._all_dedicated_params:
+            dp._reduced_grad = None
+            dp._accumulated_grad = None
+
+
+def _require_cuda(dev: torch.device) -> None:
+    if dev.type != "cuda":
+        raise RuntimeError("dmuon_amd.Muon: dedicated parameters must live on the GPU "
+                           "(the Muon update runs only on the HIP kernels)")

@@ -1,0 +1,166 @@
+/*
+ * dmuon_amd.h -- C ABI of libdmuon_amd.so, the MI355X (gfx950) kernels behind the owner-rank
+ * Muon update of X-Square-Robot/dmuon.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer is a device pointer unless stated otherwise; outputs are caller-allocated
+ *     and written in place.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as void*; NULL is the
+ *     default stream). No entry point synchronises the host and none allocates device memory
+ *     (scratch is the caller's `workspace`).
+ *   - Return value: 0 on success, nonzero on a rejected argument or a failed launch; the text
+ *     of the last error on the calling thread is returned by dmuon_last_error().
+ *   - bf16 matrices are row-major with 16-byte aligned base pointers and leading dimensions
+ *     that are multiples of 8 elements. Batched operands are [batch][rows][ld] with a batch
+ *     stride in elements.
+ *   - Per-matrix user tensors (gradients, momentum buffers, weights, outputs) are passed as
+ *     DEVICE arrays of `batch` pointers, because they are separate allocations.
+ *
+ * Reference interfaces replaced (paths relative to the dmuon source tree):
+ *   dmuon_syrk_bf16          dmuon/optim/syrk_dispatch.py:582-651   syrk_or_cublas(A, D, B, C,
+ *                                                                   alpha, beta, diag_add)
+ *                            dmuon/kernels/syrk_sm80.py:465-569     syrk_sm80(...) kernel call
+ *   dmuon_ns_gemm_bf16       dmuon/optim/newton_schulz.py:268-270   X = a*X + B @ X
+ *   dmuon_ns_gemm_final_bf16 dmuon/optim/newton_schulz.py:270-273 + dmuon/optim/muon.py:1728-1740
+ *                                                                   last NS step fused with
+ *                                                                   W *= 1-lr*wd; W += -lr*s*U
+ *   dmuon_muon_pre           dmuon/optim/muon.py:1683-1694 + newton_schulz.py:257-266
+ *                                                                   momentum, Nesterov, float(),
+ *                                                                   orientation, cast, ||X||^2
+ *   dmuon_norm_finalize      dmuon/optim/newton_schulz.py:265       X / (X.norm() + eps)
+ *   dmuon_muon_update        dmuon/optim/muon.py:1728-1740          owned.mul_/add_ update
+ *   dmuon_muon_step_group    dmuon/optim/muon.py:1683-1740          one owner's per-param Muon
+ *                                                                   math for `batch` same-shape
+ *                                                                   params (direct NS, T steps)
+ *   dmuon_newton_schulz_group dmuon/optim/newton_schulz.py:225-273  direct_newton_schulz(G) for
+ *                                                                   `batch` same-shape matrices
+ */
+#ifndef DMUON_AMD_H_
+#define DMUON_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DMUON_DTYPE_F32 0
+#define DMUON_DTYPE_BF16 1
+
+/* Text of the last error raised on this thread ("" if none). */
+const char* dmuon_last_error(void);
+
+/* ABI version (major*100 + minor). */
+int dmuon_abi_version(void);
+
+/*
+ * Launch profiler (no reference counterpart; measurement support for the benchmark harness).
+ * While enabled, every kernel launched by dmuon_muon_step_group / dmuon_newton_schulz_group is
+ * bracketed by hipEvents on its stream. dmuon_profile_collect synchronises on those events and
+ * returns, per kernel class (0 pre, 1 norm-finalize, 2 SYRK X X^T, 3 SYRK-poly, 4 NS GEMM,
+ * 5 final GEMM + update), the summed milliseconds, launch counts, useful FLOPs and algorithmic
+ * bytes, then clears the records. n_classes must be >= 6. Not thread-safe.
+ */
+int dmuon_profile_enable(int on);
+int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* bytes,
+                          int n_classes);
+
+/*
+ * D[l] = alpha * s_l * A[l] @ B[l]^T + beta * C[l] + diag_add * I     for l < batch
+ * where s_l = alpha_dev[l] if alpha_dev != NULL else 1.
+ * A, B: [M][K]; C, D: [M][M]. B == NULL means B = A. The result must be symmetric (always true
+ * for B = A; the caller guarantees it when B != A, as syrk_or_cublas requires). Only the upper
+ * triangle of tiles is computed; the lower triangle is written as its mirror. C may be NULL
+ * (then beta is ignored) and may alias A, but D must not alias A, B or C.
+ * tile: 128 or 256 (output tile edge); M % tile == 0, K % 64 == 0.
+ */
+int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
+                    int64_t strideB, const void* C, int64_t ldc, int64_t strideC, void* D,
+                    int64_t ldd, int64_t strideD, int M, int K, int batch, float alpha, float beta,
+                    float diag_add, const float* alpha_dev, int tile, void* stream);
+
+/*
+ * One Newton-Schulz step X' = s_l * (P @ X + beta * X) for l < batch, given P ([M][M], the
+ * polynomial b*A + c*A@A of A = X X^T) and XT = X^T ([N][M]); s_l = alpha * alpha_dev[l] (or
+ * alpha). Writes X' into Xout ([M][N], may alias X) and X'^T into XTout ([N][M], must not
+ * alias XT). M % tile == 0, N % tile == 0.
+ */
+int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT, int64_t ldxt,
+                       int64_t strideXT, const void* X, int64_t ldx, int64_t strideX, void* Xout,
+                       int64_t ldxo, int64_t strideXo, void* XTout, int64_t ldxto,
+                       int64_t strideXTo, int M, int N, int batch, float alpha, float beta,
+                       const float* alpha_dev, int tile, void* stream);
+
+/*
+ * Last Newton-Schulz step fused with the Muon weight update. U = s_l*(P @ X + beta*X) is formed
+ * in fp32 for the m_real x n_real corner of the padded [M][N] problem and, in the original
+ * orientation (transposed != 0: the original matrix is U^T, n_real x m_real):
+ *   out_ptrs != NULL: out[l] <- U                      (dtype out_dtype)
+ *   w_ptrs   != NULL: W[l] <- round(W*decay) - lrs*U    (dtype w_dtype; decay == 1 skips the
+ *                                                       decay rounding)
+ */
+int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT,
+                             int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx,
+                             int64_t strideX, int M, int N, int batch, float alpha, float beta,
+                             const float* alpha_dev, int m_real, int n_real, int transposed,
+                             void* const* out_ptrs, int out_dtype, void* const* w_ptrs,
+                             int w_dtype, float decay, float lrs, int tile, void* stream);
+
+/* Number of partial sums per matrix that dmuon_muon_pre writes for a padded Rp x Cp matrix. */
+int dmuon_muon_pre_partials(int Rp, int Cp);
+
+/*
+ * Momentum + Nesterov + NS-input staging for `batch` rows x cols matrices:
+ *   buf <- g (first_step) | fp32(mu*buf) + g        (buf_ptrs may be NULL: ns_in = g)
+ *   ns_in = g + mu*buf (nesterov) | buf
+ *   Y[l]  <- bf16(ns_in)    [Rp][ldy]  zero outside rows x cols
+ *   YT[l] <- bf16(ns_in)^T  [Cp][ldyt] zero outside cols x rows
+ *   partials[l][p] <- partial sums of ns_in^2 (fp32), p < dmuon_muon_pre_partials(Rp, Cp)
+ * g dtype: g_dtype; buf: fp32. Rp, Cp: multiples of 64, Rp >= rows, Cp >= cols.
+ */
+int dmuon_muon_pre(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* Y, int64_t ldy,
+                   int64_t strideY, void* YT, int64_t ldyt, int64_t strideYT, float* partials,
+                   int rows, int cols, int Rp, int Cp, int batch, float mu, int first_step,
+                   int nesterov, void* stream);
+
+/* scale[l] = 1 / (sqrt(sum_p partials[l][p]) + eps); scale_sq[l] = scale[l]^2. Deterministic. */
+int dmuon_norm_finalize(const float* partials, int nparts, int batch, float eps, float* scale,
+                        float* scale_sq, void* stream);
+
+/* W[l] <- round(W[l]*decay) - lrs*U[l] elementwise over numel elements (decay == 1: no decay). */
+int dmuon_muon_update(void* const* w_ptrs, int w_dtype, const void* const* u_ptrs, int u_dtype,
+                      int64_t numel, int batch, float decay, float lrs, void* stream);
+
+/*
+ * Planning for a group of `batch` same-shape rows x cols matrices: NS dims m = min, n = max,
+ * chosen output tile (tile_req 0 = automatic, else 128 or 256), padded m_pad / n_pad and the
+ * workspace bytes dmuon_muon_step_group / dmuon_newton_schulz_group need. Host-only.
+ */
+int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, int* m_pad,
+                  int* n_pad, int64_t* workspace_bytes);
+
+/*
+ * Full Muon update for `batch` same-shape rows x cols params (one owner's group):
+ *   momentum (+Nesterov), normalise, T direct Newton-Schulz steps with per-step coefficients
+ *   coeffs[3*t .. 3*t+2] = (a, b, c) (HOST array), then
+ *   W <- round(W*(1 - lr*wd)) - lr*0.2*sqrt(max(rows, cols)) * U    (decay skipped if wd <= 0)
+ * Each NS step is SYRK (X X^T) -> SYRK-poly (b*A + c*A A^T) -> GEMM (a*X + P X) on bf16 MFMA.
+ * workspace: device memory of at least the planned bytes; its contents need no initialisation.
+ */
+int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
+                          void* const* w_ptrs, int w_dtype, int rows, int cols, int batch,
+                          double lr, double mu, double wd, int nesterov, int first_step,
+                          const float* coeffs, int T, float eps, void* workspace,
+                          int64_t workspace_bytes, int tile, void* stream);
+
+/* direct_newton_schulz for `batch` same-shape rows x cols matrices: out[l] <- NS(g[l]). */
+int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,
+                              int out_dtype, int rows, int cols, int batch, const float* coeffs,
+                              int T, float eps, void* workspace, int64_t workspace_bytes, int tile,
+                              void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DMUON_AMD_H_ */

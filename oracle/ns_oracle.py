@@ -1,0 +1,265 @@
+"""CPU oracle for the owner-rank Muon update -- TEST INFRASTRUCTURE, NOT PRODUCT CODE.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+this module, and only as the checker (or the timed CPU baseline); ``dmuon_amd`` never does.
+
+It restates, in numpy, the reference algorithm of X-Square-Robot/dmuon on this path:
+
+* ``direct_ns``       ``dmuon/optim/newton_schulz.py:257-273`` (``direct_newton_schulz``),
+                      with the reference's cast points: fp32 normalise, then every product and
+                      every elementwise op rounded to the compute dtype (fp16 in the reference;
+                      bf16/fp32/fp64 selectable), GEMMs accumulating in fp32 (fp64 for "fp64").
+* ``gram_ns``         ``newton_schulz.py:364-448``, the torch (non-SYRK) branch, restart
+                      schedule included; ``addmm`` rounds once per call.
+* ``closed_form_ns``  exact-arithmetic NS through an fp64 SVD: X0 = U S V^T gives
+                      U f(S) V^T with f = p_T o ... o p_1, p(s) = a s + b s^3 + c s^5.
+* ``syrk_emulated_ns`` the build's own bf16 SYRK-form pipeline (bf16 operands, fp32
+                      accumulation, normalisation folded into the first SYRK/GEMM), used to
+                      bound the bf16-vs-fp16 gap and as a tight check of the GPU kernels.
+* ``muon_step``       ``dmuon/optim/muon.py:1683-1740``: sum-form momentum
+                      (``buf.mul_(mu).add_(g)``, first step ``buf = g``), Nesterov
+                      ``g + mu*buf``, NS, ``W *= 1 - lr*wd`` when wd > 0, then
+                      ``W += -lr*0.2*sqrt(max(m, n)) * U.to(W.dtype)``.
+
+Pinning (tests/test_oracle.py): ``direct_ns``/``gram_ns`` in fp64 against ``closed_form_ns``;
+``closed_form_ns`` against scalar special cases (rank-1, scaled partial identity, zero) that
+reduce to the scalar polynomial; reference-test invariants (orthogonality, Gram-vs-direct,
+tall-vs-wide); ``muon_step`` against the closed-form momentum recursion and the config-1
+known answers; coefficient tables against the published Polar-Express numbers. Mutated copies
+of the iteration (sign flip, swapped coefficients, dropped a*X term, missing transpose) are
+shown to fail the closed-form check.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import numpy as np
+
+# Keller Jordan's constant quintic (benchmarks/bench_optimizer.py:47), 5 iterations
+KELLER = [(3.4445, -4.7750, 2.0315)] * 5
+# newton_schulz.py:45-51
+YOU = [
+    (4.0848, -6.8946, 2.9270),
+    (3.9505, -6.3029, 2.6377),
+    (3.7418, -5.5913, 2.3037),
+    (2.8769, -3.1427, 1.2046),
+    (2.8366, -3.0525, 1.2012),
+]
+# newton_schulz.py:53-71 (raw table, then a/1.05, b/1.05^3, c/1.05^5)
+_PE_RAW = [
+    (8.28721201814563, -23.595886519098837, 17.300387312530933),
+    (4.107059111542203, -2.9478499167379106, 0.5448431082926601),
+    (3.9486908534822946, -2.908902115962949, 0.5518191394370137),
+    (3.3184196573706015, -2.488488024314874, 0.51004894012372),
+    (2.300652019954817, -1.6689039845747493, 0.4188073119525673),
+]
+POLAR_EXPRESS = [(a / 1.05, b / 1.05 ** 3, c / 1.05 ** 5) for (a, b, c) in _PE_RAW]
+DEFAULT_RESTART = [2]  # newton_schulz.py:75
+
+
+# ------------------------------------------------------------------------------------------
+# rounding
+# ------------------------------------------------------------------------------------------
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even to bfloat16, returned as float32 (NaN stays NaN)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(x), x, out)
+
+
+def rnd(x: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "fp16":
+        return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+    if dtype == "bf16":
+        return round_bf16(np.asarray(x, dtype=np.float32))
+    if dtype == "fp32":
+        return np.asarray(x, dtype=np.float32)
+    if dtype == "fp64":
+        return np.asarray(x, dtype=np.float64)
+    raise ValueError(dtype)
+
+
+def _mm(a: np.ndarray, b: np.ndarray, dtype: str) -> np.ndarray:
+    """Product with fp32 accumulation (fp64 for the fp64 pipeline)."""
+    if dtype == "fp64":
+        return np.asarray(a, np.float64) @ np.asarray(b, np.float64)
+    return np.asarray(a, np.float32) @ np.asarray(b, np.float32)
+
+
+def _orient_normalise(G: np.ndarray, eps: float, dtype: str):
+    """newton_schulz.py:259-266: X = float(G); transpose if tall; X /= (||X|| + eps)."""
+    if dtype == "fp64":
+        X = np.asarray(G, dtype=np.float64)
+        t = X.shape[0] > X.shape[1]
+        if t:
+            X = X.T
+        X = X / (np.linalg.norm(X) + eps)
+        return np.ascontiguousarray(X), t
+    X = np.asarray(G, dtype=np.float32)
+    t = X.shape[0] > X.shape[1]
+    if t:
+        X = X.T
+    nrm = np.float32(np.sqrt(np.sum(X.astype(np.float64) ** 2)))
+    X = (X / (nrm + np.float32(eps))).astype(np.float32)
+    return np.ascontiguousarray(X), t
+
+
+# ------------------------------------------------------------------------------------------
+# Newton-Schulz
+# ------------------------------------------------------------------------------------------
+def direct_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS, eps: float = 1e-7,
+              dtype: str = "fp16") -> np.ndarray:
+    """newton_schulz.py:257-273; returns float32 (float64 for dtype='fp64')."""
+    X, t = _orient_normalise(G, eps, dtype)
+    X = rnd(X, dtype)
+    for a, b, c in coefficients:
+        A = rnd(_mm(X, X.T, dtype), dtype)                       # A = X @ X.T
+        AA = rnd(_mm(A, A, dtype), dtype)                        # A @ A
+        B = rnd(rnd(b * A, dtype) + rnd(c * AA, dtype), dtype)   # B = b*A + c*A@A
+        X = rnd(rnd(a * X, dtype) + rnd(_mm(B, X, dtype), dtype), dtype)  # X = a*X + B@X
+    if t:
+        X = X.T
+    return np.ascontiguousarray(X)
+
+
+def gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
+            restart_iterations: Optional[Sequence[int]] = None, eps: float = 1e-7,
+            dtype: str = "fp16") -> np.ndarray:
+    """newton_schulz.py:364-448, torch branch (addmm = one rounding of beta*C + alpha*A@B)."""
+    if restart_iterations is None:
+        restart_iterations = DEFAULT_RESTART
+    X, t = _orient_normalise(G, eps, dtype)
+    X = rnd(X, dtype)
+    m = X.shape[0]
+    eye = rnd(np.eye(m), dtype)
+
+    def addmm(C, A_, B_, alpha=1.0, beta=1.0):
+        return rnd(beta * np.asarray(C, np.float64 if dtype == "fp64" else np.float32)
+                   + alpha * _mm(A_, B_, dtype), dtype)
+
+    R = rnd(_mm(X, X.T, dtype), dtype)
+    Q = None
+    n_it = len(coefficients)
+    for i, (a, b, c) in enumerate(coefficients):
+        if i in restart_iterations and i != 0:
+            X = rnd(_mm(Q, X, dtype), dtype)
+            R = rnd(_mm(X, X.T, dtype), dtype)
+            Q = None
+        Z = addmm(R, R, R, alpha=c, beta=b)
+        if Q is None:
+            Q = rnd(Z + rnd(a * eye, dtype), dtype)
+        else:
+            Q = addmm(Q, Z, Q, beta=a)
+        if i < n_it - 1 and (i + 1) not in restart_iterations:
+            RZ = addmm(R, R, Z, beta=a)
+            R = addmm(RZ, Z, RZ, beta=a)
+    X = rnd(_mm(Q, X, dtype), dtype)
+    if t:
+        X = X.T
+    return np.ascontiguousarray(X)
+
+
+def poly_compose(s: np.ndarray, coefficients: Sequence) -> np.ndarray:
+    """f(s) = p_T(...p_1(s)) with p(s) = a s + b s^3 + c s^5, in fp64."""
+    s = np.asarray(s, dtype=np.float64)
+    for a, b, c in coefficients:
+        s2 = s * s
+        s = a * s + b * s * s2 + c * s * s2 * s2
+    return s
+
+
+def closed_form_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
+                   eps: float = 1e-7) -> np.ndarray:
+    """Exact-arithmetic NS output via fp64 SVD of the oriented, normalised input."""
+    X, t = _orient_normalise(G, eps, "fp64")
+    U, S, Vt = np.linalg.svd(X, full_matrices=False)
+    out = (U * poly_compose(S, coefficients)[None, :]) @ Vt
+    return out.T.copy() if t else out
+
+
+def syrk_emulated_ns(G: np.ndarray, coefficients: Sequence = KELLER, eps: float = 1e-7,
+                     op_dtype: str = "bf16") -> np.ndarray:
+    """The build's device pipeline (not the reference's): X~ = bf16(ns_in) un-normalised,
+    s = 1/(||ns_in|| + eps); A = bf16(s^2 X~X~^T); P = bf16(c A A^T + b A);
+    X' = bf16(s (P X~ + a X~)) (s only on the first step); last step returns fp32 U."""
+    X = np.asarray(G, dtype=np.float32)
+    t = X.shape[0] > X.shape[1]
+    if t:
+        X = X.T
+    nrm = np.float32(np.sqrt(np.sum(X.astype(np.float64) ** 2)))
+    s = np.float32(1.0) / (nrm + np.float32(eps))
+    Xq = rnd(X, op_dtype)
+    T = len(coefficients)
+    for it, (a, b, c) in enumerate(coefficients):
+        sa = np.float32(s * s) if it == 0 else np.float32(1.0)
+        A = rnd(sa * _mm(Xq, Xq.T, "fp32"), op_dtype)
+        P = rnd(np.float32(c) * _mm(A, A, "fp32") + np.float32(b) * A, op_dtype)
+        sg = s if it == 0 else np.float32(1.0)
+        Xn = sg * (_mm(P, Xq, "fp32") + np.float32(a) * Xq)
+        Xq = Xn.astype(np.float32) if it == T - 1 else rnd(Xn, op_dtype)
+    if t:
+        Xq = Xq.T
+    return np.ascontiguousarray(Xq)
+
+
+# ------------------------------------------------------------------------------------------
+# Muon per-parameter update
+# ------------------------------------------------------------------------------------------
+def momentum_nesterov(g: np.ndarray, buf: Optional[np.ndarray], mu: float, nesterov: bool = True):
+    """muon.py:1683-1694 in fp32 with the reference's two roundings per line."""
+    g = np.asarray(g, dtype=np.float32)
+    mu32 = np.float32(mu)
+    if buf is None:
+        nb = g.copy()
+    else:
+        nb = (np.asarray(buf, np.float32) * mu32).astype(np.float32) + g
+    nb = nb.astype(np.float32)
+    ns_in = (g + (mu32 * nb).astype(np.float32)).astype(np.float32) if nesterov else nb
+    return nb, ns_in
+
+
+def apply_update(W: np.ndarray, U: np.ndarray, lr: float, wd: float, w_dtype: str = "fp32"):
+    """muon.py:1728-1740: W *= 1 - lr*wd (wd > 0); W += -lr*0.2*sqrt(max(m, n)) * U."""
+    rows = W.shape[0]
+    cols = W.size // rows
+    scale = 0.2 * math.sqrt(max(rows, cols))
+    Wf = np.asarray(W, dtype=np.float32)
+    if wd > 0:
+        Wf = rnd(Wf * np.float32(1.0 - lr * wd), w_dtype)
+    Uw = rnd(U, w_dtype)
+    return rnd(Wf + np.float32(-lr * scale) * Uw, w_dtype)
+
+
+def muon_step(W, g, buf, lr=0.02, mu=0.95, wd=0.0, nesterov=True, coefficients=KELLER,
+              ns="direct", dtype="fp16", eps=1e-7, w_dtype="fp32"):
+    """One owner-side Muon step; returns (W_new, buf_new, U)."""
+    nb, ns_in = momentum_nesterov(g, buf, mu, nesterov)
+    rows = ns_in.shape[0]
+    x2 = ns_in.reshape(rows, -1)
+    if ns == "direct":
+        U = direct_ns(x2, coefficients, eps, dtype)
+    elif ns == "gram":
+        U = gram_ns(x2, coefficients, None, eps, dtype)
+    elif ns == "closed":
+        U = closed_form_ns(x2, coefficients, eps)
+    elif ns == "syrk_bf16":
+        U = syrk_emulated_ns(x2, coefficients, eps, "bf16")
+    else:
+        raise ValueError(ns)
+    U = np.asarray(U, dtype=np.float32).reshape(np.shape(g))
+    return apply_update(W, U, lr, wd, w_dtype), nb, U
+
+
+def rel_fro(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    d = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / d) if d > 0 else float(np.linalg.norm(a))
+
+
+def ns_useful_flops(rows: int, cols: int, steps: int = 5) -> float:
+    m, n = min(rows, cols), max(rows, cols)
+    return float(steps) * (m * (m + 1) * n + m * (m + 1) * m + 2.0 * m * m * n)

@@ -1,0 +1,108 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/dmuon_amd.h
+declares, plans workspaces, and rejects bad arguments before any GPU work is enqueued."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from dmuon_amd import _C
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "dmuon_amd.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(dmuon_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == sorted(_C.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _C.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.dmuon_abi_version() >= 100
+    assert lib.dmuon_last_error() is not None
+
+
+@pytest.mark.parametrize("rows,cols,batch,tile,m_pad,n_pad", [
+    (4096, 4096, 1, 128, 4096, 4096),       # single square: 136 tiles of 256 would underfill
+    (4096, 4096, 64, 256, 4096, 4096),
+    (14336, 4096, 96, 256, 4096, 14336),    # tall: m = cols
+    (1408, 2048, 128, 128, 1408, 2048),     # 1408 is not a multiple of 256
+    (1000, 3000, 2, 128, 1024, 3072),       # padded
+])
+def test_plan(rows, cols, batch, tile, m_pad, n_pad):
+    t, mp, np_, ws = _C.plan(rows, cols, batch)
+    assert (t, mp, np_) == (tile, m_pad, n_pad)
+    x = mp * np_ * 2
+    a = mp * mp * 2
+    assert ws >= batch * (3 * x + 2 * a)
+
+
+def test_plan_rejects_bad_arguments():
+    with pytest.raises(RuntimeError, match="positive"):
+        _C.plan(0, 10, 1)
+    with pytest.raises(RuntimeError, match="tile"):
+        _C.plan(64, 64, 1, tile=96)
+
+
+def _err(rc):
+    assert rc != 0
+    return _C.lib().dmuon_last_error().decode()
+
+
+def test_syrk_validation_without_gpu():
+    lib = _C.lib()
+    p = ctypes.c_void_p(4096)
+    # M not a multiple of the tile
+    msg = _err(lib.dmuon_syrk_bf16(p, 256, 0, None, 0, 0, None, 0, 0, ctypes.c_void_p(1 << 20),
+                                   256, 0, 200, 256, 1, 1.0, 0.0, 0.0, None, 128, None))
+    assert "multiple of the tile" in msg
+    # bad tile
+    assert "tile" in _err(lib.dmuon_syrk_bf16(p, 256, 0, None, 0, 0, None, 0, 0, p, 256, 0, 256,
+                                              256, 1, 1.0, 0.0, 0.0, None, 64, None))
+    # misaligned pointer
+    assert "aligned" in _err(lib.dmuon_syrk_bf16(ctypes.c_void_p(4098), 256, 0, None, 0, 0, None,
+                                                 0, 0, ctypes.c_void_p(1 << 20), 256, 0, 256, 256,
+                                                 1, 1.0, 0.0, 0.0, None, 128, None))
+    # D aliasing A
+    assert "alias" in _err(lib.dmuon_syrk_bf16(p, 256, 0, None, 0, 0, None, 0, 0, p, 256, 0, 256,
+                                               256, 1, 1.0, 0.0, 0.0, None, 128, None))
+    # zero batch is a no-op success
+    assert lib.dmuon_syrk_bf16(p, 256, 0, None, 0, 0, None, 0, 0, p, 256, 0, 256, 256, 0, 1.0,
+                               0.0, 0.0, None, 128, None) == 0
+
+
+def test_group_validation_without_gpu():
+    lib = _C.lib()
+    coeff = (ctypes.c_float * 15)(*([3.4445, -4.7750, 2.0315] * 5))
+    p = ctypes.c_void_p(4096)
+    # workspace too small
+    msg = _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, 512, 1024, 1, 0.02, 0.95, 0.0, 1, 1,
+                                         coeff, 5, 1e-7, p, 16, 0, None))
+    assert "workspace" in msg
+    # unsupported dtype code
+    assert "dtype" in _err(lib.dmuon_muon_step_group(p, 7, p, p, 1, 512, 1024, 1, 0.02, 0.95, 0.0,
+                                                     1, 1, coeff, 5, 1e-7, p, 1 << 40, 0, None))
+    # no coefficients
+    assert "coefficient" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, 512, 1024, 1, 0.02,
+                                                           0.95, 0.0, 1, 1, coeff, 0, 1e-7, p,
+                                                           1 << 40, 0, None))
+    # NS group needs outputs
+    assert "out_ptrs" in _err(lib.dmuon_newton_schulz_group(p, 1, None, 1, 64, 64, 1, coeff, 5,
+                                                            1e-7, p, 1 << 30, 0, None))
+
+
+def test_pre_and_final_validation_without_gpu():
+    lib = _C.lib()
+    p = ctypes.c_void_p(4096)
+    assert "padded" in _err(lib.dmuon_muon_pre(p, 1, None, p, 128, 0, p, 128, 0, p, 100, 100, 96,
+                                               128, 1, 0.95, 1, 1, None))
+    assert "nothing to write" in _err(lib.dmuon_ns_gemm_final_bf16(
+        p, 256, 0, p, 256, 0, p, 256, 0, 256, 256, 1, 1.0, 1.0, None, 256, 256, 0, None, 0, None,
+        0, 1.0, 0.0, 128, None))
+    assert lib.dmuon_muon_pre_partials(128, 256) == 8

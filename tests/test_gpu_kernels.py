@@ -1,0 +1,195 @@
+"""GPU parity of the individual HIP kernels, called through the C ABI.
+
+Numerics follow the reference's SYRK tests (tests/unit/test_syrk.py:41-172,
+test_syrk_stress.py:28-295): products against a plain torch fp32 reference with a bf16-output
+tolerance, alpha/beta/C/diag epilogue, B != A symmetric products, exact mirror symmetry and
+10-run bit-exact determinism. The bandwidth kernels are bit-exact against torch fp32 ops.
+"""
+import ctypes
+
+import pytest
+import torch
+
+from dmuon_amd import _C
+
+pytestmark = pytest.mark.gpu
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def syrk(A, D, B=None, C=None, alpha=1.0, beta=0.0, diag=0.0, alpha_dev=None, tile=128):
+    L, M, K = A.shape
+    _C.call("dmuon_syrk_bf16", A.data_ptr(), K, M * K,
+            None if B is None else B.data_ptr(), K, M * K,
+            None if C is None else C.data_ptr(), M, M * M,
+            D.data_ptr(), M, M * M, M, K, L, alpha, beta, diag,
+            None if alpha_dev is None else alpha_dev.data_ptr(), tile, _stream())
+
+
+def _rand(shape, seed, dtype=torch.bfloat16, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(dtype)
+
+
+def _check_close(out, ref, rel=1e-2):
+    out, ref = out.float(), ref.float()
+    diff = (out - ref).abs().max().item()
+    lim = max(rel * ref.abs().max().item(), 1e-6)
+    assert diff <= lim, f"max|diff|={diff:.3e} > {lim:.3e}"
+    fro = ((out - ref).norm() / ref.norm()).item()
+    assert fro < 4e-3, f"rel Frobenius {fro:.3e}"
+
+
+@pytest.mark.parametrize("tile", [128, 256])
+@pytest.mark.parametrize("M,K,L", [(256, 64, 1), (512, 1024, 3), (768, 320, 2), (1024, 4096, 1)])
+def test_syrk_vs_torch(gpu, tile, M, K, L):
+    if M % tile:
+        pytest.skip("M not a multiple of the tile")
+    A = _rand((L, M, K), M + K).to(gpu)
+    D = torch.empty(L, M, M, dtype=torch.bfloat16, device=gpu)
+    syrk(A, D, tile=tile)
+    ref = torch.bmm(A.float(), A.float().transpose(1, 2).contiguous())
+    _check_close(D, ref)
+    # the mirror makes the result exactly symmetric
+    assert torch.equal(D, D.transpose(1, 2))
+
+
+def test_syrk_alpha_beta_c_diag(gpu):
+    M, K = 512, 256
+    A = _rand((2, M, K), 1).to(gpu)
+    S = _rand((2, M, M), 2).to(gpu)
+    C = ((S.float() + S.float().transpose(1, 2)) / 2).to(torch.bfloat16)
+    alpha_dev = torch.tensor([0.5, 2.0], device=gpu)
+    for diag in (0.0, 1.0, -3.5):
+        D = torch.empty(2, M, M, dtype=torch.bfloat16, device=gpu)
+        syrk(A, D, C=C, alpha=1.5, beta=-0.25, diag=diag, alpha_dev=alpha_dev)
+        ref = (1.5 * alpha_dev.view(2, 1, 1) * torch.bmm(A.float(), A.float().transpose(1, 2).contiguous())
+               - 0.25 * C.float() + diag * torch.eye(M, device=gpu))
+        _check_close(D, ref)
+    # diag_add = 0 is bit-identical to the plain epilogue
+    D0 = torch.empty_like(D)
+    D1 = torch.empty_like(D)
+    syrk(A, D0, C=C, alpha=1.5, beta=-0.25, diag=0.0)
+    syrk(A, D1, C=C, alpha=1.5, beta=-0.25)
+    assert torch.equal(D0, D1)
+
+
+def test_syrk_b_neq_a_symmetric_product(gpu):
+    # R and Z = R^2 are polynomials of one symmetric matrix, so R Z^T = R Z is symmetric
+    M = 512
+    X = _rand((1, M, 256), 3, std=0.05).to(gpu)
+    R = torch.bmm(X.float(), X.float().transpose(1, 2).contiguous()).to(torch.bfloat16)
+    Z = torch.bmm(R.float(), R.float()).to(torch.bfloat16)
+    D = torch.empty_like(R)
+    syrk(R, D, B=Z, C=R, alpha=1.0, beta=2.0)
+    ref = torch.bmm(R.float(), Z.float().transpose(1, 2).contiguous()) + 2.0 * R.float()
+    _check_close(D, ref, rel=2e-2)
+
+
+def test_syrk_determinism_10_runs(gpu):
+    A = _rand((2, 1024, 2048), 4).to(gpu)
+    outs = []
+    for _ in range(10):
+        D = torch.empty(2, 1024, 1024, dtype=torch.bfloat16, device=gpu)
+        syrk(A, D, tile=256)
+        outs.append(D)
+    for D in outs[1:]:
+        assert torch.equal(D, outs[0])
+
+
+def test_syrk_no_nan_across_scales(gpu):
+    for scale in (1e-4, 1e-2, 1.0, 10.0):
+        A = _rand((1, 256, 512), 5, std=scale).to(gpu)
+        D = torch.empty(1, 256, 256, dtype=torch.bfloat16, device=gpu)
+        syrk(A, D)
+        assert torch.isfinite(D).all()
+
+
+@pytest.mark.parametrize("tile", [128, 256])
+def test_ns_gemm_vs_torch(gpu, tile):
+    L, M, N = 2, 512, 1536
+    P = _rand((L, M, M), 6, std=0.05).to(gpu)
+    X = _rand((L, M, N), 7, std=0.05).to(gpu)
+    XT = X.transpose(1, 2).contiguous()
+    Xo = torch.empty_like(X)
+    XTo = torch.empty_like(XT)
+    scale = torch.tensor([0.7, 1.3], device=gpu)
+    _C.call("dmuon_ns_gemm_bf16", P.data_ptr(), M, M * M, XT.data_ptr(), M, M * N, X.data_ptr(),
+            N, M * N, Xo.data_ptr(), N, M * N, XTo.data_ptr(), M, M * N, M, N, L, 1.0, 3.4445,
+            scale.data_ptr(), tile, _stream())
+    ref = scale.view(L, 1, 1) * (torch.bmm(P.float(), X.float()) + 3.4445 * X.float())
+    _check_close(Xo, ref)
+    assert torch.equal(XTo, Xo.transpose(1, 2))
+    # in place (Xout aliases X) gives the same bits
+    X2 = X.clone()
+    XTo2 = torch.empty_like(XT)
+    _C.call("dmuon_ns_gemm_bf16", P.data_ptr(), M, M * M, XT.data_ptr(), M, M * N, X2.data_ptr(),
+            N, M * N, X2.data_ptr(), N, M * N, XTo2.data_ptr(), M, M * N, M, N, L, 1.0, 3.4445,
+            scale.data_ptr(), tile, _stream())
+    assert torch.equal(X2, Xo) and torch.equal(XTo2, XTo)
+
+
+def _ptrs(ts, dev):
+    return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
+
+
+@pytest.mark.parametrize("rows,cols,gdt", [(200, 300, torch.bfloat16), (300, 200, torch.float32),
+                                           (128, 128, torch.bfloat16), (1, 70, torch.float32)])
+@pytest.mark.parametrize("first", [1, 0])
+def test_pre_kernel_bit_exact(gpu, rows, cols, gdt, first):
+    L, mu = 3, 0.95
+    Rp, Cp = -(-rows // 64) * 64, -(-cols // 64) * 64
+    gs = [_rand((rows, cols), 10 + i, dtype=gdt, std=0.02).to(gpu) for i in range(L)]
+    bufs = [_rand((rows, cols), 20 + i, dtype=torch.float32, std=0.02).to(gpu) for i in range(L)]
+    buf0 = [b.clone() for b in bufs]
+    Y = torch.full((L, Rp, Cp), 7.0, dtype=torch.bfloat16, device=gpu)
+    YT = torch.full((L, Cp, Rp), 7.0, dtype=torch.bfloat16, device=gpu)
+    nparts = _C.lib().dmuon_muon_pre_partials(Rp, Cp)
+    parts = torch.empty(L, nparts, dtype=torch.float32, device=gpu)
+    gp, bp = _ptrs(gs, gpu), _ptrs(bufs, gpu)
+    _C.call("dmuon_muon_pre", gp.data_ptr(), _C.DTYPE_F32 if gdt == torch.float32 else _C.DTYPE_BF16,
+            bp.data_ptr(), Y.data_ptr(), Cp, Rp * Cp, YT.data_ptr(), Rp, Rp * Cp, parts.data_ptr(),
+            rows, cols, Rp, Cp, L, mu, first, 1, _stream())
+    for i in range(L):
+        g = gs[i].float()
+        nb = g.clone() if first else (buf0[i] * mu + g)
+        ns = g + nb * mu
+        assert torch.equal(bufs[i], nb)
+        exp = torch.zeros(Rp, Cp, dtype=torch.bfloat16, device=gpu)
+        exp[:rows, :cols] = ns.to(torch.bfloat16)
+        assert torch.equal(Y[i], exp)
+        assert torch.equal(YT[i], exp.t())
+        ss = parts[i].double().sum().item()
+        ref = (ns.double() ** 2).sum().item()
+        assert abs(ss - ref) <= 1e-5 * ref
+    # norm finalize
+    scale = torch.empty(L, device=gpu)
+    scale_sq = torch.empty(L, device=gpu)
+    _C.call("dmuon_norm_finalize", parts.data_ptr(), nparts, L, 1e-7, scale.data_ptr(),
+            scale_sq.data_ptr(), _stream())
+    for i in range(L):
+        g = gs[i].float()
+        nb = g.clone() if first else (buf0[i] * mu + g)
+        nrm = (g + nb * mu).double().norm().item()
+        assert scale[i].item() == pytest.approx(1.0 / (nrm + 1e-7), rel=1e-6)
+        assert scale_sq[i].item() == pytest.approx(scale[i].item() ** 2, rel=1e-6)
+
+
+@pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
+def test_update_kernel_bit_exact(gpu, wdt):
+    L, shape = 2, (300, 500)
+    Ws = [_rand(shape, 30 + i, dtype=wdt, std=0.02).to(gpu) for i in range(L)]
+    W0 = [w.clone() for w in Ws]
+    Us = [_rand(shape, 40 + i, dtype=torch.float32, std=0.05).to(gpu) for i in range(L)]
+    lr, wd = 0.02, 0.1
+    decay = 1.0 - lr * wd
+    lrs = lr * 0.2 * 500 ** 0.5
+    wp, up = _ptrs(Ws, gpu), _ptrs(Us, gpu)
+    _C.call("dmuon_muon_update", wp.data_ptr(), _C.DTYPE_F32 if wdt == torch.float32 else _C.DTYPE_BF16,
+            up.data_ptr(), _C.DTYPE_F32, 300 * 500, L, decay, lrs, _stream())
+    for i in range(L):
+        w1 = (W0[i].float() * decay).to(wdt).float()
+        exp = (w1 + (-lrs) * Us[i]).to(wdt)
+        assert torch.equal(Ws[i], exp)

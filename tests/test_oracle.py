@@ -1,0 +1,201 @@
+"""Pins the CPU oracle (oracle/ns_oracle.py) before it is trusted as the parity checker.
+
+Each check is independent of the oracle's own formula: an fp64 SVD closed form, scalar
+special cases, the reference's own test invariants (tests/unit/test_newton_schulz.py), the
+published coefficient values and hand-computed Muon known answers. Planted mistakes in a
+copy of the iteration must fail the closed-form check.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import ns_oracle as o
+
+SETS = {"keller": o.KELLER, "you": o.YOU, "pe": o.POLAR_EXPRESS}
+
+
+def _g(shape, seed=0, std=0.02):
+    return (np.random.default_rng(seed).standard_normal(shape) * std).astype(np.float32)
+
+
+@pytest.mark.parametrize("shape", [(16, 32), (32, 16), (24, 24), (64, 160)])
+@pytest.mark.parametrize("coeffs", list(SETS))
+def test_direct_fp64_matches_closed_form(shape, coeffs):
+    G = _g(shape, seed=sum(shape))
+    out = o.direct_ns(G, SETS[coeffs], dtype="fp64")
+    cf = o.closed_form_ns(G, SETS[coeffs])
+    assert out.shape == G.shape
+    assert o.rel_fro(out, cf) < 1e-10
+
+
+@pytest.mark.parametrize("restart", [[2], [], [1, 3]])
+@pytest.mark.parametrize("shape", [(16, 40), (40, 16)])
+def test_gram_fp64_matches_closed_form(shape, restart):
+    G = _g(shape, seed=7)
+    out = o.gram_ns(G, o.POLAR_EXPRESS, restart_iterations=restart, dtype="fp64")
+    assert o.rel_fro(out, o.closed_form_ns(G, o.POLAR_EXPRESS)) < 1e-9
+
+
+def test_closed_form_rank_one():
+    # G = u v^T normalises to u v^T/(|u||v|) with the single singular value 1 -> f(1) u v^T/(|u||v|)
+    rng = np.random.default_rng(3)
+    u, v = rng.standard_normal(12), rng.standard_normal(30)
+    G = np.outer(u, v)
+    f1 = 1.0
+    for a, b, c in o.KELLER:
+        f1 = a * f1 + b * f1 ** 3 + c * f1 ** 5
+    expect = f1 * np.outer(u, v) / (np.linalg.norm(u) * np.linalg.norm(v))
+    got = o.closed_form_ns(G, o.KELLER, eps=0.0)
+    np.testing.assert_allclose(got, expect, rtol=1e-10, atol=1e-12)
+
+
+def test_closed_form_scaled_partial_identity():
+    # G = s [I | 0] (m x n): all m singular values equal 1/sqrt(m) after normalisation
+    m, n = 8, 20
+    G = np.zeros((m, n))
+    G[:, :m] = 3.7 * np.eye(m)
+    x = 1.0 / math.sqrt(m)
+    for a, b, c in o.YOU:
+        x = a * x + b * x ** 3 + c * x ** 5
+    got = o.closed_form_ns(G, o.YOU, eps=0.0)
+    expect = np.zeros((m, n))
+    expect[:, :m] = x * np.eye(m)
+    np.testing.assert_allclose(got, expect, atol=1e-12)
+    # the direct iteration in fp64 gives the same
+    np.testing.assert_allclose(o.direct_ns(G, o.YOU, eps=0.0, dtype="fp64"), expect, atol=1e-12)
+
+
+def test_zero_input_gives_zero():
+    G = np.zeros((16, 48), np.float32)
+    for dt in ("fp16", "bf16", "fp32"):
+        assert np.all(o.direct_ns(G, o.KELLER, dtype=dt) == 0)
+    assert np.all(o.syrk_emulated_ns(G, o.KELLER) == 0)
+
+
+def test_transpose_equivariance():
+    G = _g((24, 56), seed=11)
+    for dt in ("fp16", "bf16"):
+        a = o.direct_ns(G, o.KELLER, dtype=dt)
+        b = o.direct_ns(G.T.copy(), o.KELLER, dtype=dt)
+        assert np.array_equal(a, b.T)
+
+
+# --- planted mistakes: a copy of the iteration with one defect must fail the pin -------------
+def _direct_mutant(G, coeffs, mutation):
+    X, t = o._orient_normalise(G, 1e-7, "fp64")
+    for a, b, c in coeffs:
+        if mutation == "swap_bc":
+            b, c = c, b
+        if mutation == "flip_b":
+            b = -b
+        A = X @ X.T
+        B = b * A + c * A @ A
+        X = (0.0 if mutation == "drop_aX" else a) * X + B @ X
+    if t and mutation != "no_transpose_back":
+        X = X.T
+    return X
+
+
+@pytest.mark.parametrize("mutation", ["swap_bc", "flip_b", "drop_aX", "no_transpose_back"])
+def test_planted_mistakes_fail_the_closed_form_pin(mutation):
+    G = _g((40, 16), seed=5)
+    cf = o.closed_form_ns(G, o.KELLER)
+    good = _direct_mutant(G, o.KELLER, None)
+    assert o.rel_fro(good, cf) < 1e-10
+    bad = _direct_mutant(G, o.KELLER, mutation)
+    if bad.shape != cf.shape:
+        return  # a missing transpose does not even give the right shape
+    assert o.rel_fro(bad, cf) > 1e-2
+
+
+# --- the reference's own test invariants (tests/unit/test_newton_schulz.py) -----------------
+def test_reference_invariants_fp16():
+    rng = np.random.default_rng(42)
+    for shape in [(128, 512), (64, 256)]:
+        G = rng.standard_normal(shape).astype(np.float32)
+        gram = o.gram_ns(G, o.POLAR_EXPRESS, dtype="fp16")
+        direct = o.direct_ns(G, o.POLAR_EXPRESS, dtype="fp16")
+        assert np.abs(gram - direct).max() < 0.1          # test_newton_schulz.py:40-65
+    G = rng.standard_normal((512, 128)).astype(np.float32)
+    tall = o.gram_ns(G, dtype="fp16")
+    wide = o.gram_ns(G.T.copy(), dtype="fp16")
+    assert np.abs(tall - wide.T).max() < 0.1              # :68-97
+    assert np.linalg.norm(tall) > 0.01
+    G = rng.standard_normal((128, 256)).astype(np.float32)
+    for coeffs in (o.YOU, o.POLAR_EXPRESS):               # :100-121, :239-270
+        U = o.gram_ns(G, coeffs, dtype="fp16")
+        assert not np.isnan(U).any()
+        assert np.abs(U @ U.T - np.eye(128)).max() < 0.15
+
+
+def test_polar_express_table_matches_published_values():
+    # numerical values of the scaled Polar-Express table (1.05 safety factor)
+    expect = [(7.8926, -20.3830, 13.5553), (3.9115, -2.5465, 0.4269),
+              (3.7607, -2.5128, 0.4324), (3.1604, -2.1496, 0.3996), (2.1911, -1.4417, 0.3281)]
+    for got, exp in zip(o.POLAR_EXPRESS, expect):
+        np.testing.assert_allclose(got, exp, atol=6e-5)
+
+
+def test_fp16_pipeline_is_close_to_exact():
+    G = _g((96, 256), seed=9)
+    cf = o.closed_form_ns(G, o.KELLER)
+    assert o.rel_fro(o.direct_ns(G, o.KELLER, dtype="fp32"), cf) < 1e-4
+    assert o.rel_fro(o.direct_ns(G, o.KELLER, dtype="fp16"), cf) < 1e-2
+    # the build's bf16 SYRK-form pipeline stays within the 2e-2 gate of the fp16 reference
+    assert o.rel_fro(o.syrk_emulated_ns(G, o.KELLER), o.direct_ns(G, o.KELLER, dtype="fp16")) < 2e-2
+
+
+# --- Muon per-parameter math ----------------------------------------------------------------
+def test_config1_known_answers():
+    rows = cols = 1024
+    lr, mu, wd = 0.02, 0.95, 0.1
+    scale = 0.2 * math.sqrt(max(rows, cols))
+    assert scale == pytest.approx(6.4, abs=0)
+    assert lr * scale == pytest.approx(0.128, rel=1e-15)
+    assert 1.0 - lr * wd == pytest.approx(0.998, rel=1e-15)
+    g = _g((64, 64), seed=1)
+    nb, ns_in = o.momentum_nesterov(g, None, mu)
+    assert np.array_equal(nb, g)                                   # first step: buf = g
+    assert np.array_equal(ns_in, (g + np.float32(mu) * g).astype(np.float32))
+    np.testing.assert_allclose(ns_in, 1.95 * g, rtol=1e-6)
+    # NS is scale invariant up to eps: NS(1.95 g) = NS(g)
+    np.testing.assert_allclose(o.closed_form_ns(ns_in, o.KELLER), o.closed_form_ns(g, o.KELLER),
+                               rtol=1e-4, atol=1e-7)
+
+
+def test_momentum_recursion_closed_form():
+    g1, g2, g3 = (_g((32, 48), seed=s) for s in (1, 2, 3))
+    mu = 0.95
+    b1, _ = o.momentum_nesterov(g1, None, mu)
+    b2, n2 = o.momentum_nesterov(g2, b1, mu)
+    b3, _ = o.momentum_nesterov(g3, b2, mu)
+    np.testing.assert_allclose(b2, mu * g1 + g2, rtol=1e-6, atol=2e-8)
+    np.testing.assert_allclose(b3, mu * mu * g1 + mu * g2 + g3, rtol=1e-6, atol=2e-8)
+    np.testing.assert_allclose(n2, g2 + mu * (mu * g1 + g2), rtol=1e-6, atol=2e-8)
+    _, nb = o.momentum_nesterov(g2, b1, mu, nesterov=False)
+    assert np.array_equal(nb, b2)
+
+
+def test_update_rule():
+    W = _g((32, 128), seed=4)
+    U = _g((32, 128), seed=5, std=0.1)
+    lr, wd = 0.02, 0.1
+    s = 0.2 * math.sqrt(128)
+    Wn = o.apply_update(W, U, lr, wd)
+    np.testing.assert_allclose(Wn, W * (1 - lr * wd) - lr * s * U, rtol=1e-6, atol=1e-8)
+    # wd == 0: no decay
+    np.testing.assert_allclose(o.apply_update(W, U, lr, 0.0), W - lr * s * U, rtol=1e-6, atol=1e-8)
+    # zero gradient: the step is pure decay (U = 0)
+    Wz, _, Uz = o.muon_step(W, np.zeros_like(W), None, lr=lr, wd=wd)
+    assert np.all(Uz == 0)
+    np.testing.assert_allclose(Wz, W * np.float32(1 - lr * wd), rtol=1e-7)
+
+
+def test_bf16_rounding_helper():
+    x = np.array([1.0, 1.00390625, 1.005859375, -3.0e-5, np.inf, 0.0], np.float32)
+    r = o.round_bf16(x)
+    assert r[0] == 1.0
+    assert r[1] == 1.0              # halfway 1 + 2^-8 rounds to even (1.0)
+    assert r[2] == np.float32(1.0078125)
+    assert np.isinf(r[4]) and r[5] == 0.0
