@@ -9,11 +9,17 @@
 //          writes X' and X'^T (EPI_NS), or on the last iteration applies the Muon
 //          weight update in the original orientation (EPI_FINAL)
 //
-// Tile machine: 256 threads = 4 waves (2x2); each wave owns a (BM/2)x(BN/2) sub-tile made of
-// 32x32 MFMA blocks (v_mfma_f32_32x32x16_bf16, fp32 accumulate). K is staged through LDS in
-// BK=64 slices, double-buffered, register-staged global loads, 16-byte chunks stored with an
-// XOR swizzle (chunk ^ (row & 7)) so both the stores and the fragment reads are bank-conflict
-// free without padding.
+// Tile machine: WM x WN waves; each wave owns a (BM/WM)x(BN/WN) sub-tile made of 32x32 MFMA
+// blocks (v_mfma_f32_32x32x16_bf16, fp32 accumulate). 256x256 tiles run 8 waves (two per SIMD,
+// so one wave's MFMAs cover the other's LDS and barrier waits); 128x128 tiles run 4 waves with
+// two blocks per CU. K is staged through LDS in
+// BK-wide slices by direct global->LDS DMA (global_load_lds_dwordx4: each wave instruction
+// fills 1 KiB of LDS, no staging registers) into an S-deep ring, so S-1 slices are in flight
+// while one is consumed; the wave waits only for the slice it needs (s_waitcnt vmcnt(N)) and
+// then meets the others at a plain s_barrier. 16-byte chunks sit in LDS under an XOR swizzle
+// (chunk ^ f(row)) chosen so that every 16-lane pass of a fragment read covers all 64 banks.
+#include <stdlib.h>
+
 #include "dmuon_amd_internal.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -24,8 +30,6 @@ typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 namespace dmuon {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kBK = 64;
 
 __device__ __forceinline__ uint16_t f2bf(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
@@ -43,26 +47,67 @@ __device__ __forceinline__ int xcd_remap(int b, int nb) {
   return base + idx;
 }
 
-template <int BM, int BN>
+template <int BM_, int BN_, int BK_, int S_, int WM_, int WN_>
 struct Tile {
-  static constexpr int TI = BM / 2 / 32;              // MFMA blocks along i per wave
-  static constexpr int TJ = BN / 2 / 32;              // MFMA blocks along j per wave
-  static constexpr int A_CH = BM * kBK / 8 / kThreads;  // 16-byte chunks per thread per slice
-  static constexpr int B_CH = BN * kBK / 8 / kThreads;
-  static constexpr int A_BYTES = BM * kBK * 2;
-  static constexpr int STAGE = (BM + BN) * kBK * 2;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, S = S_, WM = WM_, WN = WN_;
+  static constexpr int NW = WM * WN;              // waves per block
+  static constexpr int NT = 64 * NW;              // threads per block
+  static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave sub-tile
+  static constexpr int TI = WTM / 32;             // MFMA blocks along i per wave
+  static constexpr int TJ = WTN / 32;             // MFMA blocks along j per wave
+  static constexpr int ROWB = BK * 2;             // bytes of one tile row in LDS
+  static constexpr int CPR = BK / 8;              // 16-byte chunks per row
+  static constexpr int RPI = 1024 / ROWB;         // rows filled by one DMA wave instruction
+  static constexpr int A_INST = BM / RPI / NW;    // DMA instructions per wave per slice
+  static constexpr int B_INST = BN / RPI / NW;
+  static constexpr int LPT = A_INST + B_INST;     // outstanding loads a slice adds per wave
+  static constexpr int RPL = 256 / ROWB;          // rows per 256-byte LDS bank line (64 banks)
+  static constexpr int A_BYTES = BM * ROWB;
+  static constexpr int STAGE = (BM + BN) * ROWB;
+  static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0, "tile rows vs DMA rows");
+  static_assert((S - 2) * LPT <= 63, "vmcnt range");
+  // LDS slot of 16-byte chunk kc of row r. A ds_read_b128 serves 16 lanes (256 B, all 64
+  // banks) per pass; a fragment read has those 16 lanes on 16 consecutive rows at one chunk,
+  // so rows sharing a bank line (r % RPL) must take distinct slots along r / RPL.
+  static __device__ __forceinline__ int slot(int kc, int r) { return kc ^ ((r / RPL) & (CPR - 1)); }
 };
 
-template <int BM, int BN, int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+// s_waitcnt vmcnt(N) with expcnt/lgkmcnt left alone (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at
+// bits 15:14, expcnt bits 6:4 = 7, lgkmcnt bits 11:8 = 15).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Workgroup barrier without the memory fence of __syncthreads (which would also wait for every
+// in-flight LDS DMA); the empty asm statements keep the compiler from moving LDS accesses
+// across it.
+__device__ __forceinline__ void bare_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <class T>
+__device__ __forceinline__ void wait_slices(int ahead) {
+  // wait until at most `ahead` newer slices (T::LPT loads each) are still in flight
+  if constexpr (T::S >= 5) { if (ahead >= 3) { wait_vmcnt<3 * T::LPT>(); return; } }
+  if constexpr (T::S >= 4) { if (ahead >= 2) { wait_vmcnt<2 * T::LPT>(); return; } }
+  if constexpr (T::S >= 3) { if (ahead >= 1) { wait_vmcnt<1 * T::LPT>(); return; } }
+  wait_vmcnt<0>();
+}
+
+template <int BM, int BN, int BK, int S, int WM, int WN, int MODE>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void nt_mfma_kernel(const NtArgs a) {
-  using T = Tile<BM, BN>;
-  __shared__ __attribute__((aligned(16))) char smem[2 * T::STAGE];
+  using T = Tile<BM, BN, BK, S, WM, WN>;
+  __shared__ __attribute__((aligned(16))) char smem[S * T::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wi = wave >> 1, wj = wave & 1;
+  const int wi = wave / WN, wj = wave % WN;
 
   // ---- tile decode -------------------------------------------------------------------
   const int nblocks = gridDim.x;
@@ -90,14 +135,39 @@ void nt_mfma_kernel(const NtArgs a) {
   const uint16_t* __restrict__ Ab = a.A + (long long)l * a.sA + (long long)i0 * a.lda;
   const uint16_t* __restrict__ Bb = a.B + (long long)l * a.sB + (long long)j0 * a.ldb;
 
-  // ---- global -> register staging (per thread: fixed row/chunk, slices advance along K) ---
-  const int crow = tid >> 3, ckc = tid & 7;
-  const uint16_t* __restrict__ ga = Ab + (long long)crow * a.lda + ckc * 8;
-  const uint16_t* __restrict__ gb = Bb + (long long)crow * a.ldb + ckc * 8;
-  const long long astep = 32LL * a.lda, bstep = 32LL * a.ldb;  // 256 threads cover 32 rows
-  // rows crow + 32q share (row & 7), so the swizzled LDS offset is one per thread
-  const int soff = crow * 128 + ((ckc ^ (crow & 7)) << 4);
-  u32x4_t ra[T::A_CH], rb[T::B_CH];
+  // ---- global -> LDS DMA ring --------------------------------------------------------
+  // DMA instruction q of wave w fills rows R0 = (NW q + w) * RPI .. R0 + RPI - 1 of a tile: lane l
+  // writes LDS slot l % CPR of row R0 + l / CPR, so it fetches the global chunk that the
+  // swizzle places in that slot (slot() is an involution in its chunk argument).
+  const int lrow = lane / T::CPR, lsl = lane % T::CPR;
+  // element offsets from the tile's first row (fixed-size arrays: a template-dependent array
+  // bound here makes clang drop the kernel's host launch stub)
+  static_assert(T::A_INST <= 8 && T::B_INST <= 8, "DMA instructions per slice");
+  unsigned offa[8], offb[8];
+#pragma unroll
+  for (int q = 0; q < T::A_INST; ++q) {
+    const int r = (T::NW * q + wave) * T::RPI + lrow;
+    offa[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8);
+  }
+#pragma unroll
+  for (int q = 0; q < T::B_INST; ++q) {
+    const int r = (T::NW * q + wave) * T::RPI + lrow;
+    offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8);
+  }
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+#define DMUON_ISSUE(slice_)                                                                    \
+  do {                                                                                         \
+    const int sl_ = (slice_);                                                                  \
+    char* st_ = smem + (sl_ % S) * T::STAGE + wave * 1024;                                     \
+    const uint16_t* ak_ = Ab + sl_ * BK;                                                       \
+    const uint16_t* bk_ = Bb + sl_ * BK;                                                       \
+    _Pragma("unroll") for (int q = 0; q < T::A_INST; ++q)                                      \
+        __builtin_amdgcn_global_load_lds(ak_ + offa[q], (lds_ptr_t)(st_ + q * 1024 * T::NW), 16, 0, 0); \
+    _Pragma("unroll") for (int q = 0; q < T::B_INST; ++q)                                      \
+        __builtin_amdgcn_global_load_lds(bk_ + offb[q], (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * T::NW), \
+                                         16, 0, 0);                                            \
+  } while (0)
+
   f32x16_t acc[T::TI][T::TJ];
 #pragma unroll
   for (int x = 0; x < T::TI; ++x)
@@ -106,83 +176,98 @@ void nt_mfma_kernel(const NtArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.f;
 
-  const int KT = a.K / kBK;
-  {
-      const int k0_ = 0;
+  const int KT = a.K / BK;
 #pragma unroll
-      for (int q = 0; q < T::A_CH; ++q) ra[q] = *reinterpret_cast<const u32x4_t*>(ga + q * astep + k0_);
-#pragma unroll
-      for (int q = 0; q < T::B_CH; ++q) rb[q] = *reinterpret_cast<const u32x4_t*>(gb + q * bstep + k0_);
-    }
-  {
-      char* sa_ = smem + (0) * T::STAGE;
-#pragma unroll
-      for (int q = 0; q < T::A_CH; ++q) *reinterpret_cast<u32x4_t*>(sa_ + soff + q * 4096) = ra[q];
-#pragma unroll
-      for (int q = 0; q < T::B_CH; ++q)
-        *reinterpret_cast<u32x4_t*>(sa_ + T::A_BYTES + soff + q * 4096) = rb[q];
-    }
-  __syncthreads();
+  for (int s0 = 0; s0 < S - 1; ++s0)
+    if (s0 < KT) DMUON_ISSUE(s0);
 
-  const int arow0 = wi * (BM / 2) + (lane & 31);
-  const int brow0 = wj * (BN / 2) + (lane & 31);
+  const int arow0 = wi * T::WTM + (lane & 31);
+  const int brow0 = wj * T::WTN + (lane & 31);
   const int khalf = lane >> 5;
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const bool more = (kt + 1) < KT;
-    if (more) {
-      const int k0_ = (kt + 1) * kBK;
+  // Fragments of substep ks+1 are read from LDS while the MFMAs of substep ks run.
+  constexpr int KS = BK / 16;
+  auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8_t* af, bf16x8_t* bfr) {
+    const int kc = ks * 2 + khalf;
 #pragma unroll
-      for (int q = 0; q < T::A_CH; ++q) ra[q] = *reinterpret_cast<const u32x4_t*>(ga + q * astep + k0_);
-#pragma unroll
-      for (int q = 0; q < T::B_CH; ++q) rb[q] = *reinterpret_cast<const u32x4_t*>(gb + q * bstep + k0_);
+    for (int x = 0; x < T::TI; ++x) {
+      const int row = arow0 + x * 32;
+      af[x] = *reinterpret_cast<const bf16x8_t*>(sa + row * T::ROWB + (T::slot(kc, row) << 4));
     }
-    const char* sa = smem + (kt & 1) * T::STAGE;
+#pragma unroll
+    for (int y = 0; y < T::TJ; ++y) {
+      const int row = brow0 + y * 32;
+      bfr[y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
+    }
+  };
+  for (int kt = 0; kt < KT; ++kt) {
+    wait_slices<T>(min(S - 2, KT - 1 - kt));
+    bare_barrier();                       // slice kt landed for every wave; slot kt-1 is free
+    if (kt + S - 1 < KT) DMUON_ISSUE(kt + S - 1);
+    const char* sa = smem + (kt % S) * T::STAGE;
     const char* sb = sa + T::A_BYTES;
+    bf16x8_t af[2][T::TI], bfr[2][T::TJ];
+    load_frags(sa, sb, 0, af[0], bfr[0]);
 #pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int kc = ks * 2 + khalf;
-      bf16x8_t af[T::TI], bfr[T::TJ];
-#pragma unroll
-      for (int x = 0; x < T::TI; ++x) {
-        const int row = arow0 + x * 32;
-        af[x] = *reinterpret_cast<const bf16x8_t*>(sa + row * 128 + ((kc ^ (row & 7)) << 4));
-      }
-#pragma unroll
-      for (int y = 0; y < T::TJ; ++y) {
-        const int row = brow0 + y * 32;
-        bfr[y] = *reinterpret_cast<const bf16x8_t*>(sb + row * 128 + ((kc ^ (row & 7)) << 4));
-      }
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) load_frags(sa, sb, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
 #pragma unroll
       for (int x = 0; x < T::TI; ++x)
 #pragma unroll
         for (int y = 0; y < T::TJ; ++y)
           // MFMA rows <- j (B operand), MFMA cols <- i (A operand): each lane then holds
           // four consecutive j of one i, i.e. 8-byte row-major stores of D.
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[y], af[x], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][y], af[ks & 1][x],
+                                                              acc[x][y], 0, 0, 0);
     }
-    if (more) {
-      char* sa_ = smem + ((kt + 1) & 1) * T::STAGE;
+    // Scheduling shape of the slice: substep 0's fragment reads, then each later substep's
+    // reads interleaved one-for-one with the first MFMAs of the substep before it.
+    constexpr int NF = T::TI + T::TJ, NM = T::TI * T::TJ;
+    __builtin_amdgcn_sched_group_barrier(0x100, NF, 0);              // DS reads
 #pragma unroll
-      for (int q = 0; q < T::A_CH; ++q) *reinterpret_cast<u32x4_t*>(sa_ + soff + q * 4096) = ra[q];
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) {
 #pragma unroll
-      for (int q = 0; q < T::B_CH; ++q)
-        *reinterpret_cast<u32x4_t*>(sa_ + T::A_BYTES + soff + q * 4096) = rb[q];
+        for (int i = 0; i < NF; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);         // DS read
+        }
+        if constexpr (NM > NF) __builtin_amdgcn_sched_group_barrier(0x008, NM - NF, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+      }
     }
-    __syncthreads();
+  }
+#undef DMUON_ISSUE
+  wait_vmcnt<0>();
+  bare_barrier();
+
+  // The epilogue's addend C (X for the NS step, A for the polynomial) for the whole wave tile
+  // is requested at once, so its latency is paid once per tile: element (x, y, g) is 4 bf16 at
+  // row iw + 32x + li, columns jw + 32y + 8g + 4lh .. +3.
+  const int li = lane & 31, lh = lane >> 5;
+  const int iw = i0 + wi * T::WTM, jw = j0 + wj * T::WTN;
+  const uint16_t* Cb = a.C ? a.C + (long long)l * a.sC : nullptr;
+  u32x2_t cpre[T::TI][T::TJ * 4];
+  if (Cb) {
+    const unsigned lo = (unsigned)(li * a.ldc + 4 * lh);
+#pragma unroll
+    for (int x = 0; x < T::TI; ++x) {
+      const uint16_t* crow = Cb + (long long)(iw + 32 * x) * a.ldc + jw + lo;
+#pragma unroll
+      for (int q = 0; q < T::TJ * 4; ++q)
+        cpre[x][q] = *reinterpret_cast<const u32x2_t*>(crow + 32 * (q >> 2) + 8 * (q & 3));
+    }
   }
 
   // ---- epilogue -----------------------------------------------------------------------
   // element (x, y, g, e) of the wave tile, with li = lane & 31, lh = lane >> 5:
   //   i = iw + 32x + li,   j = jw + 32y + 8g + 4lh + e      (acc[x][y][4g + e])
   // Addresses split into a wave-uniform part (scalar registers) and one per-lane offset.
-  const int li = lane & 31, lh = lane >> 5;
-  const int iw = i0 + wi * (BM / 2), jw = j0 + wj * (BN / 2);
   float s = a.alpha;
   if (a.alpha_dev) s *= a.alpha_dev[l];
 
   if constexpr (MODE == EPI_SYM || MODE == EPI_NS) {
-    const uint16_t* Cb = a.C ? a.C + (long long)l * a.sC : nullptr;
     uint16_t* Db = a.D + (long long)l * a.sD;
     uint16_t* DTb = nullptr;
     long long ldt = 0;
@@ -192,20 +277,20 @@ void nt_mfma_kernel(const NtArgs a) {
       if (a.DT) { DTb = a.DT + (long long)l * a.sDT; ldt = a.lddt; }
     }
     const unsigned lo_d = (unsigned)(li * a.ldd + 4 * lh);
-    const unsigned lo_c = (unsigned)(li * a.ldc + 4 * lh);
     const unsigned lo_t = (unsigned)(4 * lh * ldt + li);
 #pragma unroll
     for (int x = 0; x < T::TI; ++x) {
       uint16_t* drow = Db + (long long)(iw + 32 * x) * a.ldd + jw;
-      const uint16_t* crow = Cb ? Cb + (long long)(iw + 32 * x) * a.ldc + jw : nullptr;
+      // all addend loads of this 32-row slab are issued before any store (D may alias C, so
+      // the compiler would otherwise serialise each load behind the previous store)
 #pragma unroll
       for (int y = 0; y < T::TJ; ++y) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int jo = 32 * y + 8 * g;
           float cv[4] = {0.f, 0.f, 0.f, 0.f};
-          if (crow) {
-            const u32x2_t c2 = *reinterpret_cast<const u32x2_t*>(crow + lo_c + jo);
+          if (Cb) {
+            const u32x2_t c2 = cpre[x][y * 4 + g];
             cv[0] = bf2f(c2.x & 0xffff); cv[1] = bf2f(c2.x >> 16);
             cv[2] = bf2f(c2.y & 0xffff); cv[3] = bf2f(c2.y >> 16);
           }
@@ -241,24 +326,21 @@ void nt_mfma_kernel(const NtArgs a) {
     // the original orientation (transposed: original[j][i]). Each 32-row slab of a wave's
     // tile goes through LDS (fp32) so the weight read-modify-write is coalesced in either
     // orientation and the register-resident accumulators are only indexed statically.
-    constexpr int kLd = BN / 2 + 4;
+    constexpr int kLd = T::WTN + 4;
     float* slab = reinterpret_cast<float*>(smem) + wave * 32 * kLd;
-    const uint16_t* Cb = a.C ? a.C + (long long)l * a.sC : nullptr;
     void* outp = a.out_ptrs ? a.out_ptrs[l] : nullptr;
     void* wp = a.w_ptrs ? a.w_ptrs[l] : nullptr;
     const long long pitch = a.transposed ? a.m_real : a.n_real;
-    const unsigned lo_c = (unsigned)(li * a.ldc + 4 * lh);
 #pragma unroll
     for (int x = 0; x < T::TI; ++x) {
-      const uint16_t* crow = Cb ? Cb + (long long)(iw + 32 * x) * a.ldc + jw : nullptr;
 #pragma unroll
       for (int y = 0; y < T::TJ; ++y) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int jo = 32 * y + 8 * g;
           float cv[4] = {0.f, 0.f, 0.f, 0.f};
-          if (crow) {
-            const u32x2_t c2 = *reinterpret_cast<const u32x2_t*>(crow + lo_c + jo);
+          if (Cb) {
+            const u32x2_t c2 = cpre[x][y * 4 + g];
             cv[0] = bf2f(c2.x & 0xffff); cv[1] = bf2f(c2.x >> 16);
             cv[2] = bf2f(c2.y & 0xffff); cv[3] = bf2f(c2.y >> 16);
           }
@@ -272,29 +354,51 @@ void nt_mfma_kernel(const NtArgs a) {
       }
       __syncthreads();
       const int ibase = iw + 32 * x;
-      for (int p = lane; p < 32 * (BN / 2); p += 64) {
-        // normal: consecutive lanes walk j; transposed: consecutive lanes walk i
-        const int r = a.transposed ? (p & 31) : p / (BN / 2);
-        const int c = a.transposed ? (p >> 5) : p % (BN / 2);
-        const int i = ibase + r, j = jw + c;
-        if (i >= a.m_real || j >= a.n_real) continue;
-        const float u = slab[r * kLd + c];
-        const long long off = a.transposed ? (long long)j * pitch + i : (long long)i * pitch + j;
-        if (outp) {
-          if (a.out_dtype == DT_F32) static_cast<float*>(outp)[off] = u;
-          else static_cast<uint16_t*>(outp)[off] = f2bf(u);
+      // 32 x WTN slab, 64 lanes: consecutive lanes walk j (normal) or i (transposed).
+      // Loads of a batch of elements are issued before their stores.
+      constexpr int PER = 32 * T::WTN / 64;
+      constexpr int BATCH = 8;
+      static_assert(PER % BATCH == 0, "slab batching");
+#pragma unroll 1
+      for (int b0 = 0; b0 < PER; b0 += BATCH) {
+        long long offs[BATCH];
+        bool ok[BATCH];
+        float u[BATCH], wv[BATCH];
+#pragma unroll
+        for (int e = 0; e < BATCH; ++e) {
+          const int p = lane + 64 * (b0 + e);
+          const int r = a.transposed ? (p & 31) : p / T::WTN;
+          const int c = a.transposed ? (p >> 5) : p % T::WTN;
+          const int i = ibase + r, j = jw + c;
+          ok[e] = i < a.m_real && j < a.n_real;
+          offs[e] = a.transposed ? (long long)j * pitch + i : (long long)i * pitch + j;
+          u[e] = slab[r * kLd + c];
+          wv[e] = 0.f;
         }
         if (wp) {
-          if (a.w_dtype == DT_F32) {
-            float* w = static_cast<float*>(wp) + off;
-            float wv = *w;
-            if (a.decay != 1.f) wv = __fmul_rn(wv, a.decay);
-            *w = __fadd_rn(wv, -a.lrs * u);
-          } else {
-            uint16_t* w = static_cast<uint16_t*>(wp) + off;
-            float wv = bf2f(*w);
-            if (a.decay != 1.f) wv = bf2f(f2bf(__fmul_rn(wv, a.decay)));
-            *w = f2bf(__fadd_rn(wv, -a.lrs * u));
+#pragma unroll
+          for (int e = 0; e < BATCH; ++e)
+            if (ok[e])
+              wv[e] = a.w_dtype == DT_F32 ? static_cast<const float*>(wp)[offs[e]]
+                                          : bf2f(static_cast<const uint16_t*>(wp)[offs[e]]);
+        }
+#pragma unroll
+        for (int e = 0; e < BATCH; ++e) {
+          if (!ok[e]) continue;
+          if (outp) {
+            if (a.out_dtype == DT_F32) static_cast<float*>(outp)[offs[e]] = u[e];
+            else static_cast<uint16_t*>(outp)[offs[e]] = f2bf(u[e]);
+          }
+          if (wp) {
+            if (a.w_dtype == DT_F32) {
+              float w = wv[e];
+              if (a.decay != 1.f) w = __fmul_rn(w, a.decay);
+              static_cast<float*>(wp)[offs[e]] = __fadd_rn(w, -a.lrs * u[e]);
+            } else {
+              float w = wv[e];
+              if (a.decay != 1.f) w = bf2f(f2bf(__fmul_rn(w, a.decay)));
+              static_cast<uint16_t*>(wp)[offs[e]] = f2bf(__fadd_rn(w, -a.lrs * u[e]));
+            }
           }
         }
       }
@@ -303,23 +407,46 @@ void nt_mfma_kernel(const NtArgs a) {
   }
 }
 
+// K-slice pipeline of the NT kernel: BK-wide slices in an S-deep LDS ring. The default is
+// 64-wide slices double-buffered (one barrier per 64 MFMAs per SIMD); DMUON_NT_PIPE=32x4 selects
+// 32-wide slices four deep (three slices of prefetch, twice the barriers) as a tuning aid.
+int nt_pipe_variant() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("DMUON_NT_PIPE");
+    v = (e && e[0] == '3') ? 0 : 1;
+  }
+  return v;
+}
+
 }  // namespace
 
 hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   const long long nb = (long long)a.tiles_per_mat * a.L;
   if (nb <= 0) return hipSuccess;
-  dim3 grid((unsigned)nb), block(kThreads);
-#define DMUON_LAUNCH(T, M) hipLaunchKernelGGL((nt_mfma_kernel<T, T, M>), grid, block, 0, stream, a)
+  dim3 grid((unsigned)nb);
+  const int v = nt_pipe_variant();
+#define DMUON_NT(TILE, BK, S, WM, WN)                                                          \
+  do {                                                                                         \
+    dim3 block(64 * WM * WN);                                                                  \
+    if (a.mode == EPI_SYM)                                                                     \
+      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_SYM>), grid, block, 0,  \
+                         stream, a);                                                           \
+    else if (a.mode == EPI_NS)                                                                 \
+      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_NS>), grid, block, 0,   \
+                         stream, a);                                                           \
+    else                                                                                       \
+      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_FINAL>), grid, block, 0,\
+                         stream, a);                                                           \
+  } while (0)
   if (tile == 256) {
-    if (a.mode == EPI_SYM) DMUON_LAUNCH(256, EPI_SYM);
-    else if (a.mode == EPI_NS) DMUON_LAUNCH(256, EPI_NS);
-    else DMUON_LAUNCH(256, EPI_FINAL);
+    if (v == 1) DMUON_NT(256, 64, 2, 2, 4);
+    else DMUON_NT(256, 32, 4, 2, 4);
   } else {
-    if (a.mode == EPI_SYM) DMUON_LAUNCH(128, EPI_SYM);
-    else if (a.mode == EPI_NS) DMUON_LAUNCH(128, EPI_NS);
-    else DMUON_LAUNCH(128, EPI_FINAL);
+    if (v == 1) DMUON_NT(128, 64, 2, 2, 2);
+    else DMUON_NT(128, 32, 4, 2, 2);
   }
-#undef DMUON_LAUNCH
+#undef DMUON_NT
   return hipGetLastError();
 }
 
