@@ -64,6 +64,16 @@ struct Tile {
   static constexpr int RPL = 256 / ROWB;          // rows per 256-byte LDS bank line (64 banks)
   static constexpr int A_BYTES = BM * ROWB;
   static constexpr int STAGE = (BM + BN) * ROWB;
+  // epilogue staging per wave, one 32-row slab: row-major pitch EPN (WTN bf16 + 8 B, so the
+  // 32 rows of a lane column fall on distinct banks), transposed pitch EPT (32 bf16 + 16 B), and
+  // the fp32 slab of the final step (32 rows of WTN + 4 floats)
+  static constexpr int EPN = WTN * 2 + 8;
+  static constexpr int EPT = 32 * 2 + 16;
+  static constexpr int EPF = 32 * (WTN + 4) * 4;
+  static constexpr int EPI_MAX2 = (32 * EPN > WTN * EPT ? 32 * EPN : WTN * EPT);
+  static constexpr int EPI_REGION_RAW = (EPI_MAX2 > EPF ? EPI_MAX2 : EPF);
+  static constexpr int EPI_REGION = (EPI_REGION_RAW + 15) / 16 * 16;
+  static constexpr int LDS_BYTES = (S * STAGE > NW * EPI_REGION ? S * STAGE : NW * EPI_REGION);
   static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0, "tile rows vs DMA rows");
   static_assert((S - 2) * LPT <= 63, "vmcnt range");
   // LDS slot of 16-byte chunk kc of row r. A ds_read_b128 serves 16 lanes (256 B, all 64
@@ -102,7 +112,8 @@ template <int BM, int BN, int BK, int S, int WM, int WN, int MODE>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void nt_mfma_kernel(const NtArgs a) {
   using T = Tile<BM, BN, BK, S, WM, WN>;
-  __shared__ __attribute__((aligned(16))) char smem[S * T::STAGE];
+  __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
+  static_assert(T::LDS_BYTES <= 160 * 1024, "LDS budget");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -242,32 +253,27 @@ void nt_mfma_kernel(const NtArgs a) {
   wait_vmcnt<0>();
   bare_barrier();
 
-  // The epilogue's addend C (X for the NS step, A for the polynomial) for the whole wave tile
-  // is requested at once, so its latency is paid once per tile: element (x, y, g) is 4 bf16 at
-  // row iw + 32x + li, columns jw + 32y + 8g + 4lh .. +3.
   const int li = lane & 31, lh = lane >> 5;
   const int iw = i0 + wi * T::WTM, jw = j0 + wj * T::WTN;
   const uint16_t* Cb = a.C ? a.C + (long long)l * a.sC : nullptr;
-  u32x2_t cpre[T::TI][T::TJ * 4];
-  if (Cb) {
-    const unsigned lo = (unsigned)(li * a.ldc + 4 * lh);
+  // addend C (X for the NS step, A for the polynomial), one 32-row slab at a time, the next
+  // slab's loads in flight while the current one is processed: element (y, g) of slab x is
+  // 4 bf16 at row iw + 32x + li, columns jw + 32y + 8g + 4lh .. +3
+  const unsigned clo = (unsigned)(li * a.ldc + 4 * lh);
+  auto load_c = [&](int x, u32x2_t* dst) {
+    const uint16_t* crow = Cb + (long long)(iw + 32 * x) * a.ldc + jw + clo;
 #pragma unroll
-    for (int x = 0; x < T::TI; ++x) {
-      const uint16_t* crow = Cb + (long long)(iw + 32 * x) * a.ldc + jw + lo;
-#pragma unroll
-      for (int q = 0; q < T::TJ * 4; ++q)
-        cpre[x][q] = *reinterpret_cast<const u32x2_t*>(crow + 32 * (q >> 2) + 8 * (q & 3));
-    }
-  }
-
-  // ---- epilogue -----------------------------------------------------------------------
-  // element (x, y, g, e) of the wave tile, with li = lane & 31, lh = lane >> 5:
-  //   i = iw + 32x + li,   j = jw + 32y + 8g + 4lh + e      (acc[x][y][4g + e])
-  // Addresses split into a wave-uniform part (scalar registers) and one per-lane offset.
+    for (int q = 0; q < T::TJ * 4; ++q)
+      dst[q] = *reinterpret_cast<const u32x2_t*>(crow + 32 * (q >> 2) + 8 * (q & 3));
+  };
   float s = a.alpha;
   if (a.alpha_dev) s *= a.alpha_dev[l];
 
   if constexpr (MODE == EPI_SYM || MODE == EPI_NS) {
+    // Each 32-row slab of the wave tile goes through a small per-wave LDS staging area twice --
+    // row-major for D, then transposed for D^T (NS step) or the mirrored block (SYRK) -- so that
+    // the global stores are row segments (8 B x 16 lanes = 128 B for D, 16 B x 4 lanes = 64 B
+    // for D^T) instead of scattered 2-byte stores.
     uint16_t* Db = a.D + (long long)l * a.sD;
     uint16_t* DTb = nullptr;
     long long ldt = 0;
@@ -276,21 +282,21 @@ void nt_mfma_kernel(const NtArgs a) {
     } else {
       if (a.DT) { DTb = a.DT + (long long)l * a.sDT; ldt = a.lddt; }
     }
-    const unsigned lo_d = (unsigned)(li * a.ldd + 4 * lh);
-    const unsigned lo_t = (unsigned)(4 * lh * ldt + li);
+    char* reg = smem + wave * T::EPI_REGION;
+    u32x2_t cbuf[2][T::TJ * 4];
+    if (Cb) load_c(0, cbuf[0]);
 #pragma unroll
     for (int x = 0; x < T::TI; ++x) {
-      uint16_t* drow = Db + (long long)(iw + 32 * x) * a.ldd + jw;
-      // all addend loads of this 32-row slab are issued before any store (D may alias C, so
-      // the compiler would otherwise serialise each load behind the previous store)
+      if (Cb && x + 1 < T::TI) load_c(x + 1, cbuf[(x + 1) & 1]);
+      u32x2_t o2[T::TJ * 4];
 #pragma unroll
-      for (int y = 0; y < T::TJ; ++y) {
+      for (int y = 0; y < T::TJ; ++y)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int jo = 32 * y + 8 * g;
           float cv[4] = {0.f, 0.f, 0.f, 0.f};
           if (Cb) {
-            const u32x2_t c2 = cpre[x][y * 4 + g];
+            const u32x2_t c2 = cbuf[x & 1][y * 4 + g];
             cv[0] = bf2f(c2.x & 0xffff); cv[1] = bf2f(c2.x >> 16);
             cv[2] = bf2f(c2.y & 0xffff); cv[3] = bf2f(c2.y >> 16);
           }
@@ -307,17 +313,41 @@ void nt_mfma_kernel(const NtArgs a) {
             }
             o[e] = f2bf(r);
           }
-          u32x2_t packed;
-          packed.x = (unsigned)o[0] | ((unsigned)o[1] << 16);
-          packed.y = (unsigned)o[2] | ((unsigned)o[3] << 16);
-          *reinterpret_cast<u32x2_t*>(drow + lo_d + jo) = packed;
-          if (DTb) {
+          o2[y * 4 + g].x = (unsigned)o[0] | ((unsigned)o[1] << 16);
+          o2[y * 4 + g].y = (unsigned)o[2] | ((unsigned)o[3] << 16);
+          *reinterpret_cast<u32x2_t*>(reg + li * T::EPN + (jo + 4 * lh) * 2) = o2[y * 4 + g];
+        }
+      {
+        constexpr int CPRW = T::WTN / 4;          // 8-byte chunks per slab row
+        constexpr int RPIT = 64 / CPRW;           // slab rows per wave instruction
+        const int cr = lane / CPRW, cc = lane % CPRW;
+        uint16_t* dst = Db + (long long)(iw + 32 * x + cr) * a.ldd + jw + 4 * cc;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              uint16_t* tcol = DTb + (long long)(jw + jo + e) * ldt + iw + 32 * x;
-              tcol[lo_t] = o[e];
-            }
+        for (int r0 = 0; r0 < 32; r0 += RPIT) {
+          const u32x2_t v = *reinterpret_cast<const u32x2_t*>(reg + (r0 + cr) * T::EPN + 8 * cc);
+          *reinterpret_cast<u32x2_t*>(dst + (long long)r0 * a.ldd) = v;
+        }
+      }
+      if (DTb) {
+        // transposed slab [WTN][32] at pitch EPT; each lane scatters its 4 consecutive j
+#pragma unroll
+        for (int y = 0; y < T::TJ; ++y)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int j = 32 * y + 8 * g + 4 * lh;
+            uint16_t* col = reinterpret_cast<uint16_t*>(reg + j * T::EPT) + li;
+            const u32x2_t p = o2[y * 4 + g];
+            col[0] = (uint16_t)(p.x & 0xffff);
+            col[T::EPT / 2] = (uint16_t)(p.x >> 16);
+            col[T::EPT] = (uint16_t)(p.y & 0xffff);
+            col[3 * T::EPT / 2] = (uint16_t)(p.y >> 16);
           }
+        const int cr = lane >> 2, cc = lane & 3;  // 4 lanes x 16 B per 32-value row
+        uint16_t* dst = DTb + (long long)(jw + cr) * ldt + iw + 32 * x + 8 * cc;
+#pragma unroll
+        for (int r0 = 0; r0 < T::WTN; r0 += 16) {
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(reg + (r0 + cr) * T::EPT + 16 * cc);
+          *reinterpret_cast<u32x4_t*>(dst + (long long)r0 * ldt) = v;
         }
       }
     }
@@ -327,12 +357,14 @@ void nt_mfma_kernel(const NtArgs a) {
     // tile goes through LDS (fp32) so the weight read-modify-write is coalesced in either
     // orientation and the register-resident accumulators are only indexed statically.
     constexpr int kLd = T::WTN + 4;
-    float* slab = reinterpret_cast<float*>(smem) + wave * 32 * kLd;
+    float* slab = reinterpret_cast<float*>(smem + wave * T::EPI_REGION);
     void* outp = a.out_ptrs ? a.out_ptrs[l] : nullptr;
     void* wp = a.w_ptrs ? a.w_ptrs[l] : nullptr;
     const long long pitch = a.transposed ? a.m_real : a.n_real;
 #pragma unroll
     for (int x = 0; x < T::TI; ++x) {
+      u32x2_t cfin[T::TJ * 4];
+      if (Cb) load_c(x, cfin);
 #pragma unroll
       for (int y = 0; y < T::TJ; ++y) {
 #pragma unroll
@@ -340,7 +372,7 @@ void nt_mfma_kernel(const NtArgs a) {
           const int jo = 32 * y + 8 * g;
           float cv[4] = {0.f, 0.f, 0.f, 0.f};
           if (Cb) {
-            const u32x2_t c2 = cpre[x][y * 4 + g];
+            const u32x2_t c2 = cfin[y * 4 + g];
             cv[0] = bf2f(c2.x & 0xffff); cv[1] = bf2f(c2.x >> 16);
             cv[2] = bf2f(c2.y & 0xffff); cv[3] = bf2f(c2.y >> 16);
           }
@@ -352,57 +384,124 @@ void nt_mfma_kernel(const NtArgs a) {
           *reinterpret_cast<float4*>(slab + li * kLd + jo + 4 * lh) = u4;
         }
       }
-      __syncthreads();
       const int ibase = iw + 32 * x;
-      // 32 x WTN slab, 64 lanes: consecutive lanes walk j (normal) or i (transposed).
-      // Loads of a batch of elements are issued before their stores.
-      constexpr int PER = 32 * T::WTN / 64;
-      constexpr int BATCH = 8;
-      static_assert(PER % BATCH == 0, "slab batching");
-#pragma unroll 1
-      for (int b0 = 0; b0 < PER; b0 += BATCH) {
-        long long offs[BATCH];
-        bool ok[BATCH];
-        float u[BATCH], wv[BATCH];
+      // Read-modify-write of the slab in 8-element vectors (16 B of bf16 / 32 B of fp32):
+      // normal orientation: vector = 8 consecutive j of one row i (8 lanes per 64-column row);
+      // transposed: vector = 8 consecutive i of one original row j (4 lanes per 32-row column).
+      // All weight loads of the slab are issued before any store. Vectors that cross the real
+      // extent, or rows whose pitch breaks 16-byte alignment, take the per-element path.
+      constexpr int NV = 32 * T::WTN / 8 / 64;
+      const bool vpitch = (pitch & 7) == 0;
+      long long voff[NV];
+      bool vfull[NV];
+      int vr[NV], vc[NV];
+      u32x4_t wraw[NV][2];
 #pragma unroll
-        for (int e = 0; e < BATCH; ++e) {
-          const int p = lane + 64 * (b0 + e);
-          const int r = a.transposed ? (p & 31) : p / T::WTN;
-          const int c = a.transposed ? (p >> 5) : p % T::WTN;
-          const int i = ibase + r, j = jw + c;
-          ok[e] = i < a.m_real && j < a.n_real;
-          offs[e] = a.transposed ? (long long)j * pitch + i : (long long)i * pitch + j;
-          u[e] = slab[r * kLd + c];
-          wv[e] = 0.f;
+      for (int v = 0; v < NV; ++v) {
+        const int idx = v * 64 + lane;
+        if (!a.transposed) {
+          vr[v] = idx / (T::WTN / 8);
+          vc[v] = (idx % (T::WTN / 8)) * 8;
+          const int i = ibase + vr[v], j = jw + vc[v];
+          voff[v] = (long long)i * pitch + j;
+          vfull[v] = vpitch && i < a.m_real && j + 7 < a.n_real;
+        } else {
+          vc[v] = idx / 4;
+          vr[v] = (idx % 4) * 8;
+          const int i = ibase + vr[v], j = jw + vc[v];
+          voff[v] = (long long)j * pitch + i;
+          vfull[v] = vpitch && j < a.n_real && i + 7 < a.m_real;
         }
-        if (wp) {
-#pragma unroll
-          for (int e = 0; e < BATCH; ++e)
-            if (ok[e])
-              wv[e] = a.w_dtype == DT_F32 ? static_cast<const float*>(wp)[offs[e]]
-                                          : bf2f(static_cast<const uint16_t*>(wp)[offs[e]]);
+        if (wp && vfull[v]) {
+          if (a.w_dtype == DT_F32) {
+            const u32x4_t* q = reinterpret_cast<const u32x4_t*>(static_cast<const float*>(wp) + voff[v]);
+            wraw[v][0] = q[0];
+            wraw[v][1] = q[1];
+          } else {
+            wraw[v][0] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(wp) + voff[v]);
+          }
         }
+      }
 #pragma unroll
-        for (int e = 0; e < BATCH; ++e) {
-          if (!ok[e]) continue;
+      for (int v = 0; v < NV; ++v) {
+        float u[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          u[t] = a.transposed ? slab[(vr[v] + t) * kLd + vc[v]] : slab[vr[v] * kLd + vc[v] + t];
+        if (vfull[v]) {
           if (outp) {
-            if (a.out_dtype == DT_F32) static_cast<float*>(outp)[offs[e]] = u[e];
-            else static_cast<uint16_t*>(outp)[offs[e]] = f2bf(u[e]);
+            if (a.out_dtype == DT_F32) {
+              u32x4_t* q = reinterpret_cast<u32x4_t*>(static_cast<float*>(outp) + voff[v]);
+              q[0] = u32x4_t{__float_as_uint(u[0]), __float_as_uint(u[1]), __float_as_uint(u[2]),
+                             __float_as_uint(u[3])};
+              q[1] = u32x4_t{__float_as_uint(u[4]), __float_as_uint(u[5]), __float_as_uint(u[6]),
+                             __float_as_uint(u[7])};
+            } else {
+              u32x4_t o;
+              o.x = (unsigned)f2bf(u[0]) | ((unsigned)f2bf(u[1]) << 16);
+              o.y = (unsigned)f2bf(u[2]) | ((unsigned)f2bf(u[3]) << 16);
+              o.z = (unsigned)f2bf(u[4]) | ((unsigned)f2bf(u[5]) << 16);
+              o.w = (unsigned)f2bf(u[6]) | ((unsigned)f2bf(u[7]) << 16);
+              *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(outp) + voff[v]) = o;
+            }
           }
           if (wp) {
             if (a.w_dtype == DT_F32) {
-              float w = wv[e];
-              if (a.decay != 1.f) w = __fmul_rn(w, a.decay);
-              static_cast<float*>(wp)[offs[e]] = __fadd_rn(w, -a.lrs * u[e]);
+              float w[8];
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                w[t] = __uint_as_float(wraw[v][0][t]);
+                w[t + 4] = __uint_as_float(wraw[v][1][t]);
+              }
+              unsigned r[8];
+#pragma unroll
+              for (int t = 0; t < 8; ++t) {
+                float wv = w[t];
+                if (a.decay != 1.f) wv = __fmul_rn(wv, a.decay);
+                r[t] = __float_as_uint(__fadd_rn(wv, -a.lrs * u[t]));
+              }
+              u32x4_t* q = reinterpret_cast<u32x4_t*>(static_cast<float*>(wp) + voff[v]);
+              q[0] = u32x4_t{r[0], r[1], r[2], r[3]};
+              q[1] = u32x4_t{r[4], r[5], r[6], r[7]};
             } else {
-              float w = wv[e];
-              if (a.decay != 1.f) w = bf2f(f2bf(__fmul_rn(w, a.decay)));
-              static_cast<uint16_t*>(wp)[offs[e]] = f2bf(__fadd_rn(w, -a.lrs * u[e]));
+              unsigned r[8];
+#pragma unroll
+              for (int t = 0; t < 8; ++t) {
+                const unsigned word = wraw[v][0][t >> 1];
+                float wv = bf2f((t & 1) ? (word >> 16) : (word & 0xffff));
+                if (a.decay != 1.f) wv = bf2f(f2bf(__fmul_rn(wv, a.decay)));
+                r[t] = f2bf(__fadd_rn(wv, -a.lrs * u[t]));
+              }
+              *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(wp) + voff[v]) =
+                  u32x4_t{r[0] | (r[1] << 16), r[2] | (r[3] << 16), r[4] | (r[5] << 16),
+                          r[6] | (r[7] << 16)};
+            }
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int i = ibase + vr[v] + (a.transposed ? t : 0);
+            const int j = jw + vc[v] + (a.transposed ? 0 : t);
+            if (i >= a.m_real || j >= a.n_real) continue;
+            const long long off = a.transposed ? (long long)j * pitch + i : (long long)i * pitch + j;
+            if (outp) {
+              if (a.out_dtype == DT_F32) static_cast<float*>(outp)[off] = u[t];
+              else static_cast<uint16_t*>(outp)[off] = f2bf(u[t]);
+            }
+            if (wp) {
+              if (a.w_dtype == DT_F32) {
+                float wv = static_cast<const float*>(wp)[off];
+                if (a.decay != 1.f) wv = __fmul_rn(wv, a.decay);
+                static_cast<float*>(wp)[off] = __fadd_rn(wv, -a.lrs * u[t]);
+              } else {
+                float wv = bf2f(static_cast<const uint16_t*>(wp)[off]);
+                if (a.decay != 1.f) wv = bf2f(f2bf(__fmul_rn(wv, a.decay)));
+                static_cast<uint16_t*>(wp)[off] = f2bf(__fadd_rn(wv, -a.lrs * u[t]));
+              }
             }
           }
         }
       }
-      __syncthreads();
     }
   }
 }
