@@ -64,10 +64,10 @@ def build_matrix_set(torch, device, dtype, n_layers):
     return m
 
 
-def cpu_baseline(budget_s: float = 25.0) -> dict:
+def cpu_baseline(budget_s: float = 60.0) -> dict:
     """Times the oracle (numpy restatement of the reference math, fp32 compute) on the host:
-    momentum + Nesterov + direct NS x5 + update, for layer-0's k, q and down matrices; the full
-    step is extrapolated by matrix counts (v, o, gate, up share those NS costs)."""
+    momentum + Nesterov + 5 direct NS steps + update for every matrix of layer 0 (q, k, v, o,
+    gate, up, down); the 32-layer step is that time x 32 (all layers have the same shapes)."""
     import numpy as np
 
     from oracle import ns_oracle as o
@@ -80,35 +80,28 @@ def cpu_baseline(budget_s: float = 25.0) -> dict:
     rng = np.random.default_rng(0)
     per = {}
     spent = 0.0
-    for name, count in (("k", 2), ("q", 2), ("down", 3)):
-        rows, cols = LLAMA3_8B_LAYER[name]
-        W = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
-        g = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
-        buf = (rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
+    for name, (rows, cols) in LLAMA3_8B_LAYER.items():
+        W = rng.standard_normal((rows, cols), dtype=np.float32) * 0.02
+        g = rng.standard_normal((rows, cols), dtype=np.float32) * 0.02
+        buf = rng.standard_normal((rows, cols), dtype=np.float32) * 0.02
         t0 = time.perf_counter()
         o.muon_step(W, g, buf, lr=0.02, mu=0.95, wd=0.1, coefficients=o.KELLER, ns="direct",
                     dtype="fp32")
         dt = time.perf_counter() - t0
         spent += dt
-        per[name] = (dt, count)
-        if spent > budget_s and name != "down":
-            break
-    # per-layer time: k,v share the k cost; q,o the q cost; gate, up, down the down cost
-    layer_s = sum(dt * count for dt, count in per.values())
-    missing = {"k", "q", "down"} - set(per)
-    if missing:
-        return {"value": None, "unit": "ms", "cores": threads, "kind": "port",
-                "sample": f"incomplete: budget exhausted before {sorted(missing)}"}
+        per[name] = round(dt, 3)
+        if spent > budget_s and len(per) < len(LLAMA3_8B_LAYER):
+            return {"value": None, "unit": "ms", "cores": threads, "kind": "port",
+                    "sample": f"incomplete: {spent:.1f} s budget exhausted after {list(per)}"}
     return {
-        "value": round(layer_s * N_LAYERS * 1e3, 1),
+        "value": round(spent * N_LAYERS * 1e3, 1),
         "unit": "ms",
         "cores": threads,
         "kind": "port",
-        "sample": ("oracle/ns_oracle.muon_step (numpy, fp32 compute; the reference's fp16 "
-                   "casts are not emulated) on one k (1024x4096), one q (4096x4096) and one down "
-                   f"(4096x14336) matrix = {spent:.1f} s of CPU work; full 224-matrix step "
-                   "extrapolated as 32 layers x (2k + 2q + 3down)"),
-        "per_matrix_s": {k: round(v[0], 3) for k, v in per.items()},
+        "sample": ("oracle/ns_oracle.muon_step (numpy, fp32 compute; the reference's fp16 casts "
+                   f"are not emulated) on the 7 matrices of layer 0 = {spent:.1f} s of CPU work; "
+                   "the 32-layer step is extrapolated as 32 x layer 0"),
+        "per_matrix_s": per,
     }
 
 
@@ -120,7 +113,7 @@ def main():
     ap.add_argument("--layers", type=int, default=N_LAYERS, help="layers of the matrix set")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-adamw", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=25.0)
+    ap.add_argument("--cpu-budget", type=float, default=60.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 1 GiB device-to-device copy (HBM counter scale)")
     args = ap.parse_args()
