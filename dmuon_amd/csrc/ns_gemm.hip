@@ -75,7 +75,7 @@ struct Tile {
   static constexpr int EPI_REGION = (EPI_REGION_RAW + 15) / 16 * 16;
   static constexpr int LDS_BYTES = (S * STAGE > NW * EPI_REGION ? S * STAGE : NW * EPI_REGION);
   static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0, "tile rows vs DMA rows");
-  static_assert((S - 2) * LPT <= 63, "vmcnt range");
+  static_assert((S - 1) * LPT <= 63 && S <= 4, "vmcnt range");
   // LDS slot of 16-byte chunk kc of row r. A ds_read_b128 serves 16 lanes (256 B, all 64
   // banks) per pass; a fragment read has those 16 lanes on 16 consecutive rows at one chunk,
   // so rows sharing a bank line (r % RPL) must take distinct slots along r / RPL.
@@ -102,14 +102,59 @@ __device__ __forceinline__ void bare_barrier() {
 template <class T>
 __device__ __forceinline__ void wait_slices(int ahead) {
   // wait until at most `ahead` newer slices (T::LPT loads each) are still in flight
-  if constexpr (T::S >= 5) { if (ahead >= 3) { wait_vmcnt<3 * T::LPT>(); return; } }
-  if constexpr (T::S >= 4) { if (ahead >= 2) { wait_vmcnt<2 * T::LPT>(); return; } }
-  if constexpr (T::S >= 3) { if (ahead >= 1) { wait_vmcnt<1 * T::LPT>(); return; } }
+  if constexpr (3 * T::LPT <= 63) { if (ahead >= 3) { wait_vmcnt<3 * T::LPT>(); return; } }
+  if constexpr (2 * T::LPT <= 63) { if (ahead >= 2) { wait_vmcnt<2 * T::LPT>(); return; } }
+  if (ahead >= 1) { wait_vmcnt<T::LPT>(); return; }
   wait_vmcnt<0>();
 }
 
+// End-of-slice meeting point: wait until at most N loads of this wave are in flight (its share
+// of the next slice has landed) and all of its LDS reads have returned (its fragments of the
+// current slot are in registers), then s_barrier. gfx9 s_waitcnt encoding: vmcnt[3:0] +
+// vmcnt[5:4] at bits 15:14, expcnt bits 6:4 = 7 (untouched), lgkmcnt bits 11:8 = 0.
+template <int N>
+__device__ __forceinline__ void slice_barrier() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// sched_group_barrier sequence of one substep: M MFMAs, each followed by up to K = ceil((R+D)/M)
+// memory instructions, DS reads (R) first, then DMA (D, VMEM reads). The builtin needs literal
+// arguments, hence the compile-time recursion.
+template <int I, int M, int R, int D>
+__device__ __forceinline__ void sched_front() {
+  if constexpr (I < M) {
+    constexpr int N = R + D, K = (N + M - 1) / M;
+    constexpr int lo = K * I < N ? K * I : N, hi = K * (I + 1) < N ? K * (I + 1) : N;
+    constexpr int rlo = lo < R ? lo : R, rhi = hi < R ? hi : R;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (rhi > rlo) __builtin_amdgcn_sched_group_barrier(0x100, rhi - rlo, 0);
+    if constexpr (hi - lo > rhi - rlo)
+      __builtin_amdgcn_sched_group_barrier(0x020, (hi - lo) - (rhi - rlo), 0);
+    sched_front<I + 1, M, R, D>();
+  }
+}
+template <int N, int M, int R>
+__device__ __forceinline__ void sched_substeps() {
+  if constexpr (N > 0) {
+    sched_front<0, M, R, 0>();
+    sched_substeps<N - 1, M, R>();
+  }
+}
+
+// Waves per SIMD: a 128x128 wave tile holds 256 accumulator registers, so its block runs one
+// wave per SIMD with the whole 512-entry register file; smaller wave tiles run two.
+template <int BM, int BN, int WM, int WN>
+struct Occupancy {
+  static constexpr int WPE = (BM / WM) * (BN / WN) >= 128 * 128 ? 1 : 2;
+};
+
 template <int BM, int BN, int BK, int S, int WM, int WN, int MODE>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(64 * WM * WN)
+__attribute__((amdgpu_waves_per_eu(Occupancy<BM, BN, WM, WN>::WPE, Occupancy<BM, BN, WM, WN>::WPE)))
 void nt_mfma_kernel(const NtArgs a) {
   using T = Tile<BM, BN, BK, S, WM, WN>;
   __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
@@ -166,12 +211,12 @@ void nt_mfma_kernel(const NtArgs a) {
     offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8);
   }
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
-#define DMUON_ISSUE(slice_)                                                                    \
+  // slice sl_ of A and B into ring slot slot_ (this wave's share)
+#define DMUON_ISSUE(slice_, slot_)                                                             \
   do {                                                                                         \
-    const int sl_ = (slice_);                                                                  \
-    char* st_ = smem + (sl_ % S) * T::STAGE + wave * 1024;                                     \
-    const uint16_t* ak_ = Ab + sl_ * BK;                                                       \
-    const uint16_t* bk_ = Bb + sl_ * BK;                                                       \
+    char* st_ = smem + (slot_) * T::STAGE + wave * 1024;                                       \
+    const uint16_t* ak_ = Ab + (slice_) * BK;                                                  \
+    const uint16_t* bk_ = Bb + (slice_) * BK;                                                  \
     _Pragma("unroll") for (int q = 0; q < T::A_INST; ++q)                                      \
         __builtin_amdgcn_global_load_lds(ak_ + offa[q], (lds_ptr_t)(st_ + q * 1024 * T::NW), 16, 0, 0); \
     _Pragma("unroll") for (int q = 0; q < T::B_INST; ++q)                                      \
@@ -188,16 +233,12 @@ void nt_mfma_kernel(const NtArgs a) {
       for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.f;
 
   const int KT = a.K / BK;
-#pragma unroll
-  for (int s0 = 0; s0 < S - 1; ++s0)
-    if (s0 < KT) DMUON_ISSUE(s0);
-
+  constexpr int KS = BK / 16;                     // MFMA substeps per slice
+  static_assert(KS % 2 == 0, "fragment double buffer alternates per substep");
   const int arow0 = wi * T::WTM + (lane & 31);
   const int brow0 = wj * T::WTN + (lane & 31);
   const int khalf = lane >> 5;
 
-  // Fragments of substep ks+1 are read from LDS while the MFMAs of substep ks run.
-  constexpr int KS = BK / 16;
   auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8_t* af, bf16x8_t* bfr) {
     const int kc = ks * 2 + khalf;
 #pragma unroll
@@ -211,17 +252,29 @@ void nt_mfma_kernel(const NtArgs a) {
       bfr[y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
     }
   };
+  constexpr int NF = T::TI + T::TJ, NM = T::TI * T::TJ;
+  bf16x8_t af[2][T::TI], bfr[2][T::TJ];
+
+  // Ring schedule: slot s % S holds slice s; the prologue fills all S slots. Iteration kt
+  // consumes slice kt. Substeps 0 .. KS-2 each read the next substep's fragments under their
+  // own MFMAs. Before the last substep the wave waits for its share of slice kt+1 and for its
+  // own reads of slice kt, then meets the others at the barrier: past it slice kt+1 is complete
+  // and slot kt % S is free, so the DMA of slice kt+S and the reads of slice kt+1's first
+  // fragments both run under the last substep's MFMAs and no wave starts a slice with an empty
+  // pipeline. Past the end the DMA re-fetches the last slice into the free slot (never read),
+  // which keeps the number of loads per iteration, and so the vmcnt targets, uniform.
+#pragma unroll
+  for (int s0 = 0; s0 < S; ++s0) DMUON_ISSUE(min(s0, KT - 1), s0);
+  wait_slices<T>(S - 1);
+  bare_barrier();
+  load_frags(smem, smem + T::A_BYTES, 0, af[0], bfr[0]);
+
   for (int kt = 0; kt < KT; ++kt) {
-    wait_slices<T>(min(S - 2, KT - 1 - kt));
-    bare_barrier();                       // slice kt landed for every wave; slot kt-1 is free
-    if (kt + S - 1 < KT) DMUON_ISSUE(kt + S - 1);
     const char* sa = smem + (kt % S) * T::STAGE;
     const char* sb = sa + T::A_BYTES;
-    bf16x8_t af[2][T::TI], bfr[2][T::TJ];
-    load_frags(sa, sb, 0, af[0], bfr[0]);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 1 < KS) load_frags(sa, sb, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      load_frags(sa, sb, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
 #pragma unroll
       for (int x = 0; x < T::TI; ++x)
 #pragma unroll
@@ -231,23 +284,21 @@ void nt_mfma_kernel(const NtArgs a) {
           acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][y], af[ks & 1][x],
                                                               acc[x][y], 0, 0, 0);
     }
-    // Scheduling shape of the slice: substep 0's fragment reads, then each later substep's
-    // reads interleaved one-for-one with the first MFMAs of the substep before it.
-    constexpr int NF = T::TI + T::TJ, NM = T::TI * T::TJ;
-    __builtin_amdgcn_sched_group_barrier(0x100, NF, 0);              // DS reads
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 1 < KS) {
-#pragma unroll
-        for (int i = 0; i < NF; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);         // DS read
-        }
-        if constexpr (NM > NF) __builtin_amdgcn_sched_group_barrier(0x008, NM - NF, 0);
-      } else {
-        __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
-      }
+    sched_substeps<KS - 1, NM, NF>();
+    slice_barrier<(S - 2) * T::LPT>();
+    {
+      // reads first in program order: the DMA writes LDS, so later reads could not be
+      // scheduled ahead of it
+      const char* na = smem + ((kt + 1) % S) * T::STAGE;
+      load_frags(na, na + T::A_BYTES, 0, af[0], bfr[0]);
     }
+    DMUON_ISSUE(min(kt + S, KT - 1), kt % S);
+#pragma unroll
+    for (int x = 0; x < T::TI; ++x)
+#pragma unroll
+      for (int y = 0; y < T::TJ; ++y)
+        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[1][y], af[1][x], acc[x][y], 0, 0, 0);
+    sched_front<0, NM, NF, T::LPT>();
   }
 #undef DMUON_ISSUE
   wait_vmcnt<0>();
@@ -513,7 +564,7 @@ int nt_pipe_variant() {
   static int v = -1;
   if (v < 0) {
     const char* e = getenv("DMUON_NT_PIPE");
-    v = (e && e[0] == '3') ? 0 : 1;
+    v = (e && e[0] == '3') ? 0 : (e && e[0] == '4') ? 2 : 1;
   }
   return v;
 }
@@ -540,10 +591,11 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   } while (0)
   if (tile == 256) {
     if (v == 1) DMUON_NT(256, 64, 2, 2, 4);
+    else if (v == 2) DMUON_NT(256, 64, 2, 2, 2);
     else DMUON_NT(256, 32, 4, 2, 4);
   } else {
-    if (v == 1) DMUON_NT(128, 64, 2, 2, 2);
-    else DMUON_NT(128, 32, 4, 2, 2);
+    if (v == 0) DMUON_NT(128, 32, 4, 2, 2);
+    else DMUON_NT(128, 64, 2, 2, 2);
   }
 #undef DMUON_NT
   return hipGetLastError();
