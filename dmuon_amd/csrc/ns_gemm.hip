@@ -172,9 +172,28 @@ void nt_mfma_kernel(const NtArgs a) {
   int t = lb - l * a.tiles_per_mat;
   int bi, bj;
   if (a.tri) {
-    bi = 0;
-    while (t >= a.mt - bi) { t -= a.mt - bi; ++bi; }
-    bj = bi + t;
+    // upper triangle in groups of 8 tile-rows, each walked column-major: first the group's
+    // own triangular diagonal block (column c holds rows 0..c), then full 8-row columns, so
+    // that the tiles resident on one XCD at a time form compact blocks sharing panels in L2
+    int g0 = 0, gs = 0;
+    for (;;) {
+      gs = min(8, a.mt - g0);
+      const int cnt = gs * (gs + 1) / 2 + gs * (a.mt - g0 - gs);
+      if (t < cnt) break;
+      t -= cnt;
+      g0 += gs;
+    }
+    const int ntri = gs * (gs + 1) / 2;
+    if (t < ntri) {
+      int c = 0;
+      while (t > c) { t -= c + 1; ++c; }
+      bi = g0 + t;
+      bj = g0 + c;
+    } else {
+      t -= ntri;
+      bi = g0 + t % gs;
+      bj = g0 + gs + t / gs;
+    }
   } else {
     // groups of 8 tile-rows walked column-major so neighbouring blocks share B panels
     const int group = 8;
