@@ -226,9 +226,16 @@ def main():
             adamw_step()
         a1.record()
         torch.cuda.synchronize()
-        adamw = {"ms_per_step": round(a0.elapsed_time(a1) / 3, 3),
-                 "params": int(sum(p.numel() for n, p in rest.named_parameters() if n != "proj")),
-                 "impl": "torch._foreach (reference muon.py:1857-1916 semantics)"}
+        a_ms = a0.elapsed_time(a1) / 3
+        a_elems = int(sum(p.numel() for n, p in rest.named_parameters() if n != "proj"))
+        a_bytes = a_elems * 14          # bf16 p, g, exp_avg, exp_avg_sq read; p, m, v written
+        a_gbs = a_bytes / (a_ms * 1e-3) / 1e9
+        adamw = {"ms_per_step": round(a_ms, 3), "params": a_elems,
+                 "impl": "fused HIP multi-tensor AdamW (dmuon_adamw_multi; reference "
+                         "muon.py:1857-1916 semantics)",
+                 "roofline": {"bound": "hbm", "achieved": round(a_gbs, 1), "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(a_gbs / HBM_PEAK_GBS, 4),
+                              "algorithmic_bytes_per_elem": 14}}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
 

@@ -46,6 +46,8 @@ _SIGNATURES = {
                                       c_int, c_vp]),
     "dmuon_newton_schulz_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_fp,
                                           c_int, c_f, c_vp, c_i64, c_int, c_vp]),
+    "dmuon_adamw_multi": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_int, c_int, c_int,
+                                  c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -84,7 +86,7 @@ def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args))
 
 
-PROFILE_CLASSES = ("pre", "norm", "syrk", "poly", "gemm", "final")
+PROFILE_CLASSES = ("pre", "norm", "syrk", "poly", "gemm", "final", "adamw")
 
 
 def profile_enable(on: bool) -> None:

@@ -13,6 +13,7 @@ from .optim import (
     Muon,
     NewtonSchulz,
     direct_newton_schulz,
+    fused_adamw_,
     get_backend_status,
     get_ns_backend,
     gram_newton_schulz,
@@ -33,7 +34,8 @@ from .utils import (
 
 __all__ = [
     "dedicate_params", "replicate", "Muon", "NewtonSchulz", "newton_schulz",
-    "gram_newton_schulz", "direct_newton_schulz", "newton_schulz_batched", "get_backend_status",
+    "gram_newton_schulz", "direct_newton_schulz", "newton_schulz_batched", "fused_adamw_",
+    "get_backend_status",
     "get_ns_backend", "get_comm_ctx", "get_dedicated_params", "get_owned_params",
     "prepare_muon_grads", "wait_all_reduces", "wait_all_replicate_broadcasts",
     "wait_all_post_step_broadcasts", "broadcast_all_updates", "broadcast_all_updates_async",

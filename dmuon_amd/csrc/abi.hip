@@ -74,7 +74,7 @@ Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch) {
 // ---- launch profiler: optional hipEvent pairs around every kernel of run_group ----------------
 // Single-threaded use only (like the launch path itself). Events are host objects; no device
 // memory is allocated.
-enum ProfClass { PC_PRE = 0, PC_NORM, PC_SYRK, PC_POLY, PC_GEMM, PC_FINAL, PC_COUNT };
+enum ProfClass { PC_PRE = 0, PC_NORM, PC_SYRK, PC_POLY, PC_GEMM, PC_FINAL, PC_ADAMW, PC_COUNT };
 struct ProfRec {
   int cls;
   hipEvent_t a, b;
@@ -452,6 +452,32 @@ int dmuon_muon_update(void* const* w_ptrs, int w_dtype, const void* const* u_ptr
   u.w_ptrs = w_ptrs; u.w_dtype = w_dtype; u.u_ptrs = u_ptrs; u.u_dtype = u_dtype;
   u.numel = numel; u.L = batch; u.decay = decay; u.lrs = lrs;
   return check_launch(launch_update(u, static_cast<hipStream_t>(stream)), who);
+}
+
+int dmuon_adamw_multi(const int64_t* p_ptrs, const int64_t* g_ptrs, const int64_t* m_ptrs,
+                      const int64_t* v_ptrs, const int64_t* offsets, int n, int64_t total,
+                      int p_dtype, int g_dtype, int apply_wd, float wd_scale, float beta1,
+                      float alpha1, float beta2, float alpha2, float bc2_sqrt, float eps,
+                      float neg_step, void* stream) {
+  const char* who = "dmuon_adamw_multi";
+  if (n == 0 || total == 0) return 0;
+  if (n < 0 || total < 0) return fail("%s: negative tensor count or size", who);
+  if (!p_ptrs || !g_ptrs || !m_ptrs || !v_ptrs || !offsets)
+    return fail("%s: pointer arrays must be non-NULL", who);
+  if ((p_dtype != DMUON_DTYPE_F32 && p_dtype != DMUON_DTYPE_BF16) ||
+      (g_dtype != DMUON_DTYPE_F32 && g_dtype != DMUON_DTYPE_BF16))
+    return fail("%s: unsupported dtype (p %d, g %d)", who, p_dtype, g_dtype);
+  if (!(bc2_sqrt > 0.f)) return fail("%s: bias correction must be positive", who);
+  AdamWArgs a{};
+  a.p_ptrs = p_ptrs; a.g_ptrs = g_ptrs; a.m_ptrs = m_ptrs; a.v_ptrs = v_ptrs;
+  a.offsets = offsets; a.n = n; a.total = total;
+  a.p_dtype = p_dtype; a.g_dtype = g_dtype; a.apply_wd = apply_wd != 0;
+  a.wd_scale = wd_scale; a.beta1 = beta1; a.alpha1 = alpha1; a.beta2 = beta2; a.alpha2 = alpha2;
+  a.bc2_sqrt = bc2_sqrt; a.eps = eps; a.neg_step = neg_step;
+  const int pb = p_dtype == DMUON_DTYPE_F32 ? 4 : 2, gb = g_dtype == DMUON_DTYPE_F32 ? 4 : 2;
+  const double bytes = (double)total * (6.0 * pb + gb);   // read p, g, m, v; write p, m, v
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return timed(PC_ADAMW, 0.0, bytes, st, who, [&] { return launch_adamw(a, st); });
 }
 
 int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, int* m_pad,

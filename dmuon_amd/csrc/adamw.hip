@@ -1,0 +1,176 @@
+// Fused multi-tensor decoupled AdamW on gfx950: one HBM pass over a bucket of tensors.
+//
+// Per element, in the storage dtype of the parameter (p, exp_avg m and exp_avg_sq v share it)
+// with fp32 arithmetic, and rounded back to that dtype after every step exactly where the
+// reference's torch._foreach sequence materialises a tensor (muon.py:1902-1916):
+//
+//   p = R(p * (1 - lr*wd))                     (only when wd > 0)
+//   m = R(m * b1);  m = R(m + (1-b1) * g)
+//   v = R(v * b2);  v = R(v + (1-b2) * (g*g))
+//   d = R(sqrt(v)); d = R(d / sqrt(bc2)); d = R(d + eps)
+//   p = R(p + (-lr/bc1) * (m / d))
+//
+// Multiplies and adds are separate roundings (the library is built with -ffp-contract=off);
+// sqrt and division are the correctly rounded ones. For fp32 storage R is the identity.
+//
+// Work split: the tensors are concatenated into one index space (offsets = prefix sums of
+// their sizes); block b takes a contiguous range of it, finds its first tensor by binary
+// search and walks the tensors the range overlaps. Inside a tensor, 8-element vectors
+// (16-byte loads/stores of bf16, two of fp32) cover the aligned middle; ragged ends and
+// tensors whose base pointers are not 16-byte aligned take the per-element path.
+#include "dmuon_amd_internal.h"
+
+namespace dmuon {
+namespace {
+
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+__device__ __forceinline__ float bf2f(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+template <int D>
+__device__ __forceinline__ float rnd(float x) {
+  if constexpr (D == DT_BF16) return bf2f(f2bf(x));
+  else return x;
+}
+
+template <int D>
+__device__ __forceinline__ float ld1(const void* p, long long i) {
+  if constexpr (D == DT_BF16) return bf2f(static_cast<const uint16_t*>(p)[i]);
+  else return static_cast<const float*>(p)[i];
+}
+template <int D>
+__device__ __forceinline__ void st1(void* p, long long i, float x) {
+  if constexpr (D == DT_BF16) static_cast<uint16_t*>(p)[i] = f2bf(x);
+  else static_cast<float*>(p)[i] = x;
+}
+
+// 8 consecutive elements starting at element i (i % 8 == 0, base 16-byte aligned)
+template <int D>
+__device__ __forceinline__ void ld8(const void* p, long long i, float* x) {
+  if constexpr (D == DT_BF16) {
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = bf2f(w[k] & 0xffff);
+      x[2 * k + 1] = bf2f(w[k] >> 16);
+    }
+  } else {
+    const u32x4_t* q = reinterpret_cast<const u32x4_t*>(static_cast<const float*>(p) + i);
+    const u32x4_t w0 = q[0], w1 = q[1];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[k] = __uint_as_float(w0[k]);
+      x[k + 4] = __uint_as_float(w1[k]);
+    }
+  }
+}
+template <int D>
+__device__ __forceinline__ void st8(void* p, long long i, const float* x) {
+  if constexpr (D == DT_BF16) {
+    u32x4_t w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w[k] = (unsigned)f2bf(x[2 * k]) | ((unsigned)f2bf(x[2 * k + 1]) << 16);
+    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p) + i) = w;
+  } else {
+    u32x4_t* q = reinterpret_cast<u32x4_t*>(static_cast<float*>(p) + i);
+    q[0] = u32x4_t{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                   __float_as_uint(x[3])};
+    q[1] = u32x4_t{__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]),
+                   __float_as_uint(x[7])};
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void adamw_elt(float& p, float g, float& m, float& v,
+                                          const AdamWArgs& a) {
+  if (a.apply_wd) p = rnd<D>(p * a.wd_scale);
+  m = rnd<D>(m * a.beta1);
+  m = rnd<D>(m + a.alpha1 * g);
+  v = rnd<D>(v * a.beta2);
+  v = rnd<D>(v + a.alpha2 * (g * g));
+  float d = rnd<D>(sqrtf(v));
+  d = rnd<D>(d / a.bc2_sqrt);
+  d = rnd<D>(d + a.eps);
+  p = rnd<D>(p + a.neg_step * (m / d));
+}
+
+template <int PD, int GD>
+__global__ __launch_bounds__(256) void adamw_kernel(const AdamWArgs a) {
+  const long long lo = (long long)blockIdx.x * a.per_block;
+  if (lo >= a.total) return;
+  const long long hi = min(lo + a.per_block, a.total);
+  // last tensor whose start is <= lo
+  int t = 0, r = a.n - 1;
+  while (t < r) {
+    const int mid = (t + r + 1) >> 1;
+    if (a.offsets[mid] <= lo) t = mid; else r = mid - 1;
+  }
+  const int tid = threadIdx.x;
+  for (; t < a.n && a.offsets[t] < hi; ++t) {
+    const long long t0 = a.offsets[t];
+    const long long s = max(lo, t0) - t0, e = min(hi, a.offsets[t + 1]) - t0;
+    if (s >= e) continue;
+    void* P = reinterpret_cast<void*>(a.p_ptrs[t]);
+    const void* G = reinterpret_cast<const void*>(a.g_ptrs[t]);
+    void* M = reinterpret_cast<void*>(a.m_ptrs[t]);
+    void* V = reinterpret_cast<void*>(a.v_ptrs[t]);
+    const bool aligned = ((a.p_ptrs[t] | a.g_ptrs[t] | a.m_ptrs[t] | a.v_ptrs[t]) & 15) == 0;
+    long long vs = e, ve = e;
+    if (aligned) {
+      vs = min((s + 7) & ~7LL, e);
+      ve = max(e & ~7LL, vs);
+    }
+    for (long long i = vs + 8LL * tid; i < ve; i += 8LL * 256) {
+      float p[8], g[8], m[8], v[8];
+      ld8<PD>(P, i, p);
+      ld8<GD>(G, i, g);
+      ld8<PD>(M, i, m);
+      ld8<PD>(V, i, v);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) adamw_elt<PD>(p[k], g[k], m[k], v[k], a);
+      st8<PD>(P, i, p);
+      st8<PD>(M, i, m);
+      st8<PD>(V, i, v);
+    }
+    // ragged head [s, vs) and tail [ve, e) (the whole range when unaligned: vs = ve = e)
+    const long long nh = vs - s, nt = e - ve;
+    for (long long k = tid; k < nh + nt; k += 256) {
+      const long long i = k < nh ? s + k : ve + (k - nh);
+      float p = ld1<PD>(P, i), m = ld1<PD>(M, i), v = ld1<PD>(V, i);
+      adamw_elt<PD>(p, ld1<GD>(G, i), m, v, a);
+      st1<PD>(P, i, p);
+      st1<PD>(M, i, m);
+      st1<PD>(V, i, v);
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_adamw(AdamWArgs a, hipStream_t stream) {
+  if (a.total <= 0 || a.n <= 0) return hipSuccess;
+  long long blocks = (a.total + 16383) / 16384;
+  if (blocks > 8192) blocks = 8192;
+  long long per = (a.total + blocks - 1) / blocks;
+  per = (per + 7) & ~7LL;
+  a.per_block = per;
+  blocks = (a.total + per - 1) / per;
+  const dim3 grid((unsigned)blocks), block(256);
+  if (a.p_dtype == DT_F32 && a.g_dtype == DT_F32)
+    hipLaunchKernelGGL((adamw_kernel<DT_F32, DT_F32>), grid, block, 0, stream, a);
+  else if (a.p_dtype == DT_F32)
+    hipLaunchKernelGGL((adamw_kernel<DT_F32, DT_BF16>), grid, block, 0, stream, a);
+  else if (a.g_dtype == DT_F32)
+    hipLaunchKernelGGL((adamw_kernel<DT_BF16, DT_F32>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((adamw_kernel<DT_BF16, DT_BF16>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace dmuon

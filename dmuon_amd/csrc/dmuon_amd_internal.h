@@ -60,4 +60,17 @@ struct UpdateArgs {
 };
 hipError_t launch_update(const UpdateArgs& a, hipStream_t stream);
 
+// Fused decoupled AdamW over n tensors concatenated into one index space of `total` elements.
+// Arrays are device-resident; p/m/v share p_dtype, g has g_dtype.
+struct AdamWArgs {
+  const int64_t* p_ptrs; const int64_t* g_ptrs; const int64_t* m_ptrs; const int64_t* v_ptrs;
+  const int64_t* offsets;                 // [n+1] prefix sums of the tensor sizes
+  int n; long long total;
+  int p_dtype, g_dtype;
+  int apply_wd;
+  float wd_scale, beta1, alpha1, beta2, alpha2, bc2_sqrt, eps, neg_step;
+  long long per_block;                    // set by launch_adamw
+};
+hipError_t launch_adamw(AdamWArgs a, hipStream_t stream);
+
 }  // namespace dmuon

@@ -1,3 +1,4 @@
+from .adamw import fused_adamw_
 from .muon import Muon
 from .newton_schulz import (
     DEFAULT_COEFFICIENTS,
@@ -15,7 +16,7 @@ from .newton_schulz import (
 )
 
 __all__ = [
-    "Muon", "NewtonSchulz", "newton_schulz", "gram_newton_schulz", "direct_newton_schulz",
+    "Muon", "fused_adamw_", "NewtonSchulz", "newton_schulz", "gram_newton_schulz", "direct_newton_schulz",
     "newton_schulz_batched", "get_ns_backend", "get_backend_status", "YOU_COEFFICIENTS",
     "POLAR_EXPRESS_COEFFICIENTS", "KELLER_COEFFICIENTS", "DEFAULT_COEFFICIENTS",
     "DEFAULT_RESTART_ITERATIONS",

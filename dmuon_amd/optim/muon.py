@@ -16,7 +16,8 @@ weight update in its epilogue. The momentum buffer is fp32 and lives in
 ``optimizer.state[id(dp)]["momentum_buffer"]`` shaped ``(rows, cols)`` like the reference's.
 
 Parameters that are not dedicated (and 1-D dedicated ones) get the reference's decoupled AdamW
-(``muon.py:1857-1916``) through ``torch._foreach`` ops.
+(``muon.py:1857-1916``): its (step, dtype) buckets, each updated by one fused HIP pass
+(``dmuon_adamw_multi``) with the rounding points of the reference's ``torch._foreach`` sequence.
 """
 from __future__ import annotations
 
@@ -30,6 +31,7 @@ from torch import Tensor, nn
 
 from dmuon_amd import _C
 from dmuon_amd.api import iter_dedicated_states
+from dmuon_amd.optim.adamw import fused_adamw_
 from dmuon_amd.optim.newton_schulz import NewtonSchulz, _coeff_array, _float_dtype_code
 
 logger = logging.getLogger(__name__)
@@ -276,7 +278,8 @@ class Muon(torch.optim.Optimizer):
 
     # ------------------------------------------------------------------ AdamW
     def _step_adamw_group(self, group) -> None:
-        """Decoupled AdamW, bucketed by step (``muon.py:1857-1916``)."""
+        """Decoupled AdamW, bucketed by (step, param dtype, device, grad dtype) as in
+        ``muon.py:1857-1916``; each bucket is one fused HIP pass (``fused_adamw_``)."""
         lr = group["lr"]
         beta1, beta2 = group["betas"]
         wd = group["weight_decay"]
@@ -298,23 +301,11 @@ class Muon(torch.optim.Optimizer):
             buckets.setdefault(key, []).append((p.data, grad, state["exp_avg"], state["exp_avg_sq"]))
             if dp is not None:
                 dp._reduced_grad = None
-        for (step, _pdt, _pdev, _gdt), items in buckets.items():
-            params = [it[0] for it in items]
-            grads = [it[1] for it in items]
-            exp_avgs = [it[2] for it in items]
-            exp_avg_sqs = [it[3] for it in items]
-            if wd > 0:
-                torch._foreach_mul_(params, 1.0 - lr * wd)
-            torch._foreach_mul_(exp_avgs, beta1)
-            torch._foreach_add_(exp_avgs, grads, alpha=1.0 - beta1)
-            torch._foreach_mul_(exp_avg_sqs, beta2)
-            torch._foreach_addcmul_(exp_avg_sqs, grads, grads, value=1.0 - beta2)
-            bc1 = 1.0 - beta1 ** step
-            bc2 = 1.0 - beta2 ** step
-            denom = torch._foreach_sqrt(exp_avg_sqs)
-            torch._foreach_div_(denom, bc2 ** 0.5)
-            torch._foreach_add_(denom, eps)
-            torch._foreach_addcdiv_(params, exp_avgs, denom, value=-(lr / bc1))
+        for (step, _pdt, pdev, _gdt), items in buckets.items():
+            _require_cuda(pdev)
+            fused_adamw_([it[0] for it in items], [it[1] for it in items],
+                         [it[2] for it in items], [it[3] for it in items], step=step, lr=lr,
+                         betas=(beta1, beta2), weight_decay=wd, eps=eps)
 
     def zero_grad(self, set_to_none: bool = True):
         for p in self.model.parameters():

@@ -34,6 +34,9 @@
  *                                                                   params (direct NS, T steps)
  *   dmuon_newton_schulz_group dmuon/optim/newton_schulz.py:225-273  direct_newton_schulz(G) for
  *                                                                   `batch` same-shape matrices
+ *   dmuon_adamw_multi        dmuon/optim/muon.py:1857-1916          _adamw_update_batch: the
+ *                                                                   torch._foreach AdamW of one
+ *                                                                   (step, dtype) bucket
  */
 #ifndef DMUON_AMD_H_
 #define DMUON_AMD_H_
@@ -55,11 +58,11 @@ int dmuon_abi_version(void);
 
 /*
  * Launch profiler (no reference counterpart; measurement support for the benchmark harness).
- * While enabled, every kernel launched by dmuon_muon_step_group / dmuon_newton_schulz_group is
- * bracketed by hipEvents on its stream. dmuon_profile_collect synchronises on those events and
- * returns, per kernel class (0 pre, 1 norm-finalize, 2 SYRK X X^T, 3 SYRK-poly, 4 NS GEMM,
- * 5 final GEMM + update), the summed milliseconds, launch counts, useful FLOPs and algorithmic
- * bytes, then clears the records. n_classes must be >= 6. Not thread-safe.
+ * While enabled, every kernel launched by dmuon_muon_step_group / dmuon_newton_schulz_group /
+ * dmuon_adamw_multi is bracketed by hipEvents on its stream. dmuon_profile_collect synchronises
+ * on those events and returns, per kernel class (0 pre, 1 norm-finalize, 2 SYRK X X^T, 3 SYRK-poly, 4 NS GEMM,
+ * 5 final GEMM + update, 6 AdamW), the summed milliseconds, launch counts, useful FLOPs and
+ * algorithmic bytes, then clears the records. n_classes must be >= 7. Not thread-safe.
  */
 int dmuon_profile_enable(int on);
 int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* bytes,
@@ -158,6 +161,25 @@ int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out
                               int out_dtype, int rows, int cols, int batch, const float* coeffs,
                               int T, float eps, void* workspace, int64_t workspace_bytes, int tile,
                               void* stream);
+
+/*
+ * Decoupled AdamW over n tensors in one pass (one bucket of the reference's
+ * _adamw_update_batch: same step count, same param dtype, same grad dtype).
+ *   p_ptrs, g_ptrs, m_ptrs, v_ptrs: DEVICE arrays of n int64 addresses of the contiguous
+ *     param, grad, exp_avg and exp_avg_sq tensors; p, exp_avg, exp_avg_sq have p_dtype.
+ *   offsets: DEVICE array of n+1 int64 prefix sums of the tensor sizes (offsets[0] = 0,
+ *     offsets[n] = total).
+ *   Scalars, as the reference derives them in double and hands them to the foreach ops:
+ *     wd_scale = 1 - lr*wd (applied only if apply_wd), beta1, alpha1 = 1 - beta1, beta2,
+ *     alpha2 = 1 - beta2, bc2_sqrt = sqrt(1 - beta2^step), eps, neg_step = -lr/(1 - beta1^step).
+ * Per element: p = R(p*wd_scale); m = R(R(m*beta1) + alpha1*g); v = R(R(v*beta2) + alpha2*g*g);
+ * d = R(R(R(sqrt(v))/bc2_sqrt) + eps); p = R(p + neg_step*(m/d)), R = rounding to p_dtype.
+ */
+int dmuon_adamw_multi(const int64_t* p_ptrs, const int64_t* g_ptrs, const int64_t* m_ptrs,
+                      const int64_t* v_ptrs, const int64_t* offsets, int n, int64_t total,
+                      int p_dtype, int g_dtype, int apply_wd, float wd_scale, float beta1,
+                      float alpha1, float beta2, float alpha2, float bc2_sqrt, float eps,
+                      float neg_step, void* stream);
 
 #ifdef __cplusplus
 }
