@@ -113,6 +113,7 @@ def main():
     ap.add_argument("--layers", type=int, default=N_LAYERS, help="layers of the matrix set")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-adamw", action="store_true")
+    ap.add_argument("--no-clip", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=60.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 1 GiB device-to-device copy (HBM counter scale)")
@@ -190,6 +191,27 @@ def main():
     achieved_tf = mf_flops / (mf_ms * 1e-3) / 1e12
     pre = prof["pre"]
     pre_gbs = pre["bytes"] / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
+
+    # ---- gradient clipping of the same Muon gradients (segmented HIP kernels), reported apart --
+    clip = None
+    if not args.no_clip:
+        opt.clip_grad_norm_(1e30)          # coefficient 1: the values stay, the traffic is full
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record()
+        for _ in range(3):
+            opt.clip_grad_norm_(1e30)
+        c1.record()
+        torch.cuda.synchronize()
+        c_ms = c0.elapsed_time(c1) / 3
+        c_bytes = n_elems * 2 * 3           # bf16: read for the norms, read + write to scale
+        c_gbs = c_bytes / (c_ms * 1e-3) / 1e9
+        clip = {"ms_per_call": round(c_ms, 3), "grads": n_mats, "elements": n_elems,
+                "impl": "Muon.clip_grad_norm_ on dmuon_segmented_l2_norm_sq + "
+                        "dmuon_segmented_scale (reference fast_clip_kernel.cu semantics)",
+                "roofline": {"bound": "hbm", "achieved": round(c_gbs, 1), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(c_gbs / HBM_PEAK_GBS, 4),
+                             "algorithmic_bytes_per_elem": 6}}
 
     # ---- AdamW-routed params of the c5 config (embeddings, lm_head, norms), reported apart ----
     adamw = None
@@ -275,6 +297,7 @@ def main():
             "algorithmic_bytes_per_elem": 12,
         },
         "kernel_classes": classes,
+        "grad_clip": clip,
         "adamw_rest": adamw,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),

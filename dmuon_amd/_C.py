@@ -48,6 +48,10 @@ _SIGNATURES = {
                                           c_int, c_f, c_vp, c_i64, c_int, c_vp]),
     "dmuon_adamw_multi": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_int, c_int, c_int,
                                   c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_vp]),
+    "dmuon_segmented_l2_norm_sq": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp,
+                                           c_vp]),
+    "dmuon_segmented_scale": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp,
+                                      c_vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -86,7 +90,7 @@ def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args))
 
 
-PROFILE_CLASSES = ("pre", "norm", "syrk", "poly", "gemm", "final", "adamw")
+PROFILE_CLASSES = ("pre", "norm", "syrk", "poly", "gemm", "final", "adamw", "clip")
 
 
 def profile_enable(on: bool) -> None:

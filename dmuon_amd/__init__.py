@@ -6,6 +6,14 @@ owner-rank update path. The compute runs in ``dmuon_amd/csrc/libdmuon_amd.so`` (
 there is no CPU fallback.
 """
 from .api import dedicate_params, replicate
+from .fast_clip import (
+    GradClipBucket,
+    GradClipBucketStats,
+    SegmentedGradClipResult,
+    clip_grad_norm_buckets_,
+    try_clip_optimizer_grad_norm_buckets_,
+)
+from .grad_clip import MuonGradClipStats, clip_grad_norm_, register_muon_grad_clip_strategy
 from .optim import (
     KELLER_COEFFICIENTS,
     POLAR_EXPRESS_COEFFICIENTS,
@@ -40,4 +48,7 @@ __all__ = [
     "prepare_muon_grads", "wait_all_reduces", "wait_all_replicate_broadcasts",
     "wait_all_post_step_broadcasts", "broadcast_all_updates", "broadcast_all_updates_async",
     "YOU_COEFFICIENTS", "POLAR_EXPRESS_COEFFICIENTS", "KELLER_COEFFICIENTS",
+    "clip_grad_norm_", "clip_grad_norm_buckets_", "try_clip_optimizer_grad_norm_buckets_",
+    "register_muon_grad_clip_strategy", "MuonGradClipStats", "GradClipBucket",
+    "GradClipBucketStats", "SegmentedGradClipResult",
 ]

@@ -74,7 +74,9 @@ Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch) {
 // ---- launch profiler: optional hipEvent pairs around every kernel of run_group ----------------
 // Single-threaded use only (like the launch path itself). Events are host objects; no device
 // memory is allocated.
-enum ProfClass { PC_PRE = 0, PC_NORM, PC_SYRK, PC_POLY, PC_GEMM, PC_FINAL, PC_ADAMW, PC_COUNT };
+enum ProfClass {
+  PC_PRE = 0, PC_NORM, PC_SYRK, PC_POLY, PC_GEMM, PC_FINAL, PC_ADAMW, PC_CLIP, PC_COUNT
+};
 struct ProfRec {
   int cls;
   hipEvent_t a, b;
@@ -478,6 +480,52 @@ int dmuon_adamw_multi(const int64_t* p_ptrs, const int64_t* g_ptrs, const int64_
   const double bytes = (double)total * (6.0 * pb + gb);   // read p, g, m, v; write p, m, v
   hipStream_t st = static_cast<hipStream_t>(stream);
   return timed(PC_ADAMW, 0.0, bytes, st, who, [&] { return launch_adamw(a, st); });
+}
+
+static int clip_common(const int64_t* ptrs, const int64_t* numels, const int32_t* dtypes,
+                       const int32_t* segments, const int32_t* job_tensor_ids,
+                       const int64_t* job_offsets, int64_t n_jobs, int64_t chunk_size,
+                       const char* who, ClipArgs* a) {
+  if (chunk_size <= 0) return fail("%s: chunk_size must be positive", who);
+  if (n_jobs < 0 || n_jobs > 0x7fffffff) return fail("%s: job count out of range", who);
+  if (n_jobs > 0 && (!ptrs || !numels || !dtypes || !segments || !job_tensor_ids || !job_offsets))
+    return fail("%s: metadata arrays must be non-NULL", who);
+  a->ptrs = ptrs; a->numels = numels; a->dtypes = dtypes; a->segments = segments;
+  a->job_tensor_ids = job_tensor_ids; a->job_offsets = job_offsets;
+  a->n_jobs = n_jobs; a->chunk = chunk_size;
+  return 0;
+}
+
+int dmuon_segmented_l2_norm_sq(const int64_t* ptrs, const int64_t* numels, const int32_t* dtypes,
+                               const int32_t* segments, const int32_t* job_tensor_ids,
+                               const int64_t* job_offsets, int64_t n_jobs, int64_t chunk_size,
+                               float* local_sq, void* stream) {
+  const char* who = "dmuon_segmented_l2_norm_sq";
+  ClipArgs a{};
+  if (clip_common(ptrs, numels, dtypes, segments, job_tensor_ids, job_offsets, n_jobs, chunk_size,
+                  who, &a))
+    return 1;
+  if (n_jobs == 0) return 0;
+  if (!local_sq) return fail("%s: local_sq must be non-NULL", who);
+  a.local_sq = local_sq;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return timed(PC_CLIP, 0.0, 0.0, st, who, [&] { return launch_clip_sumsq(a, st); });
+}
+
+int dmuon_segmented_scale(const int64_t* ptrs, const int64_t* numels, const int32_t* dtypes,
+                          const int32_t* segments, const int32_t* job_tensor_ids,
+                          const int64_t* job_offsets, int64_t n_jobs, int64_t chunk_size,
+                          const float* coefs, void* stream) {
+  const char* who = "dmuon_segmented_scale";
+  ClipArgs a{};
+  if (clip_common(ptrs, numels, dtypes, segments, job_tensor_ids, job_offsets, n_jobs, chunk_size,
+                  who, &a))
+    return 1;
+  if (n_jobs == 0) return 0;
+  if (!coefs) return fail("%s: coefs must be non-NULL", who);
+  a.coefs = coefs;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return timed(PC_CLIP, 0.0, 0.0, st, who, [&] { return launch_clip_scale(a, st); });
 }
 
 int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, int* m_pad,

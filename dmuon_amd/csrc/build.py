@@ -14,7 +14,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent.parent
-SOURCES = ["ns_gemm.hip", "ew_kernels.hip", "adamw.hip", "abi.hip"]
+SOURCES = ["ns_gemm.hip", "ew_kernels.hip", "adamw.hip", "clip.hip", "abi.hip"]
 LIB_NAME = "libdmuon_amd.so"
 ARCH = "gfx950"
 

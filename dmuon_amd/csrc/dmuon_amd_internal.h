@@ -73,4 +73,15 @@ struct AdamWArgs {
 };
 hipError_t launch_adamw(AdamWArgs a, hipStream_t stream);
 
+// Segmented clip job table (device arrays, the reference's fast-clip layout).
+struct ClipArgs {
+  const int64_t* ptrs; const int64_t* numels; const int32_t* dtypes; const int32_t* segments;
+  const int32_t* job_tensor_ids; const int64_t* job_offsets;
+  long long n_jobs, chunk;
+  float* local_sq;                        // sumsq: per-segment accumulators (added to)
+  const float* coefs;                     // scale: per-segment coefficients
+};
+hipError_t launch_clip_sumsq(const ClipArgs& a, hipStream_t stream);
+hipError_t launch_clip_scale(const ClipArgs& a, hipStream_t stream);
+
 }  // namespace dmuon

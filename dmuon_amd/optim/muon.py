@@ -31,6 +31,8 @@ from torch import Tensor, nn
 
 from dmuon_amd import _C
 from dmuon_amd.api import iter_dedicated_states
+from dmuon_amd.grad_clip import _clip_ready_muon_grad_norm_
+from dmuon_amd.utils import prepare_muon_grads
 from dmuon_amd.optim.adamw import fused_adamw_
 from dmuon_amd.optim.newton_schulz import NewtonSchulz, _coeff_array, _float_dtype_code
 
@@ -128,6 +130,16 @@ class Muon(torch.optim.Optimizer):
                                     adamw_betas, adamw_weight_decay, adamw_eps)
         defaults = dict(lr=lr, momentum=momentum, weight_decay=weight_decay)
         super().__init__(groups, defaults)
+        # Muon-routed dedicated params -> their group (the gradients clip_grad_norm_ sees)
+        self._dp_to_muon_group_idx: dict[int, int] = {}
+        for gi, g in enumerate(self.param_groups):
+            if g.get("use_muon", False):
+                for p in g["params"]:
+                    dp = self._dp_by_param.get(id(p))
+                    if dp is not None:
+                        self._dp_to_muon_group_idx[id(dp)] = gi
+        self._grads_ready = False
+        self._last_muon_grad_clip_stats = None
 
     # ------------------------------------------------------------------ groups
     def _build_groups(self, param_groups, lr, momentum, wd, adamw_lr, betas, adamw_wd, eps):
@@ -164,6 +176,30 @@ class Muon(torch.optim.Optimizer):
                         "weight_decay": wd})
         return out
 
+    # ------------------------------------------------------------------ clipping
+    def _ensure_grads_ready(self, *, coalesce_wait: bool = False) -> None:
+        """``muon.py:1311-1321``: make the owned reduced gradients available, once per step."""
+        if self._grads_ready:
+            return
+        prepare_muon_grads(self.model)
+        self._grads_ready = True
+
+    @torch.no_grad()
+    def clip_grad_norm_(self, max_norm: Optional[float], *, norm_type: Optional[float] = None,
+                        error_if_nonfinite: Optional[bool] = None,
+                        foreach: Optional[bool] = None, strategy: Optional[object] = None):
+        """Clip the dedicated Muon gradients only (``muon.py:1323-1351``); AdamW-routed
+        gradients are left to ``torch.nn.utils.clip_grad_norm_``."""
+        self._ensure_grads_ready()
+        return _clip_ready_muon_grad_norm_(
+            self, max_norm, norm_type=2.0 if norm_type is None else norm_type,
+            error_if_nonfinite=False if error_if_nonfinite is None else error_if_nonfinite,
+            foreach=foreach, strategy="global_norm" if strategy is None else strategy)
+
+    @property
+    def last_muon_grad_clip_stats(self):
+        return self._last_muon_grad_clip_stats
+
     # ------------------------------------------------------------------ step
     @torch.no_grad()
     def step(self, closure=None):
@@ -190,6 +226,7 @@ class Muon(torch.optim.Optimizer):
             self._last_step_profile = {"_events": ev, "ns_matrix_count": count,
                                        "ns_input_numel": numel}
         self._optimizer_step_index += 1
+        self._grads_ready = False
         return loss
 
     def consume_last_step_profile(self) -> dict:
@@ -308,6 +345,8 @@ class Muon(torch.optim.Optimizer):
                          betas=(beta1, beta2), weight_decay=wd, eps=eps)
 
     def zero_grad(self, set_to_none: bool = True):
+        self._grads_ready = False
+        self._last_muon_grad_clip_stats = None
         for p in self.model.parameters():
             if p.grad is None:
                 continue

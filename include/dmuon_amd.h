@@ -37,6 +37,9 @@
  *   dmuon_adamw_multi        dmuon/optim/muon.py:1857-1916          _adamw_update_batch: the
  *                                                                   torch._foreach AdamW of one
  *                                                                   (step, dtype) bucket
+ *   dmuon_segmented_l2_norm_sq dmuon/csrc/fast_clip_kernel.cu:116-155 segmented_l2_norm_sq
+ *   dmuon_segmented_scale    dmuon/csrc/fast_clip_kernel.cu:157-195 segmented_scale
+ *                            (both bound by dmuon/fast_clip.py:267,301)
  */
 #ifndef DMUON_AMD_H_
 #define DMUON_AMD_H_
@@ -59,10 +62,11 @@ int dmuon_abi_version(void);
 /*
  * Launch profiler (no reference counterpart; measurement support for the benchmark harness).
  * While enabled, every kernel launched by dmuon_muon_step_group / dmuon_newton_schulz_group /
- * dmuon_adamw_multi is bracketed by hipEvents on its stream. dmuon_profile_collect synchronises
- * on those events and returns, per kernel class (0 pre, 1 norm-finalize, 2 SYRK X X^T, 3 SYRK-poly, 4 NS GEMM,
- * 5 final GEMM + update, 6 AdamW), the summed milliseconds, launch counts, useful FLOPs and
- * algorithmic bytes, then clears the records. n_classes must be >= 7. Not thread-safe.
+ * dmuon_adamw_multi / the segmented clip entry points is bracketed by hipEvents on its stream.
+ * dmuon_profile_collect synchronises on those events and returns, per kernel class (0 pre,
+ * 1 norm-finalize, 2 SYRK X X^T, 3 SYRK-poly, 4 NS GEMM, 5 final GEMM + update, 6 AdamW,
+ * 7 segmented clip), the summed milliseconds, launch counts, useful FLOPs and algorithmic
+ * bytes, then clears the records. n_classes must be >= 8. Not thread-safe.
  */
 int dmuon_profile_enable(int on);
 int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* bytes,
@@ -180,6 +184,30 @@ int dmuon_adamw_multi(const int64_t* p_ptrs, const int64_t* g_ptrs, const int64_
                       int p_dtype, int g_dtype, int apply_wd, float wd_scale, float beta1,
                       float alpha1, float beta2, float alpha2, float bc2_sqrt, float eps,
                       float neg_step, void* stream);
+
+/*
+ * Segmented gradient clipping, the two device operations of the reference's fast-clip path,
+ * with its argument list. Tensor t (of n) is the contiguous device buffer at address ptrs[t]
+ * with numels[t] elements of dtype dtypes[t] (DMUON_CLIP_*: the reference's codes) belonging
+ * to segment segments[t]. Job j covers elements [job_offsets[j], job_offsets[j] + chunk_size)
+ * of tensor job_tensor_ids[j], clipped to its size; every array is DEVICE-resident (int64 or
+ * int32 as typed) and the job table must reference valid tensors only.
+ *   dmuon_segmented_l2_norm_sq: local_sq[segments[t]] += sum of float(x)^2 over every job
+ *     (fp32 device array, caller-initialised; float atomics, so the addition order between
+ *     jobs is not fixed).
+ *   dmuon_segmented_scale: x <- dtype(float(x) * coefs[segments[t]]) in place.
+ */
+#define DMUON_CLIP_F32 0
+#define DMUON_CLIP_F16 1
+#define DMUON_CLIP_BF16 2
+int dmuon_segmented_l2_norm_sq(const int64_t* ptrs, const int64_t* numels, const int32_t* dtypes,
+                               const int32_t* segments, const int32_t* job_tensor_ids,
+                               const int64_t* job_offsets, int64_t n_jobs, int64_t chunk_size,
+                               float* local_sq, void* stream);
+int dmuon_segmented_scale(const int64_t* ptrs, const int64_t* numels, const int32_t* dtypes,
+                          const int32_t* segments, const int32_t* job_tensor_ids,
+                          const int64_t* job_offsets, int64_t n_jobs, int64_t chunk_size,
+                          const float* coefs, void* stream);
 
 #ifdef __cplusplus
 }
