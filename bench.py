@@ -114,6 +114,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-adamw", action="store_true")
     ap.add_argument("--no-clip", action="store_true")
+    ap.add_argument("--master", choices=("bf16", "fp32"), default="bf16",
+                    help="owner master dtype: bf16 = the bf16 weights themselves (c5); fp32 = "
+                         "the reference's default policy (fp32 master + fused bf16 publish)")
     ap.add_argument("--cpu-budget", type=float, default=60.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 1 GiB device-to-device copy (HBM counter scale)")
@@ -139,7 +142,11 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     model = build_matrix_set(torch, dev, torch.bfloat16, args.layers)
-    dmuon.dedicate_params(model, None, lambda n, p: p.dim() == 2)
+    # c5 keeps the bf16 weights as the owner's master (updated in place); --master fp32 runs the
+    # reference's default policy instead: fp32 masters, bf16 forward copies published by the
+    # update epilogue
+    policy = ({"defaults": {"master_dtype": torch.bfloat16}} if args.master == "bf16" else None)
+    dmuon.dedicate_params(model, None, lambda n, p: p.dim() == 2, param_policy=policy)
     dmuon.replicate(model)
     opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1,
                      ns_backend=dmuon.NewtonSchulz("direct", coefficients=KELLER))
@@ -278,6 +285,8 @@ def main():
                                f"({n_mats} bf16 matrices, {n_elems / 1e9:.2f} G elements), "
                                "fp32 momentum, 5 direct NS steps (Keller)",
                    "matrices": n_mats, "useful_ns_tflop_per_step": round(flops / 1e12, 2),
+                   "master": ("bf16 weights updated in place" if args.master == "bf16" else
+                              "fp32 master + bf16 forward copy published in the epilogue"),
                    "parallelism": "single GPU (world_size=1 owner)"},
         "ns_tflops": round(flops / (ms_per_step * 1e-3) / 1e12, 1),
         "ns_frac_mfma_peak_step": round(flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),

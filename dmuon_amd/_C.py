@@ -33,7 +33,8 @@ _SIGNATURES = {
                                    c_f, c_f, c_vp, c_int, c_vp]),
     "dmuon_ns_gemm_final_bf16": (c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64,
                                          c_i64, c_int, c_int, c_int, c_f, c_f, c_vp, c_int, c_int,
-                                         c_int, c_vp, c_int, c_vp, c_int, c_f, c_f, c_int, c_vp]),
+                                         c_int, c_vp, c_int, c_vp, c_int, c_vp, c_int, c_f, c_f,
+                                         c_int, c_vp]),
     "dmuon_muon_pre_partials": (c_int, [c_int, c_int]),
     "dmuon_muon_pre": (c_int, [c_vp, c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp,
                                c_int, c_int, c_int, c_int, c_int, c_f, c_int, c_int, c_vp]),
@@ -41,13 +42,13 @@ _SIGNATURES = {
     "dmuon_muon_update": (c_int, [c_vp, c_int, c_vp, c_int, c_i64, c_int, c_f, c_f, c_vp]),
     "dmuon_ns_plan": (c_int, [c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int),
                               ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_i64)]),
-    "dmuon_muon_step_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int, c_d,
-                                      c_d, c_d, c_int, c_int, c_fp, c_int, c_f, c_vp, c_i64,
-                                      c_int, c_vp]),
+    "dmuon_muon_step_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_vp, c_int, c_int, c_int,
+                                      c_int, c_d, c_d, c_d, c_int, c_int, c_fp, c_int, c_f, c_vp,
+                                      c_i64, c_int, c_vp]),
     "dmuon_newton_schulz_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_fp,
                                           c_int, c_f, c_vp, c_i64, c_int, c_vp]),
-    "dmuon_adamw_multi": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_int, c_int, c_int,
-                                  c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_vp]),
+    "dmuon_adamw_multi": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_int, c_int,
+                                  c_int, c_int, c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_vp]),
     "dmuon_segmented_l2_norm_sq": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp,
                                            c_vp]),
     "dmuon_segmented_scale": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp,

@@ -5,8 +5,13 @@ identity and the post-step publish has no peer, so the objects below keep only t
 optimizer reads and writes (reference: ``dmuon/_backends/fsdp2/param.py:116-628``,
 ``fsdp2/group.py:276-2177``, ``dmuon/_core/comm.py:24-110``):
 
-* ``_owned_data``  -- the owner's copy of the weight; here the live parameter storage itself,
-  so an in-place update is what the next forward reads (no packed-buffer publish).
+* ``_owned_data``  -- the owner's master copy of the weight, in the master dtype of its policy
+  (``fsdp2/param.py:263-271``; fp32 by default, ``policy.py:64-82``). When that dtype is the
+  forward parameter's own, the master *is* the parameter storage and the update is in place;
+  otherwise it is a separate tensor and every update is followed by the publish of
+  ``round(master)`` into the parameter (the reference copies ``_owned_data`` into the packed
+  forward buffer, ``fsdp2/group.py:766-781``) -- done by the update kernels themselves, in the
+  same pass (``publish_target``).
 * ``_reduced_grad`` -- the reduced gradient the Muon step consumes (``group.py:1348-1352``);
   here the parameter's ``.grad``, set by :func:`dmuon_amd.prepare_muon_grads` or read directly
   by the optimizer; cleared after the update (``muon.py:1746-1747``).
@@ -21,7 +26,9 @@ from torch import nn
 
 
 class DedicatedParam:
-    def __init__(self, param: nn.Parameter, name: str, owner_rank: int = 0):
+    def __init__(self, param: nn.Parameter, name: str, owner_rank: int = 0,
+                 param_dtype: Optional[torch.dtype] = None,
+                 master_dtype: Optional[torch.dtype] = None):
         self.param = param
         self._orig_param = param
         self.param_name = name
@@ -33,10 +40,25 @@ class DedicatedParam:
         self.is_tp_owner = False
         self._reduced_grad: Optional[torch.Tensor] = None
         self._accumulated_grad: Optional[torch.Tensor] = None
+        self._orig_dtype = param.dtype
+        self._param_dtype = param_dtype
+        self._master_dtype = master_dtype
+        mdt = master_dtype or param.dtype
+        fdt = param_dtype or param.dtype
+        # master from the original values (before any cast of the forward parameter)
+        self._master: Optional[torch.Tensor] = (
+            None if mdt == fdt else param.data.detach().to(dtype=mdt).clone())
+        if fdt != param.dtype:
+            param.data = param.data.to(fdt)
 
     @property
     def _owned_data(self) -> torch.Tensor:
-        return self.param.data
+        return self.param.data if self._master is None else self._master
+
+    def publish_target(self) -> Optional[torch.Tensor]:
+        """The forward tensor that receives round(master) after an update, or None when the
+        master is the parameter itself."""
+        return None if self._master is None else self.param.data
 
     def current_grad(self) -> Optional[torch.Tensor]:
         g = self._reduced_grad

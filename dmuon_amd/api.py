@@ -10,6 +10,7 @@ from __future__ import annotations
 import logging
 from typing import Callable, Optional
 
+import torch
 import torch.distributed as dist
 from torch import nn
 
@@ -58,9 +59,10 @@ def dedicate_params(
     for name, p in model.named_parameters():
         if not p.requires_grad or not predicate(name, p):
             continue
+        pdt, mdt = _resolve_policy(name, compute_dtype, kwargs.get("param_policy"))
         p._dedicated_owner_rank = 0
         assignment[p] = 0
-        dps.append(DedicatedParam(p, name, 0))
+        dps.append(DedicatedParam(p, name, 0, param_dtype=pdt, master_dtype=mdt))
     if not assignment:
         logger.warning("dedicate_params: no parameters matched the predicate")
         return assignment
@@ -68,6 +70,40 @@ def dedicate_params(
     model._dedicated_states = [DedicatedState(group)]
     model._dedicated_comm_ctx = LocalCommContext()
     return assignment
+
+
+_DTYPE_NAMES = {"fp32": torch.float32, "float32": torch.float32, "bf16": torch.bfloat16,
+                "bfloat16": torch.bfloat16, "fp16": torch.float16, "float16": torch.float16}
+
+
+def _as_dtype(value) -> Optional[torch.dtype]:
+    if value is None or isinstance(value, torch.dtype):
+        return value
+    key = str(value).strip().lower()
+    if key in ("", "none", "null"):
+        return None
+    if key not in _DTYPE_NAMES:
+        raise ValueError(f"unsupported dtype {value!r}")
+    return _DTYPE_NAMES[key]
+
+
+def _resolve_policy(name: str, compute_dtype, param_policy) -> tuple:
+    """(param_dtype, master_dtype) of one dedicated parameter, as the reference resolves them
+    (``policy.py:176-262``): ``compute_dtype`` is the legacy forward dtype, the policy's master
+    dtype defaults to fp32, and ``param_policy = {"defaults": {...}, "overrides": [{"name" |
+    "contains": ..., "set": {...}}]}`` may set ``param_dtype`` / ``master_dtype``."""
+    pdt, mdt = _as_dtype(compute_dtype), torch.float32
+    if param_policy:
+        layers = [param_policy.get("defaults", {}) or {}]
+        for ov in param_policy.get("overrides", ()) or ():
+            if ("name" in ov and ov["name"] == name) or ("contains" in ov and ov["contains"] in name):
+                layers.append(ov["set"])
+        for layer in layers:
+            if "param_dtype" in layer:
+                pdt = _as_dtype(layer["param_dtype"])
+            if "master_dtype" in layer:
+                mdt = _as_dtype(layer["master_dtype"])
+    return pdt, mdt
 
 
 def replicate(model: nn.Module, mesh=None, **kwargs) -> nn.Module:

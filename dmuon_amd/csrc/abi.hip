@@ -146,7 +146,8 @@ int plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, in
 
 // The whole Newton-Schulz + optional update sequence of one group; see dmuon_muon_step_group.
 int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* const* w_ptrs,
-              int w_dtype, void* const* out_ptrs, int out_dtype, int rows, int cols, int batch,
+              int w_dtype, void* const* pub_ptrs, int pub_dtype, void* const* out_ptrs,
+              int out_dtype, int rows, int cols, int batch,
               float mu, int nesterov, int first_step, float decay, float lrs, const float* coeffs,
               int T, float eps, void* workspace, int64_t workspace_bytes, int tile_req,
               hipStream_t stream, const char* who) {
@@ -157,6 +158,9 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
     return fail("%s: unsupported weight dtype code %d", who, w_dtype);
   if (out_ptrs && out_dtype != DMUON_DTYPE_F32 && out_dtype != DMUON_DTYPE_BF16)
     return fail("%s: unsupported output dtype code %d", who, out_dtype);
+  if (pub_ptrs && !w_ptrs) return fail("%s: pub_ptrs needs w_ptrs (it copies the new W)", who);
+  if (pub_ptrs && pub_dtype != DMUON_DTYPE_F32 && pub_dtype != DMUON_DTYPE_BF16)
+    return fail("%s: unsupported publish dtype code %d", who, pub_dtype);
   if (!coeffs || T <= 0) return fail("%s: need at least one (a, b, c) coefficient triple", who);
   if (!workspace || !aligned16(workspace)) return fail("%s: workspace NULL or misaligned", who);
   int tile, m_pad, n_pad;
@@ -204,6 +208,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
   const double gemm_flops = 2.0 * Ld * md * md * nd;
   const double wbytes = w_ptrs ? 2.0 * elems * (w_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0) : 0.0;
   const double obytes = out_ptrs ? elems * (out_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0) : 0.0;
+  const double pbytes = pub_ptrs ? elems * (pub_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0) : 0.0;
 
   uint16_t* xt_cur = w.XT0;
   uint16_t* xt_nxt = w.XT1;
@@ -250,8 +255,9 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
       g.mode = EPI_FINAL;
       g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;
       g.w_ptrs = w_ptrs; g.w_dtype = w_dtype; g.decay = decay; g.lrs = lrs;
+      g.pub_ptrs = pub_ptrs; g.pub_dtype = pub_dtype;
       g.m_real = m; g.n_real = n; g.transposed = tall ? 1 : 0;
-      if (timed(PC_FINAL, gemm_flops, wbytes + obytes, stream, who,
+      if (timed(PC_FINAL, gemm_flops, wbytes + obytes + pbytes, stream, who,
                 [&] { return launch_nt(g, tile, stream); }))
         return 1;
     }
@@ -296,7 +302,7 @@ int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* 
   return rc;
 }
 
-int dmuon_abi_version(void) { return 100; }
+int dmuon_abi_version(void) { return 101; }
 
 int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
                     int64_t strideB, const void* C, int64_t ldc, int64_t strideC, void* D,
@@ -380,7 +386,8 @@ int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const 
                              int64_t strideX, int M, int N, int batch, float alpha, float beta,
                              const float* alpha_dev, int m_real, int n_real, int transposed,
                              void* const* out_ptrs, int out_dtype, void* const* w_ptrs,
-                             int w_dtype, float decay, float lrs, int tile, void* stream) {
+                             int w_dtype, void* const* pub_ptrs, int pub_dtype, float decay,
+                             float lrs, int tile, void* stream) {
   const char* who = "dmuon_ns_gemm_final_bf16";
   if (batch == 0) return 0;
   if (gemm_common_checks(who, P, ldp, strideP, XT, ldxt, strideXT, X, ldx, strideX, M, N, batch, tile))
@@ -392,6 +399,9 @@ int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const 
     return fail("%s: unsupported output dtype %d", who, out_dtype);
   if (w_ptrs && w_dtype != DMUON_DTYPE_F32 && w_dtype != DMUON_DTYPE_BF16)
     return fail("%s: unsupported weight dtype %d", who, w_dtype);
+  if (pub_ptrs && !w_ptrs) return fail("%s: pub_ptrs needs w_ptrs (it copies the new W)", who);
+  if (pub_ptrs && pub_dtype != DMUON_DTYPE_F32 && pub_dtype != DMUON_DTYPE_BF16)
+    return fail("%s: unsupported publish dtype %d", who, pub_dtype);
   NtArgs g{};
   g.A = static_cast<const uint16_t*>(P); g.lda = ldp; g.sA = strideP;
   g.B = static_cast<const uint16_t*>(XT); g.ldb = ldxt; g.sB = strideXT;
@@ -401,6 +411,7 @@ int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const 
   g.C = static_cast<const uint16_t*>(X); g.ldc = ldx; g.sC = strideX;
   g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;
   g.w_ptrs = w_ptrs; g.w_dtype = w_dtype; g.decay = decay; g.lrs = lrs;
+  g.pub_ptrs = pub_ptrs; g.pub_dtype = pub_dtype;
   g.m_real = m_real; g.n_real = n_real; g.transposed = transposed ? 1 : 0;
   return check_launch(launch_nt(g, tile, static_cast<hipStream_t>(stream)), who);
 }
@@ -457,10 +468,10 @@ int dmuon_muon_update(void* const* w_ptrs, int w_dtype, const void* const* u_ptr
 }
 
 int dmuon_adamw_multi(const int64_t* p_ptrs, const int64_t* g_ptrs, const int64_t* m_ptrs,
-                      const int64_t* v_ptrs, const int64_t* offsets, int n, int64_t total,
-                      int p_dtype, int g_dtype, int apply_wd, float wd_scale, float beta1,
-                      float alpha1, float beta2, float alpha2, float bc2_sqrt, float eps,
-                      float neg_step, void* stream) {
+                      const int64_t* v_ptrs, const int64_t* pub_ptrs, const int64_t* offsets,
+                      int n, int64_t total, int p_dtype, int g_dtype, int pub_dtype, int apply_wd,
+                      float wd_scale, float beta1, float alpha1, float beta2, float alpha2,
+                      float bc2_sqrt, float eps, float neg_step, void* stream) {
   const char* who = "dmuon_adamw_multi";
   if (n == 0 || total == 0) return 0;
   if (n < 0 || total < 0) return fail("%s: negative tensor count or size", who);
@@ -469,15 +480,19 @@ int dmuon_adamw_multi(const int64_t* p_ptrs, const int64_t* g_ptrs, const int64_
   if ((p_dtype != DMUON_DTYPE_F32 && p_dtype != DMUON_DTYPE_BF16) ||
       (g_dtype != DMUON_DTYPE_F32 && g_dtype != DMUON_DTYPE_BF16))
     return fail("%s: unsupported dtype (p %d, g %d)", who, p_dtype, g_dtype);
+  if (pub_ptrs && pub_dtype != DMUON_DTYPE_F32 && pub_dtype != DMUON_DTYPE_BF16)
+    return fail("%s: unsupported publish dtype %d", who, pub_dtype);
   if (!(bc2_sqrt > 0.f)) return fail("%s: bias correction must be positive", who);
   AdamWArgs a{};
   a.p_ptrs = p_ptrs; a.g_ptrs = g_ptrs; a.m_ptrs = m_ptrs; a.v_ptrs = v_ptrs;
+  a.pub_ptrs = pub_ptrs; a.pub_dtype = pub_dtype;
   a.offsets = offsets; a.n = n; a.total = total;
   a.p_dtype = p_dtype; a.g_dtype = g_dtype; a.apply_wd = apply_wd != 0;
   a.wd_scale = wd_scale; a.beta1 = beta1; a.alpha1 = alpha1; a.beta2 = beta2; a.alpha2 = alpha2;
   a.bc2_sqrt = bc2_sqrt; a.eps = eps; a.neg_step = neg_step;
   const int pb = p_dtype == DMUON_DTYPE_F32 ? 4 : 2, gb = g_dtype == DMUON_DTYPE_F32 ? 4 : 2;
-  const double bytes = (double)total * (6.0 * pb + gb);   // read p, g, m, v; write p, m, v
+  const double qb = pub_ptrs ? (pub_dtype == DMUON_DTYPE_F32 ? 4 : 2) : 0;
+  const double bytes = (double)total * (6.0 * pb + gb + qb);   // read p,g,m,v; write p,m,v(,q)
   hipStream_t st = static_cast<hipStream_t>(stream);
   return timed(PC_ADAMW, 0.0, bytes, st, who, [&] { return launch_adamw(a, st); });
 }
@@ -535,10 +550,10 @@ int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int*
 }
 
 int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
-                          void* const* w_ptrs, int w_dtype, int rows, int cols, int batch,
-                          double lr, double mu, double wd, int nesterov, int first_step,
-                          const float* coeffs, int T, float eps, void* workspace,
-                          int64_t workspace_bytes, int tile, void* stream) {
+                          void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype,
+                          int rows, int cols, int batch, double lr, double mu, double wd,
+                          int nesterov, int first_step, const float* coeffs, int T, float eps,
+                          void* workspace, int64_t workspace_bytes, int tile, void* stream) {
   const char* who = "dmuon_muon_step_group";
   if (batch == 0) return 0;
   if (!buf_ptrs || !w_ptrs) return fail("%s: buf_ptrs and w_ptrs must be non-NULL", who);
@@ -546,9 +561,9 @@ int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_pt
   const double scale = 0.2 * sqrt((double)(rows > cols ? rows : cols));
   const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
   const float lrs = (float)(lr * scale);
-  return run_group(g_ptrs, g_dtype, buf_ptrs, w_ptrs, w_dtype, nullptr, 0, rows, cols, batch,
-                   (float)mu, nesterov, first_step, decay, lrs, coeffs, T, eps, workspace,
-                   workspace_bytes, tile, static_cast<hipStream_t>(stream), who);
+  return run_group(g_ptrs, g_dtype, buf_ptrs, w_ptrs, w_dtype, pub_ptrs, pub_dtype, nullptr, 0,
+                   rows, cols, batch, (float)mu, nesterov, first_step, decay, lrs, coeffs, T, eps,
+                   workspace, workspace_bytes, tile, static_cast<hipStream_t>(stream), who);
 }
 
 int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,
@@ -558,8 +573,8 @@ int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out
   const char* who = "dmuon_newton_schulz_group";
   if (batch == 0) return 0;
   if (!out_ptrs) return fail("%s: out_ptrs must be non-NULL", who);
-  return run_group(g_ptrs, g_dtype, nullptr, nullptr, 0, out_ptrs, out_dtype, rows, cols, batch,
-                   0.f, 0, 1, 1.f, 0.f, coeffs, T, eps, workspace, workspace_bytes, tile,
+  return run_group(g_ptrs, g_dtype, nullptr, nullptr, 0, nullptr, 0, out_ptrs, out_dtype, rows,
+                   cols, batch, 0.f, 0, 1, 1.f, 0.f, coeffs, T, eps, workspace, workspace_bytes, tile,
                    static_cast<hipStream_t>(stream), who);
 }
 

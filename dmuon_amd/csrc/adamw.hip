@@ -9,6 +9,7 @@
 //   v = R(v * b2);  v = R(v + (1-b2) * (g*g))
 //   d = R(sqrt(v)); d = R(d / sqrt(bc2)); d = R(d + eps)
 //   p = R(p + (-lr/bc1) * (m / d))
+//   q = round_to_q_dtype(p)                    (optional: the forward copy of a master p)
 //
 // Multiplies and adds are separate roundings (the library is built with -ffp-contract=off);
 // sqrt and division are the correctly rounded ones. For fp32 storage R is the identity.
@@ -120,7 +121,10 @@ __global__ __launch_bounds__(256) void adamw_kernel(const AdamWArgs a) {
     const void* G = reinterpret_cast<const void*>(a.g_ptrs[t]);
     void* M = reinterpret_cast<void*>(a.m_ptrs[t]);
     void* V = reinterpret_cast<void*>(a.v_ptrs[t]);
-    const bool aligned = ((a.p_ptrs[t] | a.g_ptrs[t] | a.m_ptrs[t] | a.v_ptrs[t]) & 15) == 0;
+    const int64_t pub_addr = a.pub_ptrs ? a.pub_ptrs[t] : 0;
+    void* Q = reinterpret_cast<void*>(pub_addr);           // forward copy of p, or null
+    const bool aligned =
+        ((a.p_ptrs[t] | a.g_ptrs[t] | a.m_ptrs[t] | a.v_ptrs[t] | pub_addr) & 15) == 0;
     long long vs = e, ve = e;
     if (aligned) {
       vs = min((s + 7) & ~7LL, e);
@@ -137,6 +141,10 @@ __global__ __launch_bounds__(256) void adamw_kernel(const AdamWArgs a) {
       st8<PD>(P, i, p);
       st8<PD>(M, i, m);
       st8<PD>(V, i, v);
+      if (Q) {
+        if (a.pub_dtype == DT_BF16) st8<DT_BF16>(Q, i, p);
+        else st8<DT_F32>(Q, i, p);
+      }
     }
     // ragged head [s, vs) and tail [ve, e) (the whole range when unaligned: vs = ve = e)
     const long long nh = vs - s, nt = e - ve;
@@ -147,6 +155,10 @@ __global__ __launch_bounds__(256) void adamw_kernel(const AdamWArgs a) {
       st1<PD>(P, i, p);
       st1<PD>(M, i, m);
       st1<PD>(V, i, v);
+      if (Q) {
+        if (a.pub_dtype == DT_BF16) st1<DT_BF16>(Q, i, p);
+        else st1<DT_F32>(Q, i, p);
+      }
     }
   }
 }

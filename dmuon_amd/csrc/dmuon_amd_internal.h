@@ -29,6 +29,7 @@ struct NtArgs {
   uint16_t* DT; long long lddt, sDT;      // bf16 [L][N][M] (EPI_NS, optional)
   void* const* out_ptrs; int out_dtype;   // EPI_FINAL: per-matrix U outputs (original shape)
   void* const* w_ptrs; int w_dtype;       // EPI_FINAL: per-matrix weights updated in place
+  void* const* pub_ptrs; int pub_dtype;   // EPI_FINAL: optional forward copies of the new W
   float decay, lrs;                       // W <- round(W*decay) - lrs*U   (decay==1: no decay rounding)
   int m_real, n_real, transposed;         // true NS dims; transposed: original = X^T (n_real x m_real)
 };
@@ -64,9 +65,10 @@ hipError_t launch_update(const UpdateArgs& a, hipStream_t stream);
 // Arrays are device-resident; p/m/v share p_dtype, g has g_dtype.
 struct AdamWArgs {
   const int64_t* p_ptrs; const int64_t* g_ptrs; const int64_t* m_ptrs; const int64_t* v_ptrs;
+  const int64_t* pub_ptrs;                // optional forward copies of the new p (pub_dtype)
   const int64_t* offsets;                 // [n+1] prefix sums of the tensor sizes
   int n; long long total;
-  int p_dtype, g_dtype;
+  int p_dtype, g_dtype, pub_dtype;
   int apply_wd;
   float wd_scale, beta1, alpha1, beta2, alpha2, bc2_sqrt, eps, neg_step;
   long long per_block;                    // set by launch_adamw

@@ -430,7 +430,11 @@ void nt_mfma_kernel(const NtArgs a) {
     float* slab = reinterpret_cast<float*>(smem + wave * T::EPI_REGION);
     void* outp = a.out_ptrs ? a.out_ptrs[l] : nullptr;
     void* wp = a.w_ptrs ? a.w_ptrs[l] : nullptr;
+    void* pp = (wp && a.pub_ptrs) ? a.pub_ptrs[l] : nullptr;   // forward copy of the new W
     const long long pitch = a.transposed ? a.m_real : a.n_real;
+    // 16-byte vectors need 16-byte aligned bases (torch allocations are; views may not be)
+    const bool valign = ((reinterpret_cast<uintptr_t>(wp) | reinterpret_cast<uintptr_t>(outp) |
+                          reinterpret_cast<uintptr_t>(pp)) & 15) == 0;
 #pragma unroll
     for (int x = 0; x < T::TI; ++x) {
       u32x2_t cfin[T::TJ * 4];
@@ -461,7 +465,7 @@ void nt_mfma_kernel(const NtArgs a) {
       // All weight loads of the slab are issued before any store. Vectors that cross the real
       // extent, or rows whose pitch breaks 16-byte alignment, take the per-element path.
       constexpr int NV = 32 * T::WTN / 8 / 64;
-      const bool vpitch = (pitch & 7) == 0;
+      const bool vpitch = (pitch & 7) == 0 && valign;
       long long voff[NV];
       bool vfull[NV];
       int vr[NV], vc[NV];
@@ -516,6 +520,7 @@ void nt_mfma_kernel(const NtArgs a) {
             }
           }
           if (wp) {
+            float wn[8];   // the updated weights
             if (a.w_dtype == DT_F32) {
               float w[8];
 #pragma unroll
@@ -528,7 +533,8 @@ void nt_mfma_kernel(const NtArgs a) {
               for (int t = 0; t < 8; ++t) {
                 float wv = w[t];
                 if (a.decay != 1.f) wv = __fmul_rn(wv, a.decay);
-                r[t] = __float_as_uint(__fadd_rn(wv, -a.lrs * u[t]));
+                wn[t] = __fadd_rn(wv, -a.lrs * u[t]);
+                r[t] = __float_as_uint(wn[t]);
               }
               u32x4_t* q = reinterpret_cast<u32x4_t*>(static_cast<float*>(wp) + voff[v]);
               q[0] = u32x4_t{r[0], r[1], r[2], r[3]};
@@ -541,32 +547,61 @@ void nt_mfma_kernel(const NtArgs a) {
                 float wv = bf2f((t & 1) ? (word >> 16) : (word & 0xffff));
                 if (a.decay != 1.f) wv = bf2f(f2bf(__fmul_rn(wv, a.decay)));
                 r[t] = f2bf(__fadd_rn(wv, -a.lrs * u[t]));
+                wn[t] = bf2f(r[t]);
               }
               *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(wp) + voff[v]) =
                   u32x4_t{r[0] | (r[1] << 16), r[2] | (r[3] << 16), r[4] | (r[5] << 16),
                           r[6] | (r[7] << 16)};
             }
+            if (pp) {
+              // publish: the forward copy in its own dtype, same layout as W
+              if (a.pub_dtype == DT_BF16) {
+                *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(pp) + voff[v]) =
+                    u32x4_t{(unsigned)f2bf(wn[0]) | ((unsigned)f2bf(wn[1]) << 16),
+                            (unsigned)f2bf(wn[2]) | ((unsigned)f2bf(wn[3]) << 16),
+                            (unsigned)f2bf(wn[4]) | ((unsigned)f2bf(wn[5]) << 16),
+                            (unsigned)f2bf(wn[6]) | ((unsigned)f2bf(wn[7]) << 16)};
+              } else {
+                u32x4_t* q = reinterpret_cast<u32x4_t*>(static_cast<float*>(pp) + voff[v]);
+                q[0] = u32x4_t{__float_as_uint(wn[0]), __float_as_uint(wn[1]),
+                               __float_as_uint(wn[2]), __float_as_uint(wn[3])};
+                q[1] = u32x4_t{__float_as_uint(wn[4]), __float_as_uint(wn[5]),
+                               __float_as_uint(wn[6]), __float_as_uint(wn[7])};
+              }
+            }
           }
         } else {
-#pragma unroll
+          // ragged edges and unaligned bases, one element at a time (kept rolled, re-reading U
+          // from the slab, so the unrolled slab loop around it stays small)
+#pragma unroll 1
           for (int t = 0; t < 8; ++t) {
             const int i = ibase + vr[v] + (a.transposed ? t : 0);
             const int j = jw + vc[v] + (a.transposed ? 0 : t);
             if (i >= a.m_real || j >= a.n_real) continue;
             const long long off = a.transposed ? (long long)j * pitch + i : (long long)i * pitch + j;
+            const float ut = a.transposed ? slab[(vr[v] + t) * kLd + vc[v]]
+                                          : slab[vr[v] * kLd + vc[v] + t];
             if (outp) {
-              if (a.out_dtype == DT_F32) static_cast<float*>(outp)[off] = u[t];
-              else static_cast<uint16_t*>(outp)[off] = f2bf(u[t]);
+              if (a.out_dtype == DT_F32) static_cast<float*>(outp)[off] = ut;
+              else static_cast<uint16_t*>(outp)[off] = f2bf(ut);
             }
             if (wp) {
+              float wn;
               if (a.w_dtype == DT_F32) {
                 float wv = static_cast<const float*>(wp)[off];
                 if (a.decay != 1.f) wv = __fmul_rn(wv, a.decay);
-                static_cast<float*>(wp)[off] = __fadd_rn(wv, -a.lrs * u[t]);
+                wn = __fadd_rn(wv, -a.lrs * ut);
+                static_cast<float*>(wp)[off] = wn;
               } else {
                 float wv = bf2f(static_cast<const uint16_t*>(wp)[off]);
                 if (a.decay != 1.f) wv = bf2f(f2bf(__fmul_rn(wv, a.decay)));
-                static_cast<uint16_t*>(wp)[off] = f2bf(__fadd_rn(wv, -a.lrs * u[t]));
+                const uint16_t h = f2bf(__fadd_rn(wv, -a.lrs * ut));
+                static_cast<uint16_t*>(wp)[off] = h;
+                wn = bf2f(h);
+              }
+              if (pp) {
+                if (a.pub_dtype == DT_BF16) static_cast<uint16_t*>(pp)[off] = f2bf(wn);
+                else static_cast<float*>(pp)[off] = wn;
               }
             }
           }

@@ -9,7 +9,7 @@ There is no CPU path: tensors must live on the GPU.
 """
 from __future__ import annotations
 
-from typing import Sequence
+from typing import Optional, Sequence
 
 import torch
 from torch import Tensor
@@ -38,11 +38,15 @@ def adamw_scalars(step: int, lr: float, betas: tuple[float, float], weight_decay
 
 def fused_adamw_(params: Sequence[Tensor], grads: Sequence[Tensor], exp_avgs: Sequence[Tensor],
                  exp_avg_sqs: Sequence[Tensor], *, step: int, lr: float,
-                 betas: tuple[float, float], weight_decay: float, eps: float) -> None:
+                 betas: tuple[float, float], weight_decay: float, eps: float,
+                 publish: Optional[Sequence[Optional[Tensor]]] = None) -> None:
     """In-place AdamW step of one bucket (same step, param dtype and grad dtype).
 
-    Raises ``ValueError`` for mismatched lists, shapes or dtypes and ``RuntimeError`` for
-    tensors that are not on the GPU or not contiguous (gradients are made contiguous).
+    ``publish``: optional forward copies (one per param, or None) that receive the new param
+    rounded to their dtype in the same pass -- the owner's master -> forward publish; all of
+    them share one dtype. Raises ``ValueError`` for mismatched lists, shapes or dtypes and
+    ``RuntimeError`` for tensors that are not on the GPU or not contiguous (gradients are made
+    contiguous).
     """
     n = len(params)
     if not (len(grads) == len(exp_avgs) == len(exp_avg_sqs) == n):
@@ -71,15 +75,33 @@ def fused_adamw_(params: Sequence[Tensor], grads: Sequence[Tensor], exp_avgs: Se
             if not t.is_contiguous():
                 raise RuntimeError("fused_adamw_: params and AdamW state must be contiguous")
         gs.append(g if g.is_contiguous() else g.contiguous())
+    qdt = None
+    if publish is not None:
+        if len(publish) != n:
+            raise ValueError("fused_adamw_: publish must list one tensor (or None) per param")
+        for p, q in zip(params, publish):
+            if q is None:
+                continue
+            if q.device != dev or q.dtype not in _CODES or not q.is_contiguous():
+                raise ValueError("fused_adamw_: publish targets must be contiguous fp32/bf16 "
+                                 "tensors on the params' device")
+            if q.numel() != p.numel() or (qdt is not None and q.dtype != qdt):
+                raise ValueError("fused_adamw_: publish targets must match the params in size "
+                                 "and share one dtype")
+            qdt = q.dtype
     offsets = [0]
     for p in params:
         offsets.append(offsets[-1] + p.numel())
+    pubs = [0] * n if qdt is None else [0 if q is None else q.data_ptr() for q in publish]
     table = ([p.data_ptr() for p in params] + [g.data_ptr() for g in gs]
-             + [m.data_ptr() for m in exp_avgs] + [v.data_ptr() for v in exp_avg_sqs] + offsets)
+             + [m.data_ptr() for m in exp_avgs] + [v.data_ptr() for v in exp_avg_sqs] + pubs
+             + offsets)
     dtab = torch.tensor(table, dtype=torch.int64, pin_memory=True).to(dev, non_blocking=True)
     base = dtab.data_ptr()
     s = adamw_scalars(step, lr, betas, weight_decay, eps)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    _C.call("dmuon_adamw_multi", base, base + 8 * n, base + 16 * n, base + 24 * n, base + 32 * n,
-            n, offsets[-1], _CODES[pdt], _CODES[gdt], s["apply_wd"], s["wd_scale"], s["beta1"],
-            s["alpha1"], s["beta2"], s["alpha2"], s["bc2_sqrt"], s["eps"], s["neg_step"], stream)
+    _C.call("dmuon_adamw_multi", base, base + 8 * n, base + 16 * n, base + 24 * n,
+            None if qdt is None else base + 32 * n, base + 40 * n, n, offsets[-1], _CODES[pdt],
+            _CODES[gdt], 0 if qdt is None else _CODES[qdt], s["apply_wd"], s["wd_scale"],
+            s["beta1"], s["alpha1"], s["beta2"], s["alpha2"], s["bc2_sqrt"], s["eps"],
+            s["neg_step"], stream)

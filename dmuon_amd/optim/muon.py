@@ -252,7 +252,9 @@ class Muon(torch.optim.Optimizer):
             first = "momentum_buffer" not in st
             rows = p.shape[0]
             cols = p.numel() // rows
-            key = (rows, cols, g.dtype, p.dtype, g.device, first)
+            pub = dp.publish_target()
+            key = (rows, cols, g.dtype, dp._owned_data.dtype,
+                   None if pub is None else pub.dtype, g.device, first)
             buckets.setdefault(key, []).append((dp, g))
         return buckets
 
@@ -260,7 +262,7 @@ class Muon(torch.optim.Optimizer):
         lr, mu, wd = float(group["lr"]), float(group["momentum"]), float(group["weight_decay"])
         coeffs, T = _coeff_array(self._ns.resolved_coefficients())
         count = numel = 0
-        for (rows, cols, gdt, wdt, dev, first), items in self._buckets(group).items():
+        for (rows, cols, gdt, wdt, pdt, dev, first), items in self._buckets(group).items():
             _require_cuda(dev)
             L_all = len(items)
             num_cus = torch.cuda.get_device_properties(dev).multi_processor_count
@@ -270,7 +272,7 @@ class Muon(torch.optim.Optimizer):
                 L = len(part)
                 tile, _, _, nbytes = _C.plan(rows, cols, L, 0, num_cus)
                 ws = self._get_workspace(dev, nbytes)
-                gs, bufs, ws_ = [], [], []
+                gs, bufs, ws_, pubs = [], [], [], []
                 for dp, g in part:
                     st = self.state[id(dp)]
                     if "momentum_buffer" not in st:
@@ -284,14 +286,20 @@ class Muon(torch.optim.Optimizer):
                     gs.append(g)
                     bufs.append(st["momentum_buffer"])
                     ws_.append(W)
+                    if pdt is not None:
+                        pubs.append(dp.publish_target())
                 ptrs = _pinned_ptrs([t.data_ptr() for t in gs] + [t.data_ptr() for t in bufs]
-                                    + [t.data_ptr() for t in ws_], dev)
+                                    + [t.data_ptr() for t in ws_]
+                                    + [t.data_ptr() for t in pubs], dev)
                 base = ptrs.data_ptr()
                 stream = torch.cuda.current_stream(dev).cuda_stream
+                # the forward copies (master != parameter) are written by the same epilogue
+                pub_base = base + 24 * L if pubs else None
+                pub_code = _float_dtype_code(pubs[0]) if pubs else 0
                 _C.call("dmuon_muon_step_group", base, _float_dtype_code(gs[0]), base + 8 * L,
-                        base + 16 * L, _float_dtype_code(ws_[0]), rows, cols, L, lr, mu, wd,
-                        int(self._nesterov), int(first), coeffs, T, self._ns_eps,
-                        ws.data_ptr(), ws.numel(), tile, stream)
+                        base + 16 * L, _float_dtype_code(ws_[0]), pub_base, pub_code, rows, cols,
+                        L, lr, mu, wd, int(self._nesterov), int(first), coeffs, T,
+                        self._ns_eps, ws.data_ptr(), ws.numel(), tile, stream)
                 count += L
                 numel += L * rows * cols
             for dp, _ in items:
@@ -328,21 +336,27 @@ class Muon(torch.optim.Optimizer):
             if grad is None:
                 continue
             key_obj = id(dp) if dp is not None else p
+            # a dedicated param updates its master (_owned_data) and publishes the forward copy
+            param = dp._owned_data if dp is not None else p.data
+            pub = dp.publish_target() if dp is not None else None
             state = self.state[key_obj]
             if len(state) == 0:
                 state["step"] = 0
-                state["exp_avg"] = torch.zeros_like(p)
-                state["exp_avg_sq"] = torch.zeros_like(p)
+                state["exp_avg"] = torch.zeros_like(param)
+                state["exp_avg_sq"] = torch.zeros_like(param)
             state["step"] += 1
-            key = (state["step"], p.dtype, p.device, grad.dtype)
-            buckets.setdefault(key, []).append((p.data, grad, state["exp_avg"], state["exp_avg_sq"]))
+            key = (state["step"], param.dtype, param.device, grad.dtype,
+                   None if pub is None else pub.dtype)
+            buckets.setdefault(key, []).append(
+                (param, grad, state["exp_avg"], state["exp_avg_sq"], pub))
             if dp is not None:
                 dp._reduced_grad = None
-        for (step, _pdt, pdev, _gdt), items in buckets.items():
+        for (step, _pdt, pdev, _gdt, pubdt), items in buckets.items():
             _require_cuda(pdev)
             fused_adamw_([it[0] for it in items], [it[1] for it in items],
                          [it[2] for it in items], [it[3] for it in items], step=step, lr=lr,
-                         betas=(beta1, beta2), weight_decay=wd, eps=eps)
+                         betas=(beta1, beta2), weight_decay=wd, eps=eps,
+                         publish=None if pubdt is None else [it[4] for it in items])
 
     def zero_grad(self, set_to_none: bool = True):
         self._grads_ready = False

@@ -32,6 +32,7 @@
  *   dmuon_muon_step_group    dmuon/optim/muon.py:1683-1740          one owner's per-param Muon
  *                                                                   math for `batch` same-shape
  *                                                                   params (direct NS, T steps)
+ *                            + dmuon/_backends/fsdp2/group.py:766-781 owner publish copy-in
  *   dmuon_newton_schulz_group dmuon/optim/newton_schulz.py:225-273  direct_newton_schulz(G) for
  *                                                                   `batch` same-shape matrices
  *   dmuon_adamw_multi        dmuon/optim/muon.py:1857-1916          _adamw_update_batch: the
@@ -105,13 +106,17 @@ int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* 
  *   out_ptrs != NULL: out[l] <- U                      (dtype out_dtype)
  *   w_ptrs   != NULL: W[l] <- round(W*decay) - lrs*U    (dtype w_dtype; decay == 1 skips the
  *                                                       decay rounding)
+ *   pub_ptrs != NULL: pub[l] <- round(new W[l])         (dtype pub_dtype; needs w_ptrs): the
+ *     forward copy of an owner's master weight, written in the same pass (the reference copies
+ *     _owned_data into the packed forward buffer afterwards, fsdp2/group.py:766-781)
  */
 int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT,
                              int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx,
                              int64_t strideX, int M, int N, int batch, float alpha, float beta,
                              const float* alpha_dev, int m_real, int n_real, int transposed,
                              void* const* out_ptrs, int out_dtype, void* const* w_ptrs,
-                             int w_dtype, float decay, float lrs, int tile, void* stream);
+                             int w_dtype, void* const* pub_ptrs, int pub_dtype, float decay,
+                             float lrs, int tile, void* stream);
 
 /* Number of partial sums per matrix that dmuon_muon_pre writes for a padded Rp x Cp matrix. */
 int dmuon_muon_pre_partials(int Rp, int Cp);
@@ -151,14 +156,16 @@ int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int*
  *   momentum (+Nesterov), normalise, T direct Newton-Schulz steps with per-step coefficients
  *   coeffs[3*t .. 3*t+2] = (a, b, c) (HOST array), then
  *   W <- round(W*(1 - lr*wd)) - lr*0.2*sqrt(max(rows, cols)) * U    (decay skipped if wd <= 0)
+ * and, when pub_ptrs != NULL, pub[l] <- round_to_pub_dtype(new W[l]) in the same epilogue (the
+ * owner's forward copy when W is a master in another dtype; NULL when W is the forward tensor).
  * Each NS step is SYRK (X X^T) -> SYRK-poly (b*A + c*A A^T) -> GEMM (a*X + P X) on bf16 MFMA.
  * workspace: device memory of at least the planned bytes; its contents need no initialisation.
  */
 int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
-                          void* const* w_ptrs, int w_dtype, int rows, int cols, int batch,
-                          double lr, double mu, double wd, int nesterov, int first_step,
-                          const float* coeffs, int T, float eps, void* workspace,
-                          int64_t workspace_bytes, int tile, void* stream);
+                          void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype,
+                          int rows, int cols, int batch, double lr, double mu, double wd,
+                          int nesterov, int first_step, const float* coeffs, int T, float eps,
+                          void* workspace, int64_t workspace_bytes, int tile, void* stream);
 
 /* direct_newton_schulz for `batch` same-shape rows x cols matrices: out[l] <- NS(g[l]). */
 int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,
@@ -171,6 +178,8 @@ int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out
  * _adamw_update_batch: same step count, same param dtype, same grad dtype).
  *   p_ptrs, g_ptrs, m_ptrs, v_ptrs: DEVICE arrays of n int64 addresses of the contiguous
  *     param, grad, exp_avg and exp_avg_sq tensors; p, exp_avg, exp_avg_sq have p_dtype.
+ *   pub_ptrs: NULL, or a DEVICE array of n addresses of forward copies that receive
+ *     round_to_pub_dtype(new p) in the same pass (an owner's master -> forward publish).
  *   offsets: DEVICE array of n+1 int64 prefix sums of the tensor sizes (offsets[0] = 0,
  *     offsets[n] = total).
  *   Scalars, as the reference derives them in double and hands them to the foreach ops:
@@ -180,10 +189,10 @@ int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out
  * d = R(R(R(sqrt(v))/bc2_sqrt) + eps); p = R(p + neg_step*(m/d)), R = rounding to p_dtype.
  */
 int dmuon_adamw_multi(const int64_t* p_ptrs, const int64_t* g_ptrs, const int64_t* m_ptrs,
-                      const int64_t* v_ptrs, const int64_t* offsets, int n, int64_t total,
-                      int p_dtype, int g_dtype, int apply_wd, float wd_scale, float beta1,
-                      float alpha1, float beta2, float alpha2, float bc2_sqrt, float eps,
-                      float neg_step, void* stream);
+                      const int64_t* v_ptrs, const int64_t* pub_ptrs, const int64_t* offsets,
+                      int n, int64_t total, int p_dtype, int g_dtype, int pub_dtype, int apply_wd,
+                      float wd_scale, float beta1, float alpha1, float beta2, float alpha2,
+                      float bc2_sqrt, float eps, float neg_step, void* stream);
 
 /*
  * Segmented gradient clipping, the two device operations of the reference's fast-clip path,

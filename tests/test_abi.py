@@ -82,16 +82,21 @@ def test_group_validation_without_gpu():
     coeff = (ctypes.c_float * 15)(*([3.4445, -4.7750, 2.0315] * 5))
     p = ctypes.c_void_p(4096)
     # workspace too small
-    msg = _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, 512, 1024, 1, 0.02, 0.95, 0.0, 1, 1,
-                                         coeff, 5, 1e-7, p, 16, 0, None))
+    msg = _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1, 0.02, 0.95, 0.0,
+                                         1, 1, coeff, 5, 1e-7, p, 16, 0, None))
     assert "workspace" in msg
     # unsupported dtype code
-    assert "dtype" in _err(lib.dmuon_muon_step_group(p, 7, p, p, 1, 512, 1024, 1, 0.02, 0.95, 0.0,
-                                                     1, 1, coeff, 5, 1e-7, p, 1 << 40, 0, None))
+    assert "dtype" in _err(lib.dmuon_muon_step_group(p, 7, p, p, 1, None, 0, 512, 1024, 1, 0.02,
+                                                     0.95, 0.0, 1, 1, coeff, 5, 1e-7, p, 1 << 40,
+                                                     0, None))
+    # unsupported publish dtype
+    assert "publish" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 0, p, 9, 512, 1024, 1, 0.02,
+                                                       0.95, 0.0, 1, 1, coeff, 5, 1e-7, p,
+                                                       1 << 40, 0, None))
     # no coefficients
-    assert "coefficient" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, 512, 1024, 1, 0.02,
-                                                           0.95, 0.0, 1, 1, coeff, 0, 1e-7, p,
-                                                           1 << 40, 0, None))
+    assert "coefficient" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1,
+                                                           0.02, 0.95, 0.0, 1, 1, coeff, 0, 1e-7,
+                                                           p, 1 << 40, 0, None))
     # NS group needs outputs
     assert "out_ptrs" in _err(lib.dmuon_newton_schulz_group(p, 1, None, 1, 64, 64, 1, coeff, 5,
                                                             1e-7, p, 1 << 30, 0, None))
@@ -104,5 +109,8 @@ def test_pre_and_final_validation_without_gpu():
                                                128, 1, 0.95, 1, 1, None))
     assert "nothing to write" in _err(lib.dmuon_ns_gemm_final_bf16(
         p, 256, 0, p, 256, 0, p, 256, 0, 256, 256, 1, 1.0, 1.0, None, 256, 256, 0, None, 0, None,
-        0, 1.0, 0.0, 128, None))
+        0, None, 0, 1.0, 0.0, 128, None))
+    assert "needs w_ptrs" in _err(lib.dmuon_ns_gemm_final_bf16(
+        p, 256, 0, p, 256, 0, p, 256, 0, 256, 256, 1, 1.0, 1.0, None, 256, 256, 0, p, 0, None,
+        0, p, 1, 1.0, 0.0, 128, None))
     assert lib.dmuon_muon_pre_partials(128, 256) == 8

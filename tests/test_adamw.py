@@ -191,15 +191,17 @@ def test_entry_point_validation_without_gpu():
         assert rc != 0
         return lib.dmuon_last_error().decode()
 
-    args = (1, 1, 1, 1.0, 0.9, 0.1, 0.999, 0.001, 1.0, 1e-8, -1e-3, None)
-    assert lib.dmuon_adamw_multi(q, q, q, q, q, 0, 0, *args) == 0          # empty bucket
-    assert "negative" in err(lib.dmuon_adamw_multi(q, q, q, q, q, -1, 8, *args))
-    assert "non-NULL" in err(lib.dmuon_adamw_multi(None, q, q, q, q, 1, 8, *args))
-    assert "dtype" in err(lib.dmuon_adamw_multi(q, q, q, q, q, 1, 8, 5, 1, 1, 1.0, 0.9, 0.1,
-                                                0.999, 0.001, 1.0, 1e-8, -1e-3, None))
-    assert "bias correction" in err(lib.dmuon_adamw_multi(q, q, q, q, q, 1, 8, 1, 1, 1, 1.0, 0.9,
-                                                          0.1, 0.999, 0.001, 0.0, 1e-8, -1e-3,
-                                                          None))
+    args = (1, 1, 0, 1, 1.0, 0.9, 0.1, 0.999, 0.001, 1.0, 1e-8, -1e-3, None)
+    assert lib.dmuon_adamw_multi(q, q, q, q, None, q, 0, 0, *args) == 0     # empty bucket
+    assert "negative" in err(lib.dmuon_adamw_multi(q, q, q, q, None, q, -1, 8, *args))
+    assert "non-NULL" in err(lib.dmuon_adamw_multi(None, q, q, q, None, q, 1, 8, *args))
+    assert "dtype" in err(lib.dmuon_adamw_multi(q, q, q, q, None, q, 1, 8, 5, 1, 0, 1, 1.0, 0.9,
+                                                0.1, 0.999, 0.001, 1.0, 1e-8, -1e-3, None))
+    assert "publish" in err(lib.dmuon_adamw_multi(q, q, q, q, q, q, 1, 8, 1, 1, 7, 1, 1.0, 0.9,
+                                                  0.1, 0.999, 0.001, 1.0, 1e-8, -1e-3, None))
+    assert "bias correction" in err(lib.dmuon_adamw_multi(q, q, q, q, None, q, 1, 8, 1, 1, 0, 1,
+                                                          1.0, 0.9, 0.1, 0.999, 0.001, 0.0, 1e-8,
+                                                          -1e-3, None))
 
 
 # --------------------------------------------------------------------------- kernel (GPU)

@@ -38,9 +38,12 @@ def _grads(model, seed):
     return gs
 
 
-def _setup(shapes, dtype, gpu, **kw):
+BF16_MASTER = {"defaults": {"master_dtype": torch.bfloat16}}   # W updated in place in bf16
+
+
+def _setup(shapes, dtype, gpu, policy=None, **kw):
     m = Mats(shapes, dtype, gpu)
-    dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2)
+    dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2, param_policy=policy)
     dmuon.replicate(m)
     ns = dmuon.NewtonSchulz("direct", coefficients=dmuon.KELLER_COEFFICIENTS)
     opt = dmuon.Muon(m, ns_backend=ns, **kw)
@@ -95,7 +98,8 @@ def test_multi_step_momentum_and_update(gpu):
     [(176, 256)] * 8 + [(256, 176)] * 8,                                    # c4 MoE batch / 8
 ])
 def test_bf16_weights_shape_sets(gpu, shapes):
-    m, opt = _setup(shapes, torch.bfloat16, gpu, lr=0.02, momentum=0.95, weight_decay=0.1)
+    m, opt = _setup(shapes, torch.bfloat16, gpu, BF16_MASTER, lr=0.02, momentum=0.95,
+                    weight_decay=0.1)
     W0 = [p.detach().float().cpu().numpy().copy() for p in m.parameters()]
     gs = _grads(m, seed=7)
     opt.step()
@@ -117,7 +121,8 @@ def test_c5_layer_full_size_bit_exact_chain(gpu):
     """One Llama-3-8B layer (q,k,v,o,gate,up,down) at full size: momentum bit-exact; the fused
     weight update equals W*decay - lr*s*U bit for bit, with U from the stand-alone NS entry."""
     lr, mu, wd = 0.02, 0.95, 0.1
-    m, opt = _setup(LLAMA_LAYER, torch.bfloat16, gpu, lr=lr, momentum=mu, weight_decay=wd)
+    m, opt = _setup(LLAMA_LAYER, torch.bfloat16, gpu, BF16_MASTER, lr=lr, momentum=mu,
+                    weight_decay=wd)
     ps = list(m.parameters())
     dps = dmuon.get_owned_params(m)
     # step 1 establishes the momentum buffers
@@ -144,3 +149,81 @@ def test_c5_layer_full_size_bit_exact_chain(gpu):
             w1 = (W1[i].float() * decay).to(torch.bfloat16).float()
             exp = (w1 + (-lrs) * u).to(torch.bfloat16)
             assert torch.equal(ps[i].detach(), exp), shape
+
+
+# ------------------------------------------------- fp32 master + fused publish (default policy)
+@pytest.mark.parametrize("shapes", [[(256, 512), (256, 512)], [(1000, 300)], [(130, 250)]])
+def test_fp32_master_publish_matches_fp32_weights(gpu, shapes):
+    """Reference default policy on a bf16 model: the owner keeps an fp32 master
+    (_owned_data) and the forward parameter receives bf16(master) after every update. The
+    master must evolve exactly as an fp32 weight does (same kernels, same inputs) and the
+    parameter must equal its bf16 rounding, bit for bit, on vector and per-element edge paths."""
+    lr, mu, wd = 0.02, 0.95, 0.1
+    mb, optb = _setup(shapes, torch.bfloat16, gpu, None, lr=lr, momentum=mu, weight_decay=wd)
+    dps = dmuon.get_owned_params(mb)
+    for dp, p in zip(dps, mb.parameters()):
+        assert dp._owned_data.dtype == torch.float32 and p.dtype == torch.bfloat16
+        assert torch.equal(dp._owned_data, p.detach().float())
+    mf2 = Mats(shapes, torch.float32, gpu)    # fp32-weight twin starting from the same values
+    for a, b in zip(mf2.parameters(), mb.parameters()):
+        a.data.copy_(b.detach().float())
+    dmuon.dedicate_params(mf2, None, lambda n, p: p.dim() == 2)
+    dmuon.replicate(mf2)
+    optf2 = dmuon.Muon(mf2, lr=lr, momentum=mu, weight_decay=wd, ns_backend=dmuon.NewtonSchulz(
+        "direct", coefficients=dmuon.KELLER_COEFFICIENTS))
+    for step in range(2):
+        gs = _grads(mb, seed=30 + step)
+        for dpf, g in zip(dmuon.get_owned_params(mf2), gs):
+            dpf._reduced_grad = g.to(gpu)     # the same bf16 gradients, as the reduce hook hands them
+        optb.step()
+        optf2.step()
+        for dp, p, pf in zip(dps, mb.parameters(), mf2.parameters()):
+            assert torch.equal(dp._owned_data, pf.detach()), (shapes, step)
+            assert torch.equal(p.detach(), pf.detach().to(torch.bfloat16)), (shapes, step)
+
+
+def test_policy_resolution(gpu):
+    m = Mats([(64, 128), (128, 64)], torch.float32, gpu)
+    vals = [p.detach().clone() for p in m.parameters()]
+    dmuon.dedicate_params(m, None, lambda n, p: True, compute_dtype=torch.bfloat16,
+                          param_policy={"overrides": [{"contains": "ws.1",
+                                                       "set": {"master_dtype": "bf16"}}]})
+    dps = dmuon.get_owned_params(m)
+    p0, p1 = list(m.parameters())
+    assert p0.dtype == torch.bfloat16 and p1.dtype == torch.bfloat16
+    assert dps[0]._owned_data.dtype == torch.float32
+    assert torch.equal(dps[0]._owned_data, vals[0])          # the master keeps fp32 values
+    assert dps[1].publish_target() is None
+    assert dps[1]._owned_data.data_ptr() == p1.data_ptr()     # the master is the parameter
+
+
+def test_adamw_routed_master_publish(gpu):
+    from oracle import adamw_oracle as ao
+
+    class Net(nn.Module):
+        def __init__(self):
+            super().__init__()
+            gen = torch.Generator().manual_seed(4)
+            self.w = nn.Parameter((torch.randn(128, 256, generator=gen) * 0.02)
+                                  .to(torch.bfloat16).to(gpu))
+            self.norm = nn.Parameter((1 + 0.1 * torch.randn(1000, generator=gen))
+                                     .to(torch.bfloat16).to(gpu))
+
+    net = Net()
+    dmuon.dedicate_params(net, None, lambda n, p: True)        # default policy: fp32 masters
+    dmuon.replicate(net)
+    opt = dmuon.Muon(net, adamw_lr=1e-3, adamw_weight_decay=0.01)
+    dp = [d for d in dmuon.get_owned_params(net) if d.param_name == "norm"][0]
+    assert dp._owned_data.dtype == torch.float32
+    ref = (dp._owned_data.cpu().numpy().copy(), np.zeros(1000, np.float32),
+           np.zeros(1000, np.float32))
+    for step in range(1, 4):
+        gen = torch.Generator().manual_seed(60 + step)
+        gw = (torch.randn(128, 256, generator=gen) * 0.01).to(torch.bfloat16)
+        gn = (torch.randn(1000, generator=gen) * 0.01).to(torch.bfloat16)
+        net.w.grad, net.norm.grad = gw.to(gpu), gn.to(gpu)
+        opt.step()
+        ref = ao.adamw_step(ref[0], gn.float().numpy(), ref[1], ref[2], step, 1e-3,
+                            (0.9, 0.999), 0.01, 1e-8, "fp32")
+        assert np.array_equal(dp._owned_data.cpu().numpy(), ref[0]), step
+        assert torch.equal(net.norm.detach().cpu(), torch.from_numpy(ref[0]).to(torch.bfloat16))
