@@ -268,6 +268,14 @@ def main():
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
 
+    # HBM (L2-miss) bytes per NT launch: counters cannot be read from inside this process, so
+    # the figure comes from the committed rocprofv3 --pmc summary of this same workload
+    traffic = None
+    tpath = os.path.join(HERE, "profiles", "nt_mfma_traffic.json")
+    if os.path.exists(tpath) and args.layers == N_LAYERS:
+        with open(tpath) as fh:
+            traffic = json.load(fh).get("traffic_bytes_per_launch")
+
     out = {
         "metric": "Muon step ms (8B matrix set, 1 GPU); NS TFLOPS + % bf16 MFMA peak",
         "value": round(ms_per_step, 3),
@@ -294,7 +302,7 @@ def main():
             "kernel": "nt_mfma_kernel (SYRK X X^T, SYRK-poly, NS GEMM, final GEMM+update)",
             "bound": "mfma", "achieved": round(achieved_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved_tf / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "avg_launch_us": round(1e3 * mf_ms / max(mf_launch, 1), 2),
             "launches_per_step": mf_launch // prof_steps,
         },

@@ -111,18 +111,24 @@ def _total_norm(tensors, eligible, table, p, device) -> torch.Tensor:
     if not tensors:
         return torch.zeros((), device=device, dtype=torch.float32)
     eid = {id(t) for t in eligible}
-    norms = []
+    parts = []
     if table is not None:
         sq = torch.zeros(len(eligible), device=device, dtype=torch.float32)
         table.sumsq(sq)
-        # per-tensor norms in each gradient's dtype, as torch._foreach_norm returns them
-        for i, t in enumerate(eligible):
-            norms.append(torch.sqrt(sq[i]).to(t.dtype))
-    for t in tensors:
-        if table is None or id(t) not in eid:
-            norms.append(torch.linalg.vector_norm(t.detach(), p))
-    local = torch.linalg.vector_norm(
-        torch.stack([n.to(device=device, dtype=torch.float32) for n in norms]), p)
+        # per-tensor norms rounded to each gradient's dtype, as torch._foreach_norm returns them
+        # (one rounding op per dtype present, not one per tensor)
+        norms = torch.sqrt(sq)
+        dts = [t.dtype for t in eligible]
+        for dt in set(dts):
+            if dt != torch.float32:
+                idx = torch.tensor([i for i, d in enumerate(dts) if d == dt], device=device)
+                norms[idx] = norms[idx].to(dt).float()
+        parts.append(norms)
+    others = [torch.linalg.vector_norm(t.detach(), p).to(device=device, dtype=torch.float32)
+              for t in tensors if table is None or id(t) not in eid]
+    if others:
+        parts.append(torch.stack(others))
+    local = torch.linalg.vector_norm(torch.cat(parts), p)
     if p == float("inf"):
         _all_reduce_if_needed(local, op=dist.ReduceOp.MAX)
         return local
