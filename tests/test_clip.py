@@ -80,6 +80,24 @@ def test_oracle_planted_mistakes_fail():
     assert co.clip_buckets([[np.array([0.0, 1.0], np.float32)]], [["fp32"]], 6.0)[1][0] == 1.0
 
 
+def test_oracle_global_norm_matches_reference_foreach_norm():
+    # grad_clip.py:296-321 on CPU tensors: per-tensor torch._foreach_norm (returned in each
+    # grad's dtype), grouped by dtype, then the 2-norm of the stacked fp32 values
+    gen = torch.Generator().manual_seed(2)
+    ts = [torch.randn(1000, generator=gen), (torch.randn(4097, generator=gen) * 3).to(torch.bfloat16),
+          torch.randn(64, 33, generator=gen).to(torch.bfloat16), torch.randn(7, generator=gen)]
+    norms = []
+    for dt in (torch.float32, torch.bfloat16):
+        group = [t for t in ts if t.dtype == dt]
+        norms.extend(torch._foreach_norm(group, 2.0))
+    ref = float(torch.linalg.vector_norm(torch.stack([n.float() for n in norms]), 2.0))
+    got = co.global_norm_p2([_np(t) for t in ts], [_DTS[t.dtype] for t in ts])
+    assert got == pytest.approx(ref, rel=1e-6)
+    # without the per-tensor rounding the bf16 tensors' norms would differ visibly
+    exact = float(np.sqrt(sum(float(np.sum(_np(t).astype(np.float64) ** 2)) for t in ts)))
+    assert exact != pytest.approx(ref, rel=1e-6)
+
+
 # --------------------------------------------------------------- reference CPU semantics
 def test_chunk_size_defaults_and_env_override(monkeypatch):
     monkeypatch.delenv("DMUON_FAST_CLIP_CHUNK_SIZE", raising=False)
