@@ -18,6 +18,10 @@ DTYPE_BF16 = 1
 
 c_int, c_i64, c_f, c_d, c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
 c_fp = ctypes.POINTER(ctypes.c_float)
+c_ip = ctypes.POINTER(ctypes.c_int)
+
+NS_DIRECT = 0
+NS_GRAM = 1
 
 # name -> (restype, argtypes); mirrors include/dmuon_amd.h
 _SIGNATURES = {
@@ -40,13 +44,14 @@ _SIGNATURES = {
                                c_int, c_int, c_int, c_int, c_int, c_f, c_int, c_int, c_vp]),
     "dmuon_norm_finalize": (c_int, [c_vp, c_int, c_int, c_f, c_vp, c_vp, c_vp]),
     "dmuon_muon_update": (c_int, [c_vp, c_int, c_vp, c_int, c_i64, c_int, c_f, c_f, c_vp]),
-    "dmuon_ns_plan": (c_int, [c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int),
+    "dmuon_ns_plan": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int),
                               ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_i64)]),
     "dmuon_muon_step_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_vp, c_int, c_int, c_int,
-                                      c_int, c_d, c_d, c_d, c_int, c_int, c_fp, c_int, c_f, c_vp,
-                                      c_i64, c_int, c_vp]),
+                                      c_int, c_d, c_d, c_d, c_int, c_int, c_fp, c_int, c_int, c_ip,
+                                      c_int, c_f, c_vp, c_i64, c_int, c_vp]),
     "dmuon_newton_schulz_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_fp,
-                                          c_int, c_f, c_vp, c_i64, c_int, c_vp]),
+                                          c_int, c_int, c_ip, c_int, c_f, c_vp, c_i64, c_int,
+                                          c_vp]),
     "dmuon_adamw_multi": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_int, c_int,
                                   c_int, c_int, c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_vp]),
     "dmuon_segmented_l2_norm_sq": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp,
@@ -108,9 +113,16 @@ def profile_collect() -> dict:
             for i, name in enumerate(PROFILE_CLASSES)}
 
 
-def plan(rows: int, cols: int, batch: int, tile: int = 0, num_cus: int = 0):
+def plan(rows: int, cols: int, batch: int, tile: int = 0, num_cus: int = 0,
+         backend: int = NS_DIRECT):
     """(tile, m_pad, n_pad, workspace_bytes) for a group of same-shape matrices."""
     t, mp, np_, ws = c_int(), c_int(), c_int(), c_i64()
-    check(lib().dmuon_ns_plan(rows, cols, batch, tile, num_cus, ctypes.byref(t), ctypes.byref(mp),
-                              ctypes.byref(np_), ctypes.byref(ws)))
+    check(lib().dmuon_ns_plan(rows, cols, batch, tile, num_cus, backend, ctypes.byref(t),
+                              ctypes.byref(mp), ctypes.byref(np_), ctypes.byref(ws)))
     return t.value, mp.value, np_.value, ws.value
+
+
+def restart_array(restarts) -> tuple:
+    """(ctypes int array or None, count) for a restart-iteration list."""
+    r = [int(i) for i in restarts]
+    return ((c_int * len(r))(*r) if r else None), len(r)

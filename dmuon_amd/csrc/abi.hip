@@ -39,15 +39,20 @@ bool stride_ok(int64_t s, int batch) { return batch <= 1 || (s >= 0 && (s % 8) =
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 int64_t align256(int64_t b) { return round_up(b, 256); }
 
+// Power-of-two scale of the fp16 Gram-NS operand X (entries of the normalised X are at most 1)
+constexpr float kGramKx = 4096.f;
+
 struct Workspace {
   uint16_t *X, *XT0, *XT1, *Am, *Pm;
+  // Gram backend only: the accumulated polynomial Q and its transpose (ping-pong), P R
+  uint16_t *Q0, *Q1, *Q0T, *Q1T, *Wm;
   float *partials, *scale, *scale_sq;
   int nparts;
   int64_t bytes;
 };
 
 // Carves the workspace of a group; base == nullptr only computes the size.
-Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch) {
+Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch, int gram) {
   Workspace w{};
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
@@ -63,6 +68,13 @@ Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch) {
   w.XT1 = reinterpret_cast<uint16_t*>(take(L * xs));
   w.Am = reinterpret_cast<uint16_t*>(take(L * as));
   w.Pm = reinterpret_cast<uint16_t*>(take(L * as));
+  if (gram) {
+    w.Q0 = reinterpret_cast<uint16_t*>(take(L * as));
+    w.Q1 = reinterpret_cast<uint16_t*>(take(L * as));
+    w.Q0T = reinterpret_cast<uint16_t*>(take(L * as));
+    w.Q1T = reinterpret_cast<uint16_t*>(take(L * as));
+    w.Wm = reinterpret_cast<uint16_t*>(take(L * as));
+  }
   w.nparts = pre_blocks_per_mat(Rp, Cp);
   w.partials = reinterpret_cast<float*>(take(L * w.nparts * 4));
   w.scale = reinterpret_cast<float*>(take(L * 4));
@@ -116,8 +128,8 @@ int tri_tiles(int m_pad, int tile) {
   return mt * (mt + 1) / 2;
 }
 
-int plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, int* m_pad,
-         int* n_pad, int64_t* bytes) {
+int plan(int rows, int cols, int batch, int tile_req, int num_cus, int gram, int* tile,
+         int* m_pad, int* n_pad, int64_t* bytes) {
   if (rows <= 0 || cols <= 0 || batch <= 0)
     return fail("dmuon_ns_plan: rows, cols and batch must be positive (got %d, %d, %d)", rows,
                 cols, batch);
@@ -136,7 +148,7 @@ int plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, in
   const int mp = (int)round_up(m, t), np = (int)round_up(n, t);
   const bool tall = rows > cols;
   const int Rp = tall ? np : mp, Cp = tall ? mp : np;
-  Workspace w = carve(nullptr, mp, np, Rp, Cp, batch);
+  Workspace w = carve(nullptr, mp, np, Rp, Cp, batch, gram);
   *tile = t;
   *m_pad = mp;
   *n_pad = np;
@@ -144,13 +156,166 @@ int plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, in
   return 0;
 }
 
+// Gram-space NS (the reference's gram_newton_schulz, newton_schulz.py:333-448) on the fp16 NT
+// kernels, for X (m x n, m <= n) staged as fp16(KX * ns_in / ||ns_in||). With R = X X^T and
+// Z_i = c_i R^2 + b_i R, one NS step maps X to P_i X, P_i = Z_i + a_i I, so per step
+//   Q <- P_i Q  (Q = P_i after a start or restart), the accumulated polynomial: Z Q^T + a Q
+//   R <- P_i R P_i  when the next step is neither the last nor a restart:
+//        W = Z R + a R  (full product: P R is not symmetric once rounded), R = W Z + a W
+//   restart at step i: X <- Q X, R = X X^T, Q reset;   finally U = Q X / KX
+// The reference writes the R update as (R P) P on triangle tiles; the congruence P (R P) keeps R
+// the Gram matrix of P X to rounding (positive semi-definite), which in fp16 emulation roughly
+// halves the error against the exact polar-factor polynomial. fp16 as in the reference (bf16
+// loses the small eigenvalues of R). Power-of-two scales keep every operand normal in fp16:
+// X carries KX = 2^12 throughout, the first R (eigenvalues ~1/m) carries kr = 2^floor(log2 m)
+// (at most 2^12) until its first update; all scale changes are folded into alpha / beta.
+int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, int batch, bool tall,
+             const float* coeffs, int T, const int* restarts, int n_restarts,
+             void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype,
+             void* const* out_ptrs, int out_dtype, float decay, float lrs, double syrk_flops,
+             double tri_sq_flops, double gemm_flops, double final_bytes, hipStream_t stream,
+             const char* who) {
+  const long long xs = (long long)m_pad * n_pad, as = (long long)m_pad * m_pad;
+  const double full_sq_flops = 2.0 * batch * (double)m * m * m;
+  auto is_restart = [&](int it) {
+    for (int r = 0; r < n_restarts; ++r)
+      if (restarts[r] == it) return true;
+    return false;
+  };
+  // D = alpha * A B^T + beta * C + diag * I, m x m; tri: upper tiles mirrored (symmetric result)
+  auto sq = [&](const uint16_t* A, const uint16_t* B, const uint16_t* C, uint16_t* D, float alpha,
+                float beta, float diag, bool tri) -> int {
+    NtArgs s{};
+    s.elt = ELT_F16;
+    s.A = A; s.lda = m_pad; s.sA = as;
+    s.B = B; s.ldb = m_pad; s.sB = as;
+    s.M = m_pad; s.N = m_pad; s.K = m_pad; s.L = batch;
+    s.mt = s.nt = m_pad / tile;
+    s.tiles_per_mat = tri ? tri_tiles(m_pad, tile) : s.mt * s.nt; s.tri = tri ? 1 : 0;
+    s.sym_exact = 1;
+    s.mode = EPI_SYM; s.alpha = alpha; s.beta = C ? beta : 0.f; s.diag = diag;
+    s.C = C; s.ldc = m_pad; s.sC = as;
+    s.D = D; s.ldd = m_pad; s.sD = as;
+    return timed(PC_POLY, tri ? tri_sq_flops : full_sq_flops, 0.0, stream, who,
+                 [&] { return launch_nt(s, tile, stream); });
+  };
+  // R = alpha X X^T
+  auto gram_of_x = [&](uint16_t* R, float alpha) -> int {
+    NtArgs s{};
+    s.elt = ELT_F16;
+    s.A = w.X; s.lda = n_pad; s.sA = xs;
+    s.B = w.X; s.ldb = n_pad; s.sB = xs;
+    s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch;
+    s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
+    s.sym_exact = 1;
+    s.mode = EPI_SYM; s.alpha = alpha;
+    s.D = R; s.ldd = m_pad; s.sD = as;
+    return timed(PC_SYRK, syrk_flops, 0.0, stream, who, [&] { return launch_nt(s, tile, stream); });
+  };
+  uint16_t* xt_cur = w.XT0;
+  uint16_t* xt_nxt = w.XT1;
+  // X <- Q X (an NS restart), or the final U = Q X / KX with the Muon update in the epilogue
+  auto qx = [&](const uint16_t* Q, bool last) -> int {
+    NtArgs g{};
+    g.elt = ELT_F16;
+    g.A = Q; g.lda = m_pad; g.sA = as;
+    g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
+    g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch;
+    g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
+    g.beta = 0.f;
+    if (!last) {
+      g.alpha = 1.f;
+      g.mode = EPI_NS;
+      g.D = w.X; g.ldd = n_pad; g.sD = xs;
+      g.DT = xt_nxt; g.lddt = m_pad; g.sDT = xs;
+      if (timed(PC_GEMM, gemm_flops, 0.0, stream, who, [&] { return launch_nt(g, tile, stream); }))
+        return 1;
+      uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
+      return 0;
+    }
+    g.alpha = 1.f / kGramKx;
+    g.mode = EPI_FINAL;
+    g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;
+    g.w_ptrs = w_ptrs; g.w_dtype = w_dtype; g.decay = decay; g.lrs = lrs;
+    g.pub_ptrs = pub_ptrs; g.pub_dtype = pub_dtype;
+    g.m_real = m; g.n_real = n; g.transposed = tall ? 1 : 0;
+    return timed(PC_FINAL, gemm_flops, final_bytes, stream, who,
+                 [&] { return launch_nt(g, tile, stream); });
+  };
+  // Q <- P Q = Z Q + a Q as a full product (Q is a product of polynomials that no longer
+  // commute once rounded; its factor order must match R's), written with its transpose: the
+  // next update reads Q^T as the B operand. A Q that is still P itself is symmetric, so its
+  // transpose slot holds the same matrix.
+  uint16_t* qbuf[2] = {w.Q0, w.Q1};
+  const uint16_t* qtbuf[2] = {w.Q0, w.Q1};   // where the transpose of each slot's Q lives
+  auto q_update = [&](const uint16_t* Zm, int from, float a_) -> int {
+    const int to = 1 - from;
+    qtbuf[to] = to ? w.Q1T : w.Q0T;
+    NtArgs g{};
+    g.elt = ELT_F16;
+    g.A = Zm; g.lda = m_pad; g.sA = as;
+    g.B = qtbuf[from]; g.ldb = m_pad; g.sB = as;
+    g.M = m_pad; g.N = m_pad; g.K = m_pad; g.L = batch;
+    g.mt = g.nt = m_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
+    g.mode = EPI_NS; g.alpha = 1.f; g.beta = a_;
+    g.C = qbuf[from]; g.ldc = m_pad; g.sC = as;
+    g.D = qbuf[to]; g.ldd = m_pad; g.sD = as;
+    g.DT = const_cast<uint16_t*>(qtbuf[to]); g.lddt = m_pad; g.sDT = as;
+    return timed(PC_POLY, full_sq_flops, 0.0, stream, who,
+                 [&] { return launch_nt(g, tile, stream); });
+  };
+  int kr = 1;
+  while (kr * 2 <= m && kr < 4096) kr *= 2;
+  uint16_t* R = w.Am;
+  uint16_t* Z = w.Pm;
+  uint16_t* W = w.Wm;
+  int qs = -1;               // slot of the current Q, -1: none since the last (re)start
+  float rs = (float)kr;      // the stored R is rs * (X X^T of the normalised X)
+  if (gram_of_x(R, rs / (kGramKx * kGramKx))) return 1;
+  for (int it = 0; it < T; ++it) {
+    if (it != 0 && is_restart(it) && qs >= 0) {
+      if (qx(qbuf[qs], false)) return 1;
+      rs = 1.f;
+      if (gram_of_x(R, 1.f / (kGramKx * kGramKx))) return 1;
+      qs = -1;
+    }
+    const float ca = coeffs[3 * it], cb = coeffs[3 * it + 1], cc = coeffs[3 * it + 2];
+    const bool evolve = it + 1 < T && !is_restart(it + 1);
+    const float zr2 = cc / (rs * rs), zr1 = cb / rs;
+    if (qs < 0 && !evolve) {
+      // Q = Z + a I in one product (Z itself is not needed); symmetric, its own transpose
+      if (sq(R, R, R, qbuf[0], zr2, zr1, ca, true)) return 1;
+      qtbuf[0] = qbuf[0];
+      qs = 0;
+      continue;
+    }
+    if (sq(R, R, R, Z, zr2, zr1, 0.f, true)) return 1;   // Z = c R^2 + b R
+    if (qs < 0) {
+      if (timed(PC_POLY, 0.0, 4.0 * batch * (double)m_pad * m_pad, stream, who,
+                [&] { return launch_diag_copy(Z, qbuf[0], m_pad, batch, ca, stream); }))
+        return 1;
+      qtbuf[0] = qbuf[0];
+      qs = 0;
+    } else {
+      if (q_update(Z, qs, ca)) return 1;   // Q <- Z Q + a Q
+      qs = 1 - qs;
+    }
+    if (evolve) {
+      if (sq(Z, R, R, W, 1.f, ca, 0.f, false)) return 1;              // rs * (P R)
+      if (sq(W, Z, W, R, 1.f / rs, ca / rs, 0.f, true)) return 1;     // P R P
+      rs = 1.f;
+    }
+  }
+  return qx(qbuf[qs], true);
+}
+
 // The whole Newton-Schulz + optional update sequence of one group; see dmuon_muon_step_group.
 int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* const* w_ptrs,
               int w_dtype, void* const* pub_ptrs, int pub_dtype, void* const* out_ptrs,
               int out_dtype, int rows, int cols, int batch,
               float mu, int nesterov, int first_step, float decay, float lrs, const float* coeffs,
-              int T, float eps, void* workspace, int64_t workspace_bytes, int tile_req,
-              hipStream_t stream, const char* who) {
+              int T, int backend, const int* restarts, int n_restarts, float eps, void* workspace,
+              int64_t workspace_bytes, int tile_req, hipStream_t stream, const char* who) {
   if (!g_ptrs) return fail("%s: g_ptrs is NULL", who);
   if (g_dtype != DMUON_DTYPE_F32 && g_dtype != DMUON_DTYPE_BF16)
     return fail("%s: unsupported gradient dtype code %d", who, g_dtype);
@@ -162,17 +327,22 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
   if (pub_ptrs && pub_dtype != DMUON_DTYPE_F32 && pub_dtype != DMUON_DTYPE_BF16)
     return fail("%s: unsupported publish dtype code %d", who, pub_dtype);
   if (!coeffs || T <= 0) return fail("%s: need at least one (a, b, c) coefficient triple", who);
+  if (backend != DMUON_NS_DIRECT && backend != DMUON_NS_GRAM)
+    return fail("%s: unknown NS backend %d", who, backend);
+  if (n_restarts < 0 || (n_restarts > 0 && !restarts))
+    return fail("%s: restart list NULL or of negative length", who);
+  const int gram = backend == DMUON_NS_GRAM;
   if (!workspace || !aligned16(workspace)) return fail("%s: workspace NULL or misaligned", who);
   int tile, m_pad, n_pad;
   int64_t need;
-  if (plan(rows, cols, batch, tile_req, 0, &tile, &m_pad, &n_pad, &need)) return 1;
+  if (plan(rows, cols, batch, tile_req, 0, gram, &tile, &m_pad, &n_pad, &need)) return 1;
   if (workspace_bytes < need)
     return fail("%s: workspace of %lld bytes is smaller than the %lld bytes planned", who,
                 (long long)workspace_bytes, (long long)need);
   const bool tall = rows > cols;
   const int m = tall ? cols : rows, n = tall ? rows : cols;
   const int Rp = tall ? n_pad : m_pad, Cp = tall ? m_pad : n_pad;
-  Workspace w = carve(static_cast<char*>(workspace), m_pad, n_pad, Rp, Cp, batch);
+  Workspace w = carve(static_cast<char*>(workspace), m_pad, n_pad, Rp, Cp, batch, gram);
   const long long xs = (long long)m_pad * n_pad, as = (long long)m_pad * m_pad;
 
   PreArgs p{};
@@ -194,16 +364,27 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
   p.mu = mu;
   p.first_step = first_step;
   p.nesterov = nesterov;
+  p.stage = gram ? PRE_NORM : PRE_BF16;
   const double Ld = batch, md = m, nd = n, elems = (double)rows * cols * batch;
   const double gbytes = g_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0;
   // algorithmic bytes: gradient read, fp32 momentum read (not on the first step) and write,
-  // one bf16 copy of ns_in
-  const double pre_bytes = elems * (gbytes + (buf_ptrs ? (first_step ? 4.0 : 8.0) : 0.0) + 2.0);
+  // one 16-bit copy of ns_in (direct); the Gram staging has no copy in its first pass and
+  // reads the gradient and the new momentum again in the second
+  const double mom_bytes = buf_ptrs ? (first_step ? 4.0 : 8.0) : 0.0;
+  const double pre_bytes = elems * (gbytes + mom_bytes + (gram ? 0.0 : 2.0));
   if (timed(PC_PRE, 0.0, pre_bytes, stream, who, [&] { return launch_pre(p, stream); })) return 1;
   if (timed(PC_NORM, 0.0, (double)batch * w.nparts * 4, stream, who, [&] {
         return launch_norm_finalize(w.partials, w.nparts, batch, eps, w.scale, w.scale_sq, stream);
       }))
     return 1;
+  if (gram) {
+    p.stage = PRE_F16;
+    p.scale = w.scale;
+    p.kx = kGramKx;
+    const double st_bytes = elems * (gbytes + (buf_ptrs ? 4.0 : 0.0) + 2.0);
+    if (timed(PC_PRE, 0.0, st_bytes, stream, who, [&] { return launch_pre(p, stream); }))
+      return 1;
+  }
   const double syrk_flops = Ld * md * (md + 1) * nd, poly_flops = Ld * md * (md + 1) * md;
   const double gemm_flops = 2.0 * Ld * md * md * nd;
   const double wbytes = w_ptrs ? 2.0 * elems * (w_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0) : 0.0;
@@ -212,6 +393,10 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
 
   uint16_t* xt_cur = w.XT0;
   uint16_t* xt_nxt = w.XT1;
+  if (gram)
+    return run_gram(w, m, n, m_pad, n_pad, tile, batch, tall, coeffs, T, restarts, n_restarts,
+                    w_ptrs, w_dtype, pub_ptrs, pub_dtype, out_ptrs, out_dtype, decay, lrs,
+                    syrk_flops, poly_flops, gemm_flops, wbytes + obytes + pbytes, stream, who);
   for (int it = 0; it < T; ++it) {
     const float ca = coeffs[3 * it], cb = coeffs[3 * it + 1], cc = coeffs[3 * it + 2];
     // A = s^2 X X^T (s only on the first step: X holds the un-normalised ns_in)
@@ -302,7 +487,7 @@ int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* 
   return rc;
 }
 
-int dmuon_abi_version(void) { return 101; }
+int dmuon_abi_version(void) { return 102; }
 
 int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
                     int64_t strideB, const void* C, int64_t ldc, int64_t strideC, void* D,
@@ -543,17 +728,21 @@ int dmuon_segmented_scale(const int64_t* ptrs, const int64_t* numels, const int3
   return timed(PC_CLIP, 0.0, 0.0, st, who, [&] { return launch_clip_scale(a, st); });
 }
 
-int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, int* m_pad,
-                  int* n_pad, int64_t* workspace_bytes) {
+int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int backend,
+                  int* tile, int* m_pad, int* n_pad, int64_t* workspace_bytes) {
   if (!tile || !m_pad || !n_pad || !workspace_bytes) return fail("dmuon_ns_plan: NULL output");
-  return plan(rows, cols, batch, tile_req, num_cus, tile, m_pad, n_pad, workspace_bytes);
+  if (backend != DMUON_NS_DIRECT && backend != DMUON_NS_GRAM)
+    return fail("dmuon_ns_plan: unknown NS backend %d", backend);
+  return plan(rows, cols, batch, tile_req, num_cus, backend == DMUON_NS_GRAM, tile, m_pad, n_pad,
+              workspace_bytes);
 }
 
 int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
                           void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype,
                           int rows, int cols, int batch, double lr, double mu, double wd,
-                          int nesterov, int first_step, const float* coeffs, int T, float eps,
-                          void* workspace, int64_t workspace_bytes, int tile, void* stream) {
+                          int nesterov, int first_step, const float* coeffs, int T, int backend,
+                          const int* restarts, int n_restarts, float eps, void* workspace,
+                          int64_t workspace_bytes, int tile, void* stream) {
   const char* who = "dmuon_muon_step_group";
   if (batch == 0) return 0;
   if (!buf_ptrs || !w_ptrs) return fail("%s: buf_ptrs and w_ptrs must be non-NULL", who);
@@ -562,19 +751,21 @@ int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_pt
   const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
   const float lrs = (float)(lr * scale);
   return run_group(g_ptrs, g_dtype, buf_ptrs, w_ptrs, w_dtype, pub_ptrs, pub_dtype, nullptr, 0,
-                   rows, cols, batch, (float)mu, nesterov, first_step, decay, lrs, coeffs, T, eps,
-                   workspace, workspace_bytes, tile, static_cast<hipStream_t>(stream), who);
+                   rows, cols, batch, (float)mu, nesterov, first_step, decay, lrs, coeffs, T,
+                   backend, restarts, n_restarts, eps, workspace, workspace_bytes, tile,
+                   static_cast<hipStream_t>(stream), who);
 }
 
 int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,
                               int out_dtype, int rows, int cols, int batch, const float* coeffs,
-                              int T, float eps, void* workspace, int64_t workspace_bytes, int tile,
-                              void* stream) {
+                              int T, int backend, const int* restarts, int n_restarts, float eps,
+                              void* workspace, int64_t workspace_bytes, int tile, void* stream) {
   const char* who = "dmuon_newton_schulz_group";
   if (batch == 0) return 0;
   if (!out_ptrs) return fail("%s: out_ptrs must be non-NULL", who);
   return run_group(g_ptrs, g_dtype, nullptr, nullptr, 0, nullptr, 0, out_ptrs, out_dtype, rows,
-                   cols, batch, 0.f, 0, 1, 1.f, 0.f, coeffs, T, eps, workspace, workspace_bytes, tile,
+                   cols, batch, 0.f, 0, 1, 1.f, 0.f, coeffs, T, backend, restarts, n_restarts,
+                   eps, workspace, workspace_bytes, tile,
                    static_cast<hipStream_t>(stream), who);
 }
 

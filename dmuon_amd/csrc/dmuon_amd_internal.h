@@ -16,38 +16,56 @@ enum DType : int { DT_F32 = 0, DT_BF16 = 1 };
 //   EPI_FINAL U = s*(acc + beta*C) -> out[] and/or W <- W*decay - lrs*U, original orientation
 enum EpiMode : int { EPI_SYM = 0, EPI_NS = 1, EPI_FINAL = 2 };
 
+// 16-bit element type of the NT product operands, addend and outputs
+enum { ELT_BF16 = 0, ELT_F16 = 1 };
+
 struct NtArgs {
-  const uint16_t* A; long long lda, sA;   // bf16 [L][M][K], row stride lda, batch stride sA
-  const uint16_t* B; long long ldb, sB;   // bf16 [L][N][K]
+  const uint16_t* A; long long lda, sA;   // elt [L][M][K], row stride lda, batch stride sA
+  const uint16_t* B; long long ldb, sB;   // elt [L][N][K]
   int M, N, K, L;                         // multiples of the tile sizes (host pads)
   int mt, nt, tiles_per_mat, tri;         // tile grid; tri: upper-triangle tiles of an MxM result
   int mode;
   float alpha, beta, diag;
   const float* alpha_dev;                 // optional per-matrix multiplier of alpha
-  const uint16_t* C; long long ldc, sC;   // optional bf16 [L][M][N] addend
-  uint16_t* D; long long ldd, sD;         // bf16 [L][M][N]
-  uint16_t* DT; long long lddt, sDT;      // bf16 [L][N][M] (EPI_NS, optional)
+  const uint16_t* C; long long ldc, sC;   // optional elt [L][M][N] addend
+  uint16_t* D; long long ldd, sD;         // elt [L][M][N]
+  uint16_t* DT; long long lddt, sDT;      // elt [L][N][M] (EPI_NS, optional)
   void* const* out_ptrs; int out_dtype;   // EPI_FINAL: per-matrix U outputs (original shape)
   void* const* w_ptrs; int w_dtype;       // EPI_FINAL: per-matrix weights updated in place
   void* const* pub_ptrs; int pub_dtype;   // EPI_FINAL: optional forward copies of the new W
   float decay, lrs;                       // W <- round(W*decay) - lrs*U   (decay==1: no decay rounding)
   int m_real, n_real, transposed;         // true NS dims; transposed: original = X^T (n_real x m_real)
+  int elt;                                // ELT_BF16 / ELT_F16 (A, B, C, D, DT)
+  int sym_exact;                          // EPI_SYM + tri: diagonal tiles stored exactly symmetric
 };
 
 // Launches the NT MFMA kernel; picks the tile configuration from args (tile = 256 or 128).
 hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream);
 
+// What one launch of the pre kernel does:
+//   PRE_BF16  momentum update, bf16 ns_in into Y / YT, norm partials (direct NS staging)
+//   PRE_NORM  momentum update and norm partials only
+//   PRE_F16   after PRE_NORM + norm finalise: recompute ns_in from g and the updated buffer
+//             and write fp16(kx * scale * ns_in) into Y / YT (Gram NS staging); no buffer write
+enum { PRE_BF16 = 0, PRE_NORM = 1, PRE_F16 = 2 };
+
 struct PreArgs {
   void* const* g_ptrs; int g_dtype;       // per-matrix gradient (rows x cols, row-major)
   float* const* buf_ptrs;                 // per-matrix fp32 momentum buffer (rows x cols)
-  uint16_t* Y; long long ldy, sY;         // bf16 ns_in in the gradient's layout, padded [L][Rp][Cp]
-  uint16_t* YT; long long ldyt, sYT;      // bf16 ns_in transposed, padded [L][Cp][Rp]
+  uint16_t* Y; long long ldy, sY;         // 16-bit ns_in in the gradient's layout, padded [L][Rp][Cp]
+  uint16_t* YT; long long ldyt, sYT;      // 16-bit ns_in transposed, padded [L][Cp][Rp]
   float* partials;                        // [L][blocks_per_mat] sum of squares of ns_in
   int rows, cols, Rp, Cp, L;
   float mu; int first_step, nesterov;
+  int stage;                              // PRE_*
+  const float* scale; float kx;           // PRE_F16: per-matrix 1/(||ns_in|| + eps), power of 2
 };
 hipError_t launch_pre(const PreArgs& a, hipStream_t stream);
 int pre_blocks_per_mat(int Rp, int Cp);
+
+// Gram NS: Q = Z + diag * I over L matrices of m x m fp16 (ld m), Z the polynomial part
+hipError_t launch_diag_copy(const uint16_t* Z, uint16_t* Q, int m, int L, float diag,
+                            hipStream_t stream);
 
 // scale[l] = 1/(sqrt(sum partials[l]) + eps), scale_sq[l] = scale^2
 hipError_t launch_norm_finalize(const float* partials, int nparts, int L, float eps,

@@ -4,8 +4,14 @@
 //           writes bf16(ns_in) twice -- in the gradient's own layout and transposed (LDS-tiled
 //           64x64 transpose) -- into zero-padded NS operands, plus per-block partial sums of
 //           ns_in^2 for the Frobenius norm. One pass: 2 (g) + 4 + 4 (buf) + 2 + 2 (copies) B/elt.
+//           The Gram NS stages in two passes instead: PRE_NORM (momentum + partials), then,
+//           once the norm is known, PRE_F16 recomputes ns_in and writes fp16(kx * ns_in / norm)
+//           (fp16 cannot hold an un-normalised gradient safely). 2+4+4, then 2+4+2+2 B/elt.
 //  finalize scale = 1/(||ns_in||_F + eps) per matrix, fixed-order (deterministic) reduction.
+//  diag     Q = Z + a I for the Gram iteration's first polynomial after a (re)start.
 //  update   W <- W*(1 - lr*wd) - lr*scale*U   for callers holding a materialised U.
+#include <algorithm>
+
 #include "dmuon_amd_internal.h"
 
 namespace dmuon {
@@ -32,6 +38,14 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+template <int ST>
 __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t tileT[kTile][kTile + kPad];
   __shared__ float red[4];
@@ -47,6 +61,9 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
   uint16_t* YT = a.YT + (long long)l * a.sYT;
   const float mu = a.mu;
   const bool vec = (a.cols & 3) == 0;
+  // PRE_F16 reads the buffer PRE_NORM left (the new momentum) and only recomputes ns_in
+  const bool read_buf = buf && (ST == PRE_F16 || !a.first_step);
+  const float sc = ST == PRE_F16 ? a.scale[l] * a.kx : 1.f;
 
   float ss = 0.f;
 #pragma unroll
@@ -68,7 +85,7 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
         gv[0] = bf2f(t.x & 0xffff); gv[1] = bf2f(t.x >> 16);
         gv[2] = bf2f(t.y & 0xffff); gv[3] = bf2f(t.y >> 16);
       }
-      if (buf && !a.first_step) {
+      if (read_buf) {
         const float4 t = *reinterpret_cast<const float4*>(buf + base);
         bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
       }
@@ -77,7 +94,7 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
       for (int e = 0; e < 4; ++e) {
         if (in[e]) {
           gv[e] = load_any(g, a.g_dtype, base + e);
-          if (buf && !a.first_step) bv[e] = buf[base + e];
+          if (read_buf) bv[e] = buf[base + e];
         }
       }
     }
@@ -86,7 +103,8 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
     for (int e = 0; e < 4; ++e) {
       // buf.mul_(mu).add_(g): two roundings, as the reference does them
       if (buf) {
-        nb[e] = a.first_step ? gv[e] : __fadd_rn(__fmul_rn(bv[e], mu), gv[e]);
+        if constexpr (ST == PRE_F16) nb[e] = bv[e];
+        else nb[e] = a.first_step ? gv[e] : __fadd_rn(__fmul_rn(bv[e], mu), gv[e]);
         ns[e] = a.nesterov ? __fadd_rn(gv[e], __fmul_rn(mu, nb[e])) : nb[e];
       } else {
         nb[e] = gv[e];
@@ -95,7 +113,7 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
       if (!in[e]) ns[e] = 0.f;
       ss += ns[e] * ns[e];
     }
-    if (buf) {
+    if (ST != PRE_F16 && buf) {
       if (vec && in[3]) {
         *reinterpret_cast<float4*>(buf + base) = make_float4(nb[0], nb[1], nb[2], nb[3]);
       } else {
@@ -104,9 +122,10 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
           if (in[e]) buf[base + e] = nb[e];
       }
     }
+    if constexpr (ST == PRE_NORM) continue;
     uint16_t o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = f2bf(ns[e]);
+    for (int e = 0; e < 4; ++e) o[e] = ST == PRE_F16 ? f2h(__fmul_rn(ns[e], sc)) : f2bf(ns[e]);
     if (row < a.Rp) {
       uint2 p;
       p.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
@@ -116,8 +135,8 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) tileT[4 * tc + e][rl] = o[e];
   }
-  __syncthreads();
-  {
+  if constexpr (ST != PRE_NORM) {
+    __syncthreads();
     // transposed write: row cl of YT gets 64 consecutive source rows (128 B)
     const int cl = tid >> 2, seg = tid & 3;
     const int col = c0 + cl;
@@ -128,6 +147,7 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
       dst[1] = src[1];
     }
   }
+  if constexpr (ST == PRE_F16) return;
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
@@ -180,13 +200,48 @@ __global__ __launch_bounds__(256) void muon_update_kernel(const UpdateArgs a) {
   }
 }
 
+// Q = Z + diag * I, fp16, 16-byte vectors; each matrix holds m*m/8 vectors and a vector holds
+// a diagonal element iff its row's diagonal column falls inside it.
+__global__ __launch_bounds__(256) void diag_copy_kernel(const uint16_t* __restrict__ Z,
+                                                        uint16_t* __restrict__ Q, int m,
+                                                        long long n8, float diag) {
+  const long long per = (long long)m * m / 8;
+  for (long long v = (long long)blockIdx.x * 256 + threadIdx.x; v < n8;
+       v += (long long)gridDim.x * 256) {
+    uint4 t = reinterpret_cast<const uint4*>(Z)[v];
+    const long long e = (v % per) * 8;           // element index within the matrix
+    const int row = (int)(e / m), col = (int)(e % m);
+    const int d = row - col;                     // diagonal at lane d of this vector
+    if (d >= 0 && d < 8) {
+      unsigned* w = reinterpret_cast<unsigned*>(&t) + (d >> 1);
+      const unsigned h = (d & 1) ? (*w >> 16) : (*w & 0xffff);
+      const unsigned r = f2h(h2f((uint16_t)h) + diag);
+      *w = (d & 1) ? ((*w & 0xffffu) | (r << 16)) : ((*w & 0xffff0000u) | r);
+    }
+    reinterpret_cast<uint4*>(Q)[v] = t;
+  }
+}
+
 }  // namespace
 
 int pre_blocks_per_mat(int Rp, int Cp) { return (Rp / kTile) * (Cp / kTile); }
 
 hipError_t launch_pre(const PreArgs& a, hipStream_t stream) {
   dim3 grid(a.Cp / kTile, a.Rp / kTile, a.L), block(256);
-  hipLaunchKernelGGL(muon_pre_kernel, grid, block, 0, stream, a);
+  if (a.stage == PRE_NORM)
+    hipLaunchKernelGGL(muon_pre_kernel<PRE_NORM>, grid, block, 0, stream, a);
+  else if (a.stage == PRE_F16)
+    hipLaunchKernelGGL(muon_pre_kernel<PRE_F16>, grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL(muon_pre_kernel<PRE_BF16>, grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_diag_copy(const uint16_t* Z, uint16_t* Q, int m, int L, float diag,
+                            hipStream_t stream) {
+  const long long n8 = (long long)m * m / 8 * L;   // m is a multiple of 128
+  const int blocks = (int)std::min<long long>((n8 + 255) / 256, 16384);
+  hipLaunchKernelGGL(diag_copy_kernel, dim3(blocks), dim3(256), 0, stream, Z, Q, m, n8, diag);
   return hipGetLastError();
 }
 

@@ -1,4 +1,4 @@
-// NT-form bf16 MFMA product family for the Newton-Schulz iteration on gfx950 (CDNA4).
+// NT-form bf16 / fp16 MFMA product family for the Newton-Schulz iteration on gfx950 (CDNA4).
 //
 //   acc[i][j] = sum_k A[i][k] * B[j][k]          (both operands K-contiguous, row-major)
 //
@@ -10,7 +10,7 @@
 //          weight update in the original orientation (EPI_FINAL)
 //
 // Tile machine: WM x WN waves; each wave owns a (BM/WM)x(BN/WN) sub-tile made of 32x32 MFMA
-// blocks (v_mfma_f32_32x32x16_bf16, fp32 accumulate). 256x256 tiles run 8 waves (two per SIMD,
+// blocks (v_mfma_f32_32x32x16_bf16 or _f16, fp32 accumulate). 256x256 tiles run 8 waves (two per SIMD,
 // so one wave's MFMAs cover the other's LDS and barrier waits); 128x128 tiles run 4 waves with
 // two blocks per CU. K is staged through LDS in
 // BK-wide slices by direct global->LDS DMA (global_load_lds_dwordx4: each wave instruction
@@ -23,6 +23,7 @@
 #include "dmuon_amd_internal.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
@@ -36,6 +37,27 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 }
 __device__ __forceinline__ float bf2f(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Operand / intermediate element type of one kernel instance: E = ELT_BF16 or ELT_F16. The
+// product operands, the addend C and the outputs D / D^T are 16-bit words of that type; the
+// accumulators are fp32 either way (round to nearest even on the way out).
+template <int E>
+__device__ __forceinline__ uint16_t to_elt(float f) {
+  if constexpr (E == ELT_F16) return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  else return f2bf(f);
+}
+template <int E>
+__device__ __forceinline__ float from_elt(uint16_t h) {
+  if constexpr (E == ELT_F16) return static_cast<float>(__builtin_bit_cast(_Float16, h));
+  else return bf2f(h);
+}
+template <int E>
+__device__ __forceinline__ f32x16_t mfma_32x32x16(bf16x8_t b, bf16x8_t a, f32x16_t c) {
+  if constexpr (E == ELT_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, b),
+                                                  __builtin_bit_cast(f16x8_t, a), c, 0, 0, 0);
+  else return __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0);
 }
 
 // Maps the hardware block id so that each XCD (blocks are dealt round-robin over 8 XCDs)
@@ -152,20 +174,12 @@ struct Occupancy {
   static constexpr int WPE = (BM / WM) * (BN / WN) >= 128 * 128 ? 1 : 2;
 };
 
-template <int BM, int BN, int BK, int S, int WM, int WN, int MODE>
-__global__ __launch_bounds__(64 * WM * WN)
-__attribute__((amdgpu_waves_per_eu(Occupancy<BM, BN, WM, WN>::WPE, Occupancy<BM, BN, WM, WN>::WPE)))
-void nt_mfma_kernel(const NtArgs a) {
-  using T = Tile<BM, BN, BK, S, WM, WN>;
-  __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
-  static_assert(T::LDS_BYTES <= 160 * 1024, "LDS budget");
+// Logical tile of this block: matrix l of the batch, tile row bi, tile column bj.
+struct TilePos {
+  int l, bi, bj;
+};
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wi = wave / WN, wj = wave % WN;
-
-  // ---- tile decode -------------------------------------------------------------------
+__device__ __forceinline__ TilePos decode_tile(const NtArgs& a) {
   const int nblocks = gridDim.x;
   const int lb = xcd_remap(blockIdx.x, nblocks);
   const int l = lb / a.tiles_per_mat;
@@ -205,124 +219,17 @@ void nt_mfma_kernel(const NtArgs a) {
     bi = first + r % gsize;
     bj = r / gsize;
   }
-  const int i0 = bi * BM, j0 = bj * BN;
+  return TilePos{l, bi, bj};
+}
 
-  const uint16_t* __restrict__ Ab = a.A + (long long)l * a.sA + (long long)i0 * a.lda;
-  const uint16_t* __restrict__ Bb = a.B + (long long)l * a.sB + (long long)j0 * a.ldb;
-
-  // ---- global -> LDS DMA ring --------------------------------------------------------
-  // DMA instruction q of wave w fills rows R0 = (NW q + w) * RPI .. R0 + RPI - 1 of a tile: lane l
-  // writes LDS slot l % CPR of row R0 + l / CPR, so it fetches the global chunk that the
-  // swizzle places in that slot (slot() is an involution in its chunk argument).
-  const int lrow = lane / T::CPR, lsl = lane % T::CPR;
-  // element offsets from the tile's first row (fixed-size arrays: a template-dependent array
-  // bound here makes clang drop the kernel's host launch stub)
-  static_assert(T::A_INST <= 8 && T::B_INST <= 8, "DMA instructions per slice");
-  unsigned offa[8], offb[8];
-#pragma unroll
-  for (int q = 0; q < T::A_INST; ++q) {
-    const int r = (T::NW * q + wave) * T::RPI + lrow;
-    offa[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8);
-  }
-#pragma unroll
-  for (int q = 0; q < T::B_INST; ++q) {
-    const int r = (T::NW * q + wave) * T::RPI + lrow;
-    offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8);
-  }
-  typedef __attribute__((address_space(3))) void* lds_ptr_t;
-  // slice sl_ of A and B into ring slot slot_ (this wave's share)
-#define DMUON_ISSUE(slice_, slot_)                                                             \
-  do {                                                                                         \
-    char* st_ = smem + (slot_) * T::STAGE + wave * 1024;                                       \
-    const uint16_t* ak_ = Ab + (slice_) * BK;                                                  \
-    const uint16_t* bk_ = Bb + (slice_) * BK;                                                  \
-    _Pragma("unroll") for (int q = 0; q < T::A_INST; ++q)                                      \
-        __builtin_amdgcn_global_load_lds(ak_ + offa[q], (lds_ptr_t)(st_ + q * 1024 * T::NW), 16, 0, 0); \
-    _Pragma("unroll") for (int q = 0; q < T::B_INST; ++q)                                      \
-        __builtin_amdgcn_global_load_lds(bk_ + offb[q], (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * T::NW), \
-                                         16, 0, 0);                                            \
-  } while (0)
-
-  f32x16_t acc[T::TI][T::TJ];
-#pragma unroll
-  for (int x = 0; x < T::TI; ++x)
-#pragma unroll
-    for (int y = 0; y < T::TJ; ++y)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.f;
-
-  const int KT = a.K / BK;
-  constexpr int KS = BK / 16;                     // MFMA substeps per slice
-  static_assert(KS % 2 == 0, "fragment double buffer alternates per substep");
-  const int arow0 = wi * T::WTM + (lane & 31);
-  const int brow0 = wj * T::WTN + (lane & 31);
-  const int khalf = lane >> 5;
-
-  auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8_t* af, bf16x8_t* bfr) {
-    const int kc = ks * 2 + khalf;
-#pragma unroll
-    for (int x = 0; x < T::TI; ++x) {
-      const int row = arow0 + x * 32;
-      af[x] = *reinterpret_cast<const bf16x8_t*>(sa + row * T::ROWB + (T::slot(kc, row) << 4));
-    }
-#pragma unroll
-    for (int y = 0; y < T::TJ; ++y) {
-      const int row = brow0 + y * 32;
-      bfr[y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
-    }
-  };
-  constexpr int NF = T::TI + T::TJ, NM = T::TI * T::TJ;
-  bf16x8_t af[2][T::TI], bfr[2][T::TJ];
-
-  // Ring schedule: slot s % S holds slice s; the prologue fills all S slots. Iteration kt
-  // consumes slice kt. Substeps 0 .. KS-2 each read the next substep's fragments under their
-  // own MFMAs. Before the last substep the wave waits for its share of slice kt+1 and for its
-  // own reads of slice kt, then meets the others at the barrier: past it slice kt+1 is complete
-  // and slot kt % S is free, so the DMA of slice kt+S and the reads of slice kt+1's first
-  // fragments both run under the last substep's MFMAs and no wave starts a slice with an empty
-  // pipeline. Past the end the DMA re-fetches the last slice into the free slot (never read),
-  // which keeps the number of loads per iteration, and so the vmcnt targets, uniform.
-#pragma unroll
-  for (int s0 = 0; s0 < S; ++s0) DMUON_ISSUE(min(s0, KT - 1), s0);
-  wait_slices<T>(S - 1);
-  bare_barrier();
-  load_frags(smem, smem + T::A_BYTES, 0, af[0], bfr[0]);
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const char* sa = smem + (kt % S) * T::STAGE;
-    const char* sb = sa + T::A_BYTES;
-#pragma unroll
-    for (int ks = 0; ks + 1 < KS; ++ks) {
-      load_frags(sa, sb, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
-#pragma unroll
-      for (int x = 0; x < T::TI; ++x)
-#pragma unroll
-        for (int y = 0; y < T::TJ; ++y)
-          // MFMA rows <- j (B operand), MFMA cols <- i (A operand): each lane then holds
-          // four consecutive j of one i, i.e. 8-byte row-major stores of D.
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][y], af[ks & 1][x],
-                                                              acc[x][y], 0, 0, 0);
-    }
-    sched_substeps<KS - 1, NM, NF>();
-    slice_barrier<(S - 2) * T::LPT>();
-    {
-      // reads first in program order: the DMA writes LDS, so later reads could not be
-      // scheduled ahead of it
-      const char* na = smem + ((kt + 1) % S) * T::STAGE;
-      load_frags(na, na + T::A_BYTES, 0, af[0], bfr[0]);
-    }
-    DMUON_ISSUE(min(kt + S, KT - 1), kt % S);
-#pragma unroll
-    for (int x = 0; x < T::TI; ++x)
-#pragma unroll
-      for (int y = 0; y < T::TJ; ++y)
-        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[1][y], af[1][x], acc[x][y], 0, 0, 0);
-    sched_front<0, NM, NF, T::LPT>();
-  }
-#undef DMUON_ISSUE
-  wait_vmcnt<0>();
-  bare_barrier();
-
+// Epilogue of a finished tile: the accumulators of this wave (rows iw.., columns jw.. of
+// matrix l) through the MODE-specific staging and stores. Uses the per-wave LDS area
+// smem + wave * EPI_REGION; the caller guarantees no operand slice is still in use there.
+template <class T, int MODE, int E>
+__device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
+                                            f32x16_t (&acc)[T::TI][T::TJ], int l, int bi,
+                                            int bj, int i0, int j0, int lane, int wave,
+                                            int wi, int wj) {
   const int li = lane & 31, lh = lane >> 5;
   const int iw = i0 + wi * T::WTM, jw = j0 + wj * T::WTN;
   const uint16_t* Cb = a.C ? a.C + (long long)l * a.sC : nullptr;
@@ -353,6 +260,10 @@ void nt_mfma_kernel(const NtArgs a) {
       if (a.DT) { DTb = a.DT + (long long)l * a.sDT; ldt = a.lddt; }
     }
     char* reg = smem + wave * T::EPI_REGION;
+    // diagonal tile of a result that must be exactly symmetric: only its upper triangle is
+    // kept, stored at (i, j) and mirrored to (j, i) (a product of two different symmetric
+    // factors is symmetric only to rounding otherwise)
+    const bool exact = MODE == EPI_SYM && a.sym_exact && a.tri && bi == bj;
     u32x2_t cbuf[2][T::TJ * 4];
     if (Cb) load_c(0, cbuf[0]);
 #pragma unroll
@@ -367,8 +278,8 @@ void nt_mfma_kernel(const NtArgs a) {
           float cv[4] = {0.f, 0.f, 0.f, 0.f};
           if (Cb) {
             const u32x2_t c2 = cbuf[x & 1][y * 4 + g];
-            cv[0] = bf2f(c2.x & 0xffff); cv[1] = bf2f(c2.x >> 16);
-            cv[2] = bf2f(c2.y & 0xffff); cv[3] = bf2f(c2.y >> 16);
+            cv[0] = from_elt<E>(c2.x & 0xffff); cv[1] = from_elt<E>(c2.x >> 16);
+            cv[2] = from_elt<E>(c2.y & 0xffff); cv[3] = from_elt<E>(c2.y >> 16);
           }
           uint16_t o[4];
 #pragma unroll
@@ -381,12 +292,29 @@ void nt_mfma_kernel(const NtArgs a) {
             } else {
               r = s * (v + a.beta * cv[e]);
             }
-            o[e] = f2bf(r);
+            o[e] = to_elt<E>(r);
           }
           o2[y * 4 + g].x = (unsigned)o[0] | ((unsigned)o[1] << 16);
           o2[y * 4 + g].y = (unsigned)o[2] | ((unsigned)o[3] << 16);
-          *reinterpret_cast<u32x2_t*>(reg + li * T::EPN + (jo + 4 * lh) * 2) = o2[y * 4 + g];
+          if (!exact)
+            *reinterpret_cast<u32x2_t*>(reg + li * T::EPN + (jo + 4 * lh) * 2) = o2[y * 4 + g];
         }
+      if (exact) {
+        const int i = iw + 32 * x + li;
+#pragma unroll
+        for (int y = 0; y < T::TJ; ++y)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int j = jw + 32 * y + 8 * g + 4 * lh + e;
+              const unsigned word = e < 2 ? o2[y * 4 + g].x : o2[y * 4 + g].y;
+              const uint16_t h = (uint16_t)((e & 1) ? (word >> 16) : (word & 0xffff));
+              if (i <= j) Db[(long long)i * a.ldd + j] = h;
+              if (i < j) Db[(long long)j * a.ldd + i] = h;
+            }
+        continue;
+      }
       {
         constexpr int CPRW = T::WTN / 4;          // 8-byte chunks per slab row
         constexpr int RPIT = 64 / CPRW;           // slab rows per wave instruction
@@ -447,8 +375,8 @@ void nt_mfma_kernel(const NtArgs a) {
           float cv[4] = {0.f, 0.f, 0.f, 0.f};
           if (Cb) {
             const u32x2_t c2 = cfin[y * 4 + g];
-            cv[0] = bf2f(c2.x & 0xffff); cv[1] = bf2f(c2.x >> 16);
-            cv[2] = bf2f(c2.y & 0xffff); cv[3] = bf2f(c2.y >> 16);
+            cv[0] = from_elt<E>(c2.x & 0xffff); cv[1] = from_elt<E>(c2.x >> 16);
+            cv[2] = from_elt<E>(c2.y & 0xffff); cv[3] = from_elt<E>(c2.y >> 16);
           }
           float4 u4;
           u4.x = s * (acc[x][y][4 * g + 0] + a.beta * cv[0]);
@@ -611,6 +539,142 @@ void nt_mfma_kernel(const NtArgs a) {
   }
 }
 
+template <int BM, int BN, int BK, int S, int WM, int WN, int MODE, int E>
+__global__ __launch_bounds__(64 * WM * WN)
+__attribute__((amdgpu_waves_per_eu(Occupancy<BM, BN, WM, WN>::WPE, Occupancy<BM, BN, WM, WN>::WPE)))
+void nt_mfma_kernel(const NtArgs a) {
+  using T = Tile<BM, BN, BK, S, WM, WN>;
+  __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
+  static_assert(T::LDS_BYTES <= 160 * 1024, "LDS budget");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wi = wave / WN, wj = wave % WN;
+
+  // ---- tile decode -------------------------------------------------------------------
+  const TilePos tp = decode_tile(a);
+  const int l = tp.l, bi = tp.bi, bj = tp.bj;
+  const int i0 = bi * BM, j0 = bj * BN;
+
+  const uint16_t* __restrict__ Ab = a.A + (long long)l * a.sA + (long long)i0 * a.lda;
+  const uint16_t* __restrict__ Bb = a.B + (long long)l * a.sB + (long long)j0 * a.ldb;
+
+  // ---- global -> LDS DMA ring --------------------------------------------------------
+  // DMA instruction q of wave w fills rows R0 = (NW q + w) * RPI .. R0 + RPI - 1 of a tile: lane l
+  // writes LDS slot l % CPR of row R0 + l / CPR, so it fetches the global chunk that the
+  // swizzle places in that slot (slot() is an involution in its chunk argument).
+  const int lrow = lane / T::CPR, lsl = lane % T::CPR;
+  // element offsets from the tile's first row (fixed-size arrays: a template-dependent array
+  // bound here makes clang drop the kernel's host launch stub)
+  static_assert(T::A_INST <= 8 && T::B_INST <= 8, "DMA instructions per slice");
+  unsigned offa[8], offb[8];
+#pragma unroll
+  for (int q = 0; q < T::A_INST; ++q) {
+    const int r = (T::NW * q + wave) * T::RPI + lrow;
+    offa[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8);
+  }
+#pragma unroll
+  for (int q = 0; q < T::B_INST; ++q) {
+    const int r = (T::NW * q + wave) * T::RPI + lrow;
+    offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8);
+  }
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  // slice sl_ of A and B into ring slot slot_ (this wave's share)
+#define DMUON_ISSUE(slice_, slot_)                                                             \
+  do {                                                                                         \
+    char* st_ = smem + (slot_) * T::STAGE + wave * 1024;                                       \
+    const uint16_t* ak_ = Ab + (slice_) * BK;                                                  \
+    const uint16_t* bk_ = Bb + (slice_) * BK;                                                  \
+    _Pragma("unroll") for (int q = 0; q < T::A_INST; ++q)                                      \
+        __builtin_amdgcn_global_load_lds(ak_ + offa[q], (lds_ptr_t)(st_ + q * 1024 * T::NW), 16, 0, 0); \
+    _Pragma("unroll") for (int q = 0; q < T::B_INST; ++q)                                      \
+        __builtin_amdgcn_global_load_lds(bk_ + offb[q], (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * T::NW), \
+                                         16, 0, 0);                                            \
+  } while (0)
+
+  f32x16_t acc[T::TI][T::TJ];
+#pragma unroll
+  for (int x = 0; x < T::TI; ++x)
+#pragma unroll
+    for (int y = 0; y < T::TJ; ++y)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.f;
+
+  const int KT = a.K / BK;
+  constexpr int KS = BK / 16;                     // MFMA substeps per slice
+  static_assert(KS % 2 == 0, "fragment double buffer alternates per substep");
+  const int arow0 = wi * T::WTM + (lane & 31);
+  const int brow0 = wj * T::WTN + (lane & 31);
+  const int khalf = lane >> 5;
+
+  auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8_t* af, bf16x8_t* bfr) {
+    const int kc = ks * 2 + khalf;
+#pragma unroll
+    for (int x = 0; x < T::TI; ++x) {
+      const int row = arow0 + x * 32;
+      af[x] = *reinterpret_cast<const bf16x8_t*>(sa + row * T::ROWB + (T::slot(kc, row) << 4));
+    }
+#pragma unroll
+    for (int y = 0; y < T::TJ; ++y) {
+      const int row = brow0 + y * 32;
+      bfr[y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
+    }
+  };
+  constexpr int NF = T::TI + T::TJ, NM = T::TI * T::TJ;
+  bf16x8_t af[2][T::TI], bfr[2][T::TJ];
+
+  // Ring schedule: slot s % S holds slice s; the prologue fills all S slots. Iteration kt
+  // consumes slice kt. Substeps 0 .. KS-2 each read the next substep's fragments under their
+  // own MFMAs. Before the last substep the wave waits for its share of slice kt+1 and for its
+  // own reads of slice kt, then meets the others at the barrier: past it slice kt+1 is complete
+  // and slot kt % S is free, so the DMA of slice kt+S and the reads of slice kt+1's first
+  // fragments both run under the last substep's MFMAs and no wave starts a slice with an empty
+  // pipeline. Past the end the DMA re-fetches the last slice into the free slot (never read),
+  // which keeps the number of loads per iteration, and so the vmcnt targets, uniform.
+#pragma unroll
+  for (int s0 = 0; s0 < S; ++s0) DMUON_ISSUE(min(s0, KT - 1), s0);
+  wait_slices<T>(S - 1);
+  bare_barrier();
+  load_frags(smem, smem + T::A_BYTES, 0, af[0], bfr[0]);
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const char* sa = smem + (kt % S) * T::STAGE;
+    const char* sb = sa + T::A_BYTES;
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      load_frags(sa, sb, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
+#pragma unroll
+      for (int x = 0; x < T::TI; ++x)
+#pragma unroll
+        for (int y = 0; y < T::TJ; ++y)
+          // MFMA rows <- j (B operand), MFMA cols <- i (A operand): each lane then holds
+          // four consecutive j of one i, i.e. 8-byte row-major stores of D.
+          acc[x][y] = mfma_32x32x16<E>(bfr[ks & 1][y], af[ks & 1][x], acc[x][y]);
+    }
+    sched_substeps<KS - 1, NM, NF>();
+    slice_barrier<(S - 2) * T::LPT>();
+    {
+      // reads first in program order: the DMA writes LDS, so later reads could not be
+      // scheduled ahead of it
+      const char* na = smem + ((kt + 1) % S) * T::STAGE;
+      load_frags(na, na + T::A_BYTES, 0, af[0], bfr[0]);
+    }
+    DMUON_ISSUE(min(kt + S, KT - 1), kt % S);
+#pragma unroll
+    for (int x = 0; x < T::TI; ++x)
+#pragma unroll
+      for (int y = 0; y < T::TJ; ++y)
+        acc[x][y] = mfma_32x32x16<E>(bfr[1][y], af[1][x], acc[x][y]);
+    sched_front<0, NM, NF, T::LPT>();
+  }
+#undef DMUON_ISSUE
+  wait_vmcnt<0>();
+  bare_barrier();
+
+  nt_epilogue<T, MODE, E>(a, smem, acc, l, bi, bj, i0, j0, lane, wave, wi, wj);
+}
+
 // K-slice pipeline of the NT kernel: BK-wide slices in an S-deep LDS ring. The default is
 // 64-wide slices double-buffered (one barrier per 64 MFMAs per SIMD); DMUON_NT_PIPE=32x4 selects
 // 32-wide slices four deep (three slices of prefetch, twice the barriers) as a tuning aid.
@@ -630,26 +694,30 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   if (nb <= 0) return hipSuccess;
   dim3 grid((unsigned)nb);
   const int v = nt_pipe_variant();
-#define DMUON_NT(TILE, BK, S, WM, WN)                                                          \
+#define DMUON_NT(TILE, BK, S, WM, WN, E)                                                       \
   do {                                                                                         \
     dim3 block(64 * WM * WN);                                                                  \
     if (a.mode == EPI_SYM)                                                                     \
-      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_SYM>), grid, block, 0,  \
-                         stream, a);                                                           \
+      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_SYM, E>), grid, block, \
+                         0, stream, a);                                                        \
     else if (a.mode == EPI_NS)                                                                 \
-      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_NS>), grid, block, 0,   \
-                         stream, a);                                                           \
+      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_NS, E>), grid, block,  \
+                         0, stream, a);                                                        \
     else                                                                                       \
-      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_FINAL>), grid, block, 0,\
-                         stream, a);                                                           \
+      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_FINAL, E>), grid,      \
+                         block, 0, stream, a);                                                 \
   } while (0)
-  if (tile == 256) {
-    if (v == 1) DMUON_NT(256, 64, 2, 2, 4);
-    else if (v == 2) DMUON_NT(256, 64, 2, 2, 2);
-    else DMUON_NT(256, 32, 4, 2, 4);
+  if (a.elt == ELT_F16) {
+    // fp16 operands (the Gram-space iteration): the default pipelines only
+    if (tile == 256) DMUON_NT(256, 64, 2, 2, 4, ELT_F16);
+    else DMUON_NT(128, 64, 2, 2, 2, ELT_F16);
+  } else if (tile == 256) {
+    if (v == 1) DMUON_NT(256, 64, 2, 2, 4, ELT_BF16);
+    else if (v == 2) DMUON_NT(256, 64, 2, 2, 2, ELT_BF16);
+    else DMUON_NT(256, 32, 4, 2, 4, ELT_BF16);
   } else {
-    if (v == 0) DMUON_NT(128, 32, 4, 2, 2);
-    else DMUON_NT(128, 64, 2, 2, 2);
+    if (v == 0) DMUON_NT(128, 32, 4, 2, 2, ELT_BF16);
+    else DMUON_NT(128, 64, 2, 2, 2, ELT_BF16);
   }
 #undef DMUON_NT
   return hipGetLastError();

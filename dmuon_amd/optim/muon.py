@@ -11,8 +11,8 @@ Constructor, ``step()`` and ``zero_grad()`` keep the reference's signature and e
 
 runs on the GPU as one C-ABI call per bucket of same-shape parameters
 (``dmuon_muon_step_group``): a fused momentum/Nesterov/staging kernel, a norm finalise, and
-per NS step three bf16 MFMA kernels (SYRK, SYRK-polynomial, GEMM), the last GEMM applying the
-weight update in its epilogue. The momentum buffer is fp32 and lives in
+the bf16 MFMA products of the chosen NS form (``ns_backend``: "gram", the default, or
+"direct"), the last product applying the weight update in its epilogue. The momentum buffer is fp32 and lives in
 ``optimizer.state[id(dp)]["momentum_buffer"]`` shaped ``(rows, cols)`` like the reference's.
 
 Parameters that are not dedicated (and 1-D dedicated ones) get the reference's decoupled AdamW
@@ -34,7 +34,8 @@ from dmuon_amd.api import iter_dedicated_states
 from dmuon_amd.grad_clip import _clip_ready_muon_grad_norm_
 from dmuon_amd.utils import prepare_muon_grads
 from dmuon_amd.optim.adamw import fused_adamw_
-from dmuon_amd.optim.newton_schulz import NewtonSchulz, _coeff_array, _float_dtype_code
+from dmuon_amd.optim.newton_schulz import (NewtonSchulz, _backend_code, _coeff_array,
+                                           _float_dtype_code)
 
 logger = logging.getLogger(__name__)
 
@@ -261,16 +262,18 @@ class Muon(torch.optim.Optimizer):
     def _step_muon_group(self, group) -> tuple[int, int]:
         lr, mu, wd = float(group["lr"]), float(group["momentum"]), float(group["weight_decay"])
         coeffs, T = _coeff_array(self._ns.resolved_coefficients())
+        backend = _backend_code(self._ns.backend)
+        rst, n_rst = _C.restart_array(self._ns.restart_codes())
         count = numel = 0
         for (rows, cols, gdt, wdt, pdt, dev, first), items in self._buckets(group).items():
             _require_cuda(dev)
             L_all = len(items)
             num_cus = torch.cuda.get_device_properties(dev).multi_processor_count
-            chunk = self._chunk_size(rows, cols, L_all, num_cus)
+            chunk = self._chunk_size(rows, cols, L_all, num_cus, backend)
             for s in range(0, L_all, chunk):
                 part = items[s:s + chunk]
                 L = len(part)
-                tile, _, _, nbytes = _C.plan(rows, cols, L, 0, num_cus)
+                tile, _, _, nbytes = _C.plan(rows, cols, L, 0, num_cus, backend)
                 ws = self._get_workspace(dev, nbytes)
                 gs, bufs, ws_, pubs = [], [], [], []
                 for dp, g in part:
@@ -298,18 +301,19 @@ class Muon(torch.optim.Optimizer):
                 pub_code = _float_dtype_code(pubs[0]) if pubs else 0
                 _C.call("dmuon_muon_step_group", base, _float_dtype_code(gs[0]), base + 8 * L,
                         base + 16 * L, _float_dtype_code(ws_[0]), pub_base, pub_code, rows, cols,
-                        L, lr, mu, wd, int(self._nesterov), int(first), coeffs, T,
-                        self._ns_eps, ws.data_ptr(), ws.numel(), tile, stream)
+                        L, lr, mu, wd, int(self._nesterov), int(first), coeffs, T, backend, rst,
+                        n_rst, self._ns_eps, ws.data_ptr(), ws.numel(), tile, stream)
                 count += L
                 numel += L * rows * cols
             for dp, _ in items:
                 dp._reduced_grad = None
         return count, numel
 
-    def _chunk_size(self, rows: int, cols: int, L: int, num_cus: int) -> int:
-        per = _C.plan(rows, cols, 1, 0, num_cus)[3]
+    def _chunk_size(self, rows: int, cols: int, L: int, num_cus: int, backend: int) -> int:
+        per = _C.plan(rows, cols, 1, 0, num_cus, backend)[3]
         chunk = max(1, min(L, self._workspace_limit // max(per, 1)))
-        while chunk > 1 and _C.plan(rows, cols, chunk, 0, num_cus)[3] > self._workspace_limit:
+        while chunk > 1 and _C.plan(rows, cols, chunk, 0, num_cus, backend)[3] > \
+                self._workspace_limit:
             chunk -= 1
         return chunk
 

@@ -5,18 +5,25 @@ coefficient sets (``:45-75``), the :class:`NewtonSchulz` configuration object (`
 ``direct_newton_schulz`` (``:225-273``), ``newton_schulz`` (``:299-327``) and
 ``gram_newton_schulz`` (``:333-448``).
 
-Every entry point runs the same device algorithm, the direct iteration in SYRK form, for each
-per-step coefficient triple ``(a, b, c)``::
+Two device algorithms, both on the bf16 MFMA NT kernels, for X = G / (||G||_F + eps) oriented
+so that X has m = min(rows, cols) rows and n = max(rows, cols) columns:
 
-    A = X X^T            (bf16 MFMA SYRK, upper-triangle tiles, mirrored)
+``backend="direct"`` (``direct_newton_schulz``), per coefficient triple ``(a, b, c)``::
+
+    A = X X^T            (SYRK: upper-triangle tiles, mirrored)
     P = b*A + c*A A^T    (the same SYRK kernel with C = A in the epilogue)
-    X = a*X + P X        (bf16 MFMA GEMM against the transposed copy of X)
+    X = a*X + P X        (GEMM against the transposed copy of X)
 
-with X = G / (||G||_F + eps) oriented so that X has min(rows, cols) rows. In exact arithmetic
-the Gram-space recurrence with restarts (``newton_schulz.py:364-448``) produces the same
-polynomial of X X^T applied to X, so ``backend="gram"`` selects only its default coefficients
-and restart schedule; the restart schedule itself is not needed by the direct form. Results
-differ from the reference's fp16 pipeline by rounding (bf16 operands, fp32 accumulation).
+``backend="gram"`` (``gram_newton_schulz``, the reference's default), in fp16 as the reference
+runs it: R = X X^T once, then per step only m x m products -- ``Z = c R R + b R``,
+``P = Z + a I``, ``Q <- P Q`` (``Q = P`` after a start or restart) and, unless the next step is
+the last or a restart, ``R <- P R P`` -- with ``X <- Q X; R = X X^T`` at each restart index and
+``U = Q X`` at the end (``newton_schulz.py:364-448``). For n > m this needs fewer flops than the
+direct form. bf16 is not accurate enough for this recurrence (R's small eigenvalues drown in
+its rounding), so X is staged as fp16 of the normalised input times a power of two.
+
+Results differ from the reference's fp16 pipeline by rounding (bf16 operands, fp32
+accumulation).
 
 There is no CPU path: CPU tensors raise.
 """
@@ -97,6 +104,25 @@ def _coeff_array(coefficients: Sequence[Sequence[float]]):
     return (ctypes.c_float * len(flat))(*flat), len(flat) // 3
 
 
+def _backend_code(backend: str) -> int:
+    if backend == "direct":
+        return _C.NS_DIRECT
+    if backend == "gram":
+        return _C.NS_GRAM
+    raise ValueError(f"backend must be 'gram' or 'direct', got '{backend}'")
+
+
+def _restarts(restart_iterations) -> list:
+    if restart_iterations is None:
+        return list(DEFAULT_RESTART_ITERATIONS)
+    out = []
+    for r in restart_iterations:
+        if not isinstance(r, int):
+            raise TypeError("restart_iterations must be a list of ints")
+        out.append(r)
+    return out
+
+
 def _ptr_array(tensors: Sequence[Tensor], device: torch.device) -> Tensor:
     host = torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64, pin_memory=True)
     return host.to(device, non_blocking=True)
@@ -129,8 +155,12 @@ def newton_schulz_batched(
     eps: float = 1e-7,
     out: Optional[Sequence[Tensor]] = None,
     tile: int = 0,
+    backend: str = "direct",
+    restart_iterations: Sequence[int] = (),
 ) -> list[Tensor]:
-    """Direct NS of several same-shape, same-dtype 2-D GPU matrices in one grouped launch chain."""
+    """NS of several same-shape, same-dtype 2-D GPU matrices in one grouped launch chain.
+
+    ``backend`` "direct" or "gram" (with ``restart_iterations``), as described above."""
     if len(Gs) == 0:
         return []
     G0 = Gs[0]
@@ -154,15 +184,17 @@ def newton_schulz_batched(
     rows, cols = G0.shape
     L = len(ins)
     coeff, T = _coeff_array(coefficients)
+    code = _backend_code(backend)
+    rst, n_rst = _C.restart_array(restart_iterations if code == _C.NS_GRAM else ())
     num_cus = torch.cuda.get_device_properties(G0.device).multi_processor_count
-    t, _mp, _np, nbytes = _C.plan(rows, cols, L, tile, num_cus)
+    t, _mp, _np, nbytes = _C.plan(rows, cols, L, tile, num_cus, code)
     ws = _WORKSPACE.get(G0.device, nbytes)
     gp = _ptr_array(ins, G0.device)
     op = _ptr_array(outs, G0.device)
     stream = torch.cuda.current_stream(G0.device).cuda_stream
     _C.call("dmuon_newton_schulz_group", gp.data_ptr(), _float_dtype_code(ins[0]), op.data_ptr(),
-            _float_dtype_code(outs[0]), rows, cols, L, coeff, T, float(eps), ws.data_ptr(),
-            ws.numel(), t, stream)
+            _float_dtype_code(outs[0]), rows, cols, L, coeff, T, code, rst, n_rst, float(eps),
+            ws.data_ptr(), ws.numel(), t, stream)
     if out is None and G0.dtype != work_dtype:
         return [o.to(G0.dtype) for o in outs]
     return outs
@@ -189,18 +221,15 @@ def gram_newton_schulz(
     restart_iterations: Optional[list[int]] = None,
     deterministic: bool = False,
 ) -> Tensor:
-    """Gram-space NS entry point (``newton_schulz.py:333-448``) on the SYRK-form device path.
+    """Gram-space NS (``newton_schulz.py:333-448``) on the HIP kernels.
 
-    ``restart_iterations`` is validated but not needed (see the module docstring);
-    ``deterministic`` is accepted for compatibility (the HIP kernels are deterministic).
+    ``restart_iterations`` defaults to ``[2]``; ``deterministic`` is accepted for compatibility
+    (the HIP kernels are deterministic).
     """
     if coefficients is None:
         coefficients = DEFAULT_COEFFICIENTS
-    if restart_iterations is not None:
-        for r in restart_iterations:
-            if not isinstance(r, int):
-                raise TypeError("restart_iterations must be a list of ints")
-    return newton_schulz_batched([G], coefficients, eps)[0]
+    return newton_schulz_batched([G], coefficients, eps, backend="gram",
+                                 restart_iterations=_restarts(restart_iterations))[0]
 
 
 def newton_schulz(
@@ -222,8 +251,8 @@ class NewtonSchulz:
     ``kernel`` in {"auto", "hip", "hip_gfx950", "cublas"} -- every accepted value selects the
     HIP kernels; "quack" and "cute_sm80" name NVIDIA kernels and raise at construction, as the
     reference does for an unavailable kernel. ``coefficients=None`` uses the Polar-Express set;
-    ``restart_iterations`` defaults to ``[2]`` and is recorded only; ``deterministic`` is
-    accepted (the HIP path is bit-reproducible run to run).
+    ``restart_iterations`` (gram only) defaults to ``[2]``; ``deterministic`` is accepted (the
+    HIP path is bit-reproducible run to run).
     """
 
     def __init__(
@@ -248,8 +277,7 @@ class NewtonSchulz:
         self.backend = backend
         self.kernel = _KERNEL_ALIASES[kernel]
         self.coefficients = coefficients
-        self.restart_iterations = (
-            list(DEFAULT_RESTART_ITERATIONS) if restart_iterations is None else list(restart_iterations))
+        self.restart_iterations = _restarts(restart_iterations)
         self.deterministic = True
 
     def resolved_coefficients(self) -> list:
@@ -257,7 +285,12 @@ class NewtonSchulz:
 
     def local(self, G: Tensor, steps: int) -> Tensor:
         """NS of one full matrix (``newton_schulz.py:194-212``)."""
-        return newton_schulz_batched([G], self.resolved_coefficients())[0]
+        return newton_schulz_batched([G], self.resolved_coefficients(), backend=self.backend,
+                                     restart_iterations=self.restart_iterations)[0]
+
+    def restart_codes(self) -> list:
+        """The restart list the device algorithm receives (empty for the direct backend)."""
+        return list(self.restart_iterations) if self.backend == "gram" else []
 
     def __repr__(self) -> str:
         coeff = "default" if self.coefficients is None else f"{len(self.coefficients)}-step custom"
@@ -266,7 +299,8 @@ class NewtonSchulz:
 
 def get_ns_backend() -> str:
     """One-line description of the NS kernel (``syrk_dispatch.py:42-66``)."""
-    return "Direct NS in SYRK form · kernel=hip_gfx950 (MI355X CDNA4, bf16 MFMA 32x32x16)"
+    return ("Gram-space NS with restarts / direct NS in SYRK form · kernel=hip_gfx950 "
+            "(MI355X CDNA4, bf16 MFMA 32x32x16)")
 
 
 def get_backend_status() -> dict:
@@ -285,11 +319,29 @@ def get_backend_status() -> dict:
     return status
 
 
-def ns_useful_flops(rows: int, cols: int, steps: int = 5) -> float:
-    """Useful NS FLOPs of one matrix: T*[m(m+1)n + m(m+1)m + 2 m^2 n] (one triangle of each
-    symmetric product, full P X), m = min(rows, cols), n = max(rows, cols)."""
+def ns_useful_flops(rows: int, cols: int, steps: int = 5, backend: str = "direct",
+                    restart_iterations: Sequence[int] = (2,)) -> float:
+    """Useful NS FLOPs of one matrix (one triangle of each symmetric product, full GEMMs),
+    m = min(rows, cols), n = max(rows, cols).
+
+    direct: T*[m(m+1)n + m(m+1)m + 2 m^2 n].
+    gram: (1 + r) m(m+1)n Gram products and r + 1 Q X products (2 m^2 n), r = the restarts
+    inside (0, T); per step m(m+1)m for Z, m(m+1)m for Q <- P Q except right after a (re)start,
+    and, unless the next step is the last or a restart, the R update P R P: 2 m^3 for the full
+    product W = P R plus m(m+1)m for W P."""
     m, n = min(rows, cols), max(rows, cols)
-    return float(steps) * (m * (m + 1) * n + m * (m + 1) * m + 2.0 * m * m * n)
+    sq, gram_mn, qx = m * (m + 1) * m, m * (m + 1) * n, 2.0 * m * m * n
+    if backend == "direct":
+        return float(steps) * (gram_mn + sq + qx)
+    rs = {int(r) for r in restart_iterations if 0 < int(r) < steps}
+    total = (1 + len(rs)) * (gram_mn + qx)
+    for i in range(steps):
+        total += sq
+        if i != 0 and i not in rs:
+            total += sq
+        if i + 1 < steps and (i + 1) not in rs:
+            total += 2.0 * m * m * m + sq
+    return float(total)
 
 
 def muon_update_scale(rows: int, cols: int) -> float:

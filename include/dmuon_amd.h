@@ -33,7 +33,8 @@
  *                                                                   math for `batch` same-shape
  *                                                                   params (direct NS, T steps)
  *                            + dmuon/_backends/fsdp2/group.py:766-781 owner publish copy-in
- *   dmuon_newton_schulz_group dmuon/optim/newton_schulz.py:225-273  direct_newton_schulz(G) for
+ *   dmuon_newton_schulz_group dmuon/optim/newton_schulz.py:225-273  direct_newton_schulz(G) /
+ *                            dmuon/optim/newton_schulz.py:333-448  gram_newton_schulz(G) for
  *                                                                   `batch` same-shape matrices
  *   dmuon_adamw_multi        dmuon/optim/muon.py:1857-1916          _adamw_update_batch: the
  *                                                                   torch._foreach AdamW of one
@@ -53,6 +54,10 @@ extern "C" {
 
 #define DMUON_DTYPE_F32 0
 #define DMUON_DTYPE_BF16 1
+
+/* Newton-Schulz device algorithms (the `backend` argument below). */
+#define DMUON_NS_DIRECT 0 /* X <- a X + (b A + c A A^T) X, A = X X^T, every step */
+#define DMUON_NS_GRAM 1   /* Gram-space iteration with restarts (gram_newton_schulz) */
 
 /* Text of the last error raised on this thread ("" if none). */
 const char* dmuon_last_error(void);
@@ -146,32 +151,40 @@ int dmuon_muon_update(void* const* w_ptrs, int w_dtype, const void* const* u_ptr
 /*
  * Planning for a group of `batch` same-shape rows x cols matrices: NS dims m = min, n = max,
  * chosen output tile (tile_req 0 = automatic, else 128 or 256), padded m_pad / n_pad and the
- * workspace bytes dmuon_muon_step_group / dmuon_newton_schulz_group need. Host-only.
+ * workspace bytes dmuon_muon_step_group / dmuon_newton_schulz_group need for `backend`
+ * (DMUON_NS_GRAM needs three more m_pad x m_pad bf16 matrices per group member). Host-only.
  */
-int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int* tile, int* m_pad,
-                  int* n_pad, int64_t* workspace_bytes);
+int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int backend,
+                  int* tile, int* m_pad, int* n_pad, int64_t* workspace_bytes);
 
 /*
  * Full Muon update for `batch` same-shape rows x cols params (one owner's group):
- *   momentum (+Nesterov), normalise, T direct Newton-Schulz steps with per-step coefficients
+ *   momentum (+Nesterov), normalise, T Newton-Schulz steps with per-step coefficients
  *   coeffs[3*t .. 3*t+2] = (a, b, c) (HOST array), then
  *   W <- round(W*(1 - lr*wd)) - lr*0.2*sqrt(max(rows, cols)) * U    (decay skipped if wd <= 0)
  * and, when pub_ptrs != NULL, pub[l] <- round_to_pub_dtype(new W[l]) in the same epilogue (the
  * owner's forward copy when W is a master in another dtype; NULL when W is the forward tensor).
- * Each NS step is SYRK (X X^T) -> SYRK-poly (b*A + c*A A^T) -> GEMM (a*X + P X) on bf16 MFMA.
+ * backend DMUON_NS_DIRECT: each step is SYRK (A = X X^T) -> SYRK-poly (b*A + c*A A^T) -> GEMM
+ *   (a*X + P X) on bf16 MFMA (direct_newton_schulz, newton_schulz.py:225-273).
+ * backend DMUON_NS_GRAM: gram_newton_schulz (newton_schulz.py:333-448): R = X X^T once; per step
+ *   P = a I + b R + c R R, Q <- P Q, R <- (R P) P, all m x m; at each step index listed in
+ *   restarts[0 .. n_restarts-1] (HOST array; index 0 ignored) X <- Q X and R = X X^T again;
+ *   finally U = Q X. Fewer flops than direct when n > m.
  * workspace: device memory of at least the planned bytes; its contents need no initialisation.
  */
 int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
                           void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype,
                           int rows, int cols, int batch, double lr, double mu, double wd,
-                          int nesterov, int first_step, const float* coeffs, int T, float eps,
-                          void* workspace, int64_t workspace_bytes, int tile, void* stream);
+                          int nesterov, int first_step, const float* coeffs, int T, int backend,
+                          const int* restarts, int n_restarts, float eps, void* workspace,
+                          int64_t workspace_bytes, int tile, void* stream);
 
-/* direct_newton_schulz for `batch` same-shape rows x cols matrices: out[l] <- NS(g[l]). */
+/* direct_newton_schulz / gram_newton_schulz (by `backend`, as above) for `batch` same-shape
+ * rows x cols matrices: out[l] <- NS(g[l]). */
 int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,
                               int out_dtype, int rows, int cols, int batch, const float* coeffs,
-                              int T, float eps, void* workspace, int64_t workspace_bytes, int tile,
-                              void* stream);
+                              int T, int backend, const int* restarts, int n_restarts, float eps,
+                              void* workspace, int64_t workspace_bytes, int tile, void* stream);
 
 /*
  * Decoupled AdamW over n tensors in one pass (one bucket of the reference's

@@ -16,6 +16,7 @@ It restates, in numpy, the reference algorithm of X-Square-Robot/dmuon on this p
 * ``syrk_emulated_ns`` the build's own bf16 SYRK-form pipeline (bf16 operands, fp32
                       accumulation, normalisation folded into the first SYRK/GEMM), used to
                       bound the bf16-vs-fp16 gap and as a tight check of the GPU kernels.
+* ``syrk_emulated_gram_ns`` the same for the build's Gram-form pipeline.
 * ``muon_step``       ``dmuon/optim/muon.py:1683-1740``: sum-form momentum
                       (``buf.mul_(mu).add_(g)``, first step ``buf = g``), Nesterov
                       ``g + mu*buf``, NS, ``W *= 1 - lr*wd`` when wd > 0, then
@@ -203,6 +204,81 @@ def syrk_emulated_ns(G: np.ndarray, coefficients: Sequence = KELLER, eps: float 
     if t:
         Xq = Xq.T
     return np.ascontiguousarray(Xq)
+
+
+def _upper_mirror(D: np.ndarray) -> np.ndarray:
+    """The upper triangle of D mirrored into the lower one (exactly symmetric storage, as the
+    device stores the Gram iteration's symmetric products)."""
+    return np.triu(D) + np.triu(D, 1).T
+
+
+def syrk_emulated_gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
+                          restart_iterations: Optional[Sequence[int]] = None, eps: float = 1e-7,
+                          op_dtype: str = "fp16", kx: float = 4096.0) -> np.ndarray:
+    """The build's device Gram pipeline (the reference's recurrence, newton_schulz.py:364-448,
+    with the build's product forms and roundings), rnd = op_dtype:
+    X = rnd(kx s ns_in), s = 1/(||ns_in|| + eps); R = rnd(kr/kx^2 X X^T) with the stored-R
+    scale rs = kr = 2^floor(log2 m) (at most 2^12); per step Z = rnd(c/rs^2 R R^T + b/rs R);
+    Q = rnd(Z + a I) after a start/restart, else Q = rnd(Z Q + a Q) (the full product: Q is a
+    product of polynomials that no longer commute once rounded, and its order must match R's);
+    unless the next step is the last or a restart W = rnd(Z R^T + a R),
+    R = rnd(W Z^T / rs + a/rs W), rs = 1; restart: X = rnd(Q X), R = rnd(X X^T / kx^2), rs = 1;
+    U = fp32(Q X / kx). Symmetric results (R, Z, a fresh Q) keep their upper triangle,
+    mirrored."""
+    if restart_iterations is None:
+        restart_iterations = DEFAULT_RESTART
+    X = np.asarray(G, dtype=np.float32)
+    t = X.shape[0] > X.shape[1]
+    if t:
+        X = X.T
+    nrm = np.float32(np.sqrt(np.sum(X.astype(np.float64) ** 2)))
+    s = np.float32(1.0) / (nrm + np.float32(eps))
+    f32 = np.float32
+    Xq = rnd((X * f32(s * f32(kx))).astype(np.float32), op_dtype)
+    m = Xq.shape[0]
+    kr = 1
+    while kr * 2 <= m and kr < 4096:
+        kr *= 2
+    eye = np.eye(m, dtype=np.float32)
+    sym = _upper_mirror
+
+    def epi(acc, alpha, C=None, beta=0.0, diag=0.0):
+        r = f32(alpha) * acc.astype(np.float32)
+        if C is not None:
+            r = r + f32(beta) * C
+        if diag:
+            r = r + f32(diag) * eye
+        return r
+
+    rs = f32(kr)
+    R = sym(rnd(epi(_mm(Xq, Xq.T, "fp32"), rs / f32(kx * kx)), op_dtype))
+    Q = None
+    n_it = len(coefficients)
+    for i, (a, b, c) in enumerate(coefficients):
+        if i in restart_iterations and i != 0:
+            Xq = rnd(_mm(Q, Xq, "fp32"), op_dtype)
+            rs = f32(1.0)
+            R = sym(rnd(epi(_mm(Xq, Xq.T, "fp32"), f32(1.0) / f32(kx * kx)), op_dtype))
+            Q = None
+        evolve = i < n_it - 1 and (i + 1) not in restart_iterations
+        z2, z1 = f32(c) / (rs * rs), f32(b) / rs
+        RR = _mm(R, R.T, "fp32")
+        if Q is None and not evolve:
+            Q = sym(rnd(epi(RR, z2, R, z1, a), op_dtype))
+            continue
+        Z = sym(rnd(epi(RR, z2, R, z1), op_dtype))
+        if Q is None:
+            Q = rnd(Z + f32(a) * eye, op_dtype)
+        else:
+            Q = rnd(epi(_mm(Z, Q, "fp32"), 1.0, Q, a), op_dtype)
+        if evolve:
+            W = rnd(epi(_mm(Z, R.T, "fp32"), 1.0, R, a), op_dtype)
+            R = sym(rnd(epi(_mm(W, Z.T, "fp32"), f32(1.0) / rs, W, f32(a) / rs), op_dtype))
+            rs = f32(1.0)
+    U = (f32(1.0 / kx) * _mm(Q, Xq, "fp32")).astype(np.float32)
+    if t:
+        U = U.T
+    return np.ascontiguousarray(U)
 
 
 # ------------------------------------------------------------------------------------------

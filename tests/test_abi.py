@@ -41,6 +41,9 @@ def test_plan(rows, cols, batch, tile, m_pad, n_pad):
     x = mp * np_ * 2
     a = mp * mp * 2
     assert ws >= batch * (3 * x + 2 * a)
+    tg, mpg, npg, wsg = _C.plan(rows, cols, batch, backend=_C.NS_GRAM)
+    assert (tg, mpg, npg) == (tile, m_pad, n_pad)
+    assert wsg >= ws + batch * 3 * a       # R, P and two Q buffers plus R P
 
 
 def test_plan_rejects_bad_arguments():
@@ -48,6 +51,8 @@ def test_plan_rejects_bad_arguments():
         _C.plan(0, 10, 1)
     with pytest.raises(RuntimeError, match="tile"):
         _C.plan(64, 64, 1, tile=96)
+    with pytest.raises(RuntimeError, match="backend"):
+        _C.plan(64, 64, 1, backend=7)
 
 
 def _err(rc):
@@ -83,23 +88,35 @@ def test_group_validation_without_gpu():
     p = ctypes.c_void_p(4096)
     # workspace too small
     msg = _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1, 0.02, 0.95, 0.0,
-                                         1, 1, coeff, 5, 1e-7, p, 16, 0, None))
+                                         1, 1, coeff, 5, 0, None, 0, 1e-7, p, 16, 0, None))
     assert "workspace" in msg
     # unsupported dtype code
     assert "dtype" in _err(lib.dmuon_muon_step_group(p, 7, p, p, 1, None, 0, 512, 1024, 1, 0.02,
-                                                     0.95, 0.0, 1, 1, coeff, 5, 1e-7, p, 1 << 40,
-                                                     0, None))
+                                                     0.95, 0.0, 1, 1, coeff, 5, 0, None, 0, 1e-7, p,
+                                                     1 << 40, 0, None))
     # unsupported publish dtype
     assert "publish" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 0, p, 9, 512, 1024, 1, 0.02,
-                                                       0.95, 0.0, 1, 1, coeff, 5, 1e-7, p,
-                                                       1 << 40, 0, None))
+                                                       0.95, 0.0, 1, 1, coeff, 5, 0, None, 0, 1e-7,
+                                                       p, 1 << 40, 0, None))
     # no coefficients
     assert "coefficient" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1,
-                                                           0.02, 0.95, 0.0, 1, 1, coeff, 0, 1e-7,
-                                                           p, 1 << 40, 0, None))
+                                                           0.02, 0.95, 0.0, 1, 1, coeff, 0, 0, None,
+                                                           0, 1e-7, p, 1 << 40, 0, None))
     # NS group needs outputs
     assert "out_ptrs" in _err(lib.dmuon_newton_schulz_group(p, 1, None, 1, 64, 64, 1, coeff, 5,
-                                                            1e-7, p, 1 << 30, 0, None))
+                                                            0, None, 0, 1e-7, p, 1 << 30, 0, None))
+    # unknown backend, restart list missing
+    assert "backend" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1, 0.02,
+                                                       0.95, 0.0, 1, 1, coeff, 5, 5, None, 0,
+                                                       1e-7, p, 1 << 40, 0, None))
+    assert "restart" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1, 0.02,
+                                                       0.95, 0.0, 1, 1, coeff, 5, 1, None, 2,
+                                                       1e-7, p, 1 << 40, 0, None))
+    # gram workspace is larger than direct's
+    ws_direct = _C.plan(512, 1024, 1)[3]
+    assert "workspace" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1,
+                                                         0.02, 0.95, 0.0, 1, 1, coeff, 5, 1, None,
+                                                         0, 1e-7, p, ws_direct, 0, None))
 
 
 def test_pre_and_final_validation_without_gpu():

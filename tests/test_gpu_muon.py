@@ -151,6 +151,40 @@ def test_c5_layer_full_size_bit_exact_chain(gpu):
             assert torch.equal(ps[i].detach(), exp), shape
 
 
+# ------------------------------------------------------------ Gram NS backend (the default)
+@pytest.mark.parametrize("shapes,dtype", [
+    ([(256, 1024), (1024, 256), (300, 1000)], torch.float32),
+    ([(256, 640)] * 3 + [(640, 256)] * 2, torch.bfloat16),
+])
+def test_default_gram_backend_step(gpu, shapes, dtype):
+    """Muon with its default ns_backend ("gram", Polar-Express, restarts [2]) against the
+    reference's fp16 gram_newton_schulz inside the oracle's Muon step; momentum bit-exact."""
+    lr, mu, wd = 0.02, 0.95, 0.1
+    m = Mats(shapes, dtype, gpu)
+    policy = BF16_MASTER if dtype == torch.bfloat16 else None
+    dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2, param_policy=policy)
+    dmuon.replicate(m)
+    opt = dmuon.Muon(m, lr=lr, momentum=mu, weight_decay=wd)
+    assert opt._ns.backend == "gram"
+    wdt = "bf16" if dtype == torch.bfloat16 else "fp32"
+    W = [p.detach().float().cpu().numpy().copy() for p in m.parameters()]
+    bufs = [None] * len(shapes)
+    for step in range(2):
+        gs = _grads(m, seed=50 + step)
+        opt.step()
+        for i, (p, g) in enumerate(zip(m.parameters(), gs)):
+            Wr, bufs[i], _ = o.muon_step(W[i], g.float().numpy(), bufs[i], lr=lr, mu=mu, wd=wd,
+                                         coefficients=o.POLAR_EXPRESS, ns="gram", dtype="fp16",
+                                         w_dtype=wdt)
+            dp = dmuon.get_owned_params(m)[i]
+            assert np.array_equal(opt.state[id(dp)]["momentum_buffer"].cpu().numpy(), bufs[i])
+            Wg = p.detach().float().cpu().numpy()
+            base = o.rnd(W[i] * np.float32(1 - lr * wd), wdt)
+            err = o.rel_fro(Wg - base, Wr - base)
+            assert err < (3e-2 if wdt == "bf16" else 2e-2), (step, p.shape, err)
+            W[i] = Wg.copy()
+
+
 # ------------------------------------------------- fp32 master + fused publish (default policy)
 @pytest.mark.parametrize("shapes", [[(256, 512), (256, 512)], [(1000, 300)], [(130, 250)]])
 def test_fp32_master_publish_matches_fp32_weights(gpu, shapes):

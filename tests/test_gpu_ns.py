@@ -20,8 +20,8 @@ from oracle import ns_oracle as o
 pytestmark = pytest.mark.gpu
 
 BF16_TOL = 2e-2       # north-star bf16 gate: relative Frobenius vs the reference pipeline
-SELF_TOL = 1e-2       # GPU vs the CPU restatement of the same bf16 pipeline (accumulation
-                      # order differs; Keller's a=3.44 amplifies tiny-sigma differences)
+SELF_TOL = 1e-2       # GPU vs the CPU restatement of the same pipeline (accumulation order
+                      # differs; Keller's a=3.44 amplifies tiny-sigma differences)
 
 
 def _g(shape, seed, std=0.02):
@@ -54,6 +54,57 @@ def test_gram_ns_default_vs_oracle(gpu, shape):
     assert o.rel_fro(U, ref) < BF16_TOL
     assert o.rel_fro(U, o.closed_form_ns(Gn, o.POLAR_EXPRESS)) < BF16_TOL
     assert np.abs(U - ref).max() < 0.1       # test_newton_schulz.py:40-65 bound
+
+
+@pytest.mark.parametrize("restart", [[2], [], [1, 3], [0, 4]])
+@pytest.mark.parametrize("shape", [(256, 1024), (1024, 256), (1000, 300), (384, 384)])
+def test_gram_device_path_vs_oracle(gpu, shape, restart):
+    """The fp16 Gram-form device algorithm (R = X X^T, Z = cR^2 + bR, Q <- (Z + aI) Q,
+    R <- P R P, restarts) against the reference's fp16 gram_ns, the CPU restatement of the
+    same device pipeline and the closed form."""
+    G = _g(shape, seed=shape[0] + 3 * shape[1])
+    U = dmuon.gram_newton_schulz(G.to(gpu), restart_iterations=restart).cpu().numpy()
+    Gn = G.numpy()
+    e_self = o.rel_fro(U, o.syrk_emulated_gram_ns(Gn, o.POLAR_EXPRESS, restart))
+    e_ref = o.rel_fro(U, o.gram_ns(Gn, o.POLAR_EXPRESS, restart, dtype="fp16"))
+    e_cf = o.rel_fro(U, o.closed_form_ns(Gn, o.POLAR_EXPRESS))
+    print(f"{shape} restarts {restart}: vs fp16 restatement {e_self:.2e}, "
+          f"vs fp16 reference {e_ref:.2e}, vs closed form {e_cf:.2e}")
+    assert e_self < SELF_TOL
+    assert e_ref < BF16_TOL
+    assert e_cf < BF16_TOL
+
+
+def test_gram_batched_keller_and_ragged(gpu):
+    Gs = [_g((256, 640), seed=s) for s in range(3)]
+    outs = newton_schulz_batched([g.to(gpu) for g in Gs], o.KELLER, backend="gram",
+                                 restart_iterations=[2])
+    for g, u in zip(Gs, outs):
+        assert torch.equal(u, newton_schulz_batched([g.to(gpu)], o.KELLER, backend="gram",
+                                                    restart_iterations=[2])[0])
+        ref = o.gram_ns(g.numpy(), o.KELLER, [2], dtype="fp16")
+        assert o.rel_fro(u.cpu().numpy(), ref) < BF16_TOL
+    for shape in [(3, 17), (130, 250), (257, 129)]:
+        G = _g(shape, seed=sum(shape))
+        U = dmuon.gram_newton_schulz(G.to(gpu)).cpu().numpy()
+        assert np.isfinite(U).all() and U.shape == shape
+        assert o.rel_fro(U, o.syrk_emulated_gram_ns(G.numpy())) < SELF_TOL, shape
+    Z = torch.zeros(256, 640, device=gpu)
+    assert torch.count_nonzero(dmuon.gram_newton_schulz(Z)) == 0
+
+
+def test_gram_exact_symmetry_and_fp16_range(gpu):
+    """Large m (many subnormal entries if X were staged unscaled in fp16), tiny and huge input
+    scales (the power-of-two staging keeps them identical up to the normaliser's rounding)."""
+    G = _g((2048, 4096), seed=3)
+    Ug = dmuon.gram_newton_schulz(G.to(gpu))
+    e = o.rel_fro(Ug.cpu().numpy(), o.closed_form_ns(G.numpy(), o.POLAR_EXPRESS))
+    print(f"2048x4096 gram vs closed form {e:.2e}")
+    assert e < 1e-2
+    for k in (1e-6, 1e4):
+        Uk = dmuon.gram_newton_schulz((G * k).to(gpu))
+        assert torch.isfinite(Uk).all()
+        assert ((Uk - Ug).norm() / Ug.norm()).item() < 1e-2, k
 
 
 def test_reference_invariants_on_gpu(gpu):

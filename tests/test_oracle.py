@@ -137,6 +137,64 @@ def test_polar_express_table_matches_published_values():
         np.testing.assert_allclose(got, exp, atol=6e-5)
 
 
+# --- the build's Gram-form restatement: exact recurrence, then its bf16 rounding gap -------
+@pytest.mark.parametrize("restart", [[2], [], [1, 3], [0, 4]])
+@pytest.mark.parametrize("shape", [(24, 64), (64, 24), (32, 32)])
+def test_gram_emulation_matches_closed_form(shape, restart):
+    G = _g(shape, seed=13)
+    cf = o.closed_form_ns(G, o.POLAR_EXPRESS)
+    e32 = o.rel_fro(o.syrk_emulated_gram_ns(G, o.POLAR_EXPRESS, restart, op_dtype="fp32"), cf)
+    assert e32 < 1e-4, e32
+    bf = o.syrk_emulated_gram_ns(G, o.POLAR_EXPRESS, restart)
+    assert o.rel_fro(bf, o.gram_ns(G, o.POLAR_EXPRESS, restart, dtype="fp16")) < 2e-2
+
+
+def _gram_mutant(G, coeffs, restarts, mutation):
+    X, t = o._orient_normalise(G, 1e-7, "fp64")
+    m = X.shape[0]
+    R, Q = X @ X.T, None
+    for i, (a, b, c) in enumerate(coeffs):
+        if i in restarts and i != 0:
+            X = Q @ X
+            if mutation != "stale_R_after_restart":
+                R = X @ X.T
+            Q = None
+        P = a * np.eye(m) + b * R + c * R @ R
+        if mutation == "no_identity":
+            P -= a * np.eye(m)
+        Q = P if Q is None else (Q if mutation == "drop_Q_update" else P @ Q)
+        if i < len(coeffs) - 1 and (i + 1) not in restarts:
+            if mutation == "single_R_factor":
+                R = R @ P
+            elif mutation != "no_R_evolve":
+                R = R @ P @ P
+    X = Q @ X
+    return X.T if t else X
+
+
+@pytest.mark.parametrize("mutation", ["no_R_evolve", "single_R_factor", "stale_R_after_restart",
+                                      "no_identity", "drop_Q_update"])
+def test_planted_gram_mistakes_fail_the_closed_form_pin(mutation):
+    G = _g((24, 72), seed=17)
+    cf = o.closed_form_ns(G, o.POLAR_EXPRESS)
+    restarts = [2]
+    assert o.rel_fro(_gram_mutant(G, o.POLAR_EXPRESS, restarts, None), cf) < 1e-10
+    assert o.rel_fro(_gram_mutant(G, o.POLAR_EXPRESS, restarts, mutation), cf) > 1e-2
+
+
+def test_gram_useful_flops_count_the_schedule():
+    from dmuon_amd.optim.newton_schulz import ns_useful_flops
+    m, n = 4096, 14336
+    sq, mn, qx = m * (m + 1) * m, m * (m + 1) * n, 2.0 * m * m * n
+    ev = 2.0 * m ** 3 + sq
+    # restart at 2, T = 5: 2 Gram and 2 Q X products; Z x5; Q <- P Q at 1, 3, 4; R evolve
+    # after steps 0, 2, 3
+    expect = 2 * (mn + qx) + 5 * sq + 3 * sq + 3 * ev
+    assert ns_useful_flops(m, n, 5, "gram", [2]) == expect
+    assert ns_useful_flops(m, n, 5, "gram", [0, 7]) == (mn + qx) + 5 * sq + 4 * sq + 4 * ev
+    assert ns_useful_flops(m, n, 5) == 5 * (mn + sq + qx)
+
+
 def test_fp16_pipeline_is_close_to_exact():
     G = _g((96, 256), seed=9)
     cf = o.closed_form_ns(G, o.KELLER)
