@@ -36,11 +36,6 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
 
 
-def ns_useful_flops(rows, cols, steps=5):
-    m, n = min(rows, cols), max(rows, cols)
-    return float(steps) * (m * (m + 1) * n + m * (m + 1) * m + 2.0 * m * m * n)
-
-
 def build_matrix_set(torch, device, dtype, n_layers):
     from torch import nn
 
@@ -114,6 +109,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-adamw", action="store_true")
     ap.add_argument("--no-clip", action="store_true")
+    ap.add_argument("--ns", choices=("gram", "direct"), default="gram",
+                    help="gram: the reference Muon's default NS (gram_newton_schulz, "
+                         "Polar-Express coefficients, restart at step 2; fp16 operands); "
+                         "direct: direct_newton_schulz with Keller's constant quintic (bf16)")
     ap.add_argument("--master", choices=("bf16", "fp32"), default="bf16",
                     help="owner master dtype: bf16 = the bf16 weights themselves (c5); fp32 = "
                          "the reference's default policy (fp32 master + fused bf16 publish)")
@@ -148,11 +147,17 @@ def main():
     policy = ({"defaults": {"master_dtype": torch.bfloat16}} if args.master == "bf16" else None)
     dmuon.dedicate_params(model, None, lambda n, p: p.dim() == 2, param_policy=policy)
     dmuon.replicate(model)
-    opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1,
-                     ns_backend=dmuon.NewtonSchulz("direct", coefficients=KELLER))
+    from dmuon_amd.optim.newton_schulz import ns_useful_flops
+
+    if args.ns == "gram":
+        ns = dmuon.NewtonSchulz("gram")                   # Polar-Express, restarts [2]
+    else:
+        ns = dmuon.NewtonSchulz("direct", coefficients=KELLER)
+    opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=ns)
     n_mats = sum(1 for _ in model.parameters())
     n_elems = sum(p.numel() for p in model.parameters())
-    flops = sum(ns_useful_flops(*p.shape) for p in model.parameters())
+    flops = sum(ns_useful_flops(*p.shape, 5, ns.backend, ns.restart_iterations)
+                for p in model.parameters())
 
     for _ in range(args.warmup):
         opt.step()

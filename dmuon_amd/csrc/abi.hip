@@ -161,11 +161,13 @@ int plan(int rows, int cols, int batch, int tile_req, int num_cus, int gram, int
 // Z_i = c_i R^2 + b_i R, one NS step maps X to P_i X, P_i = Z_i + a_i I, so per step
 //   Q <- P_i Q  (Q = P_i after a start or restart), the accumulated polynomial: Z Q^T + a Q
 //   R <- P_i R P_i  when the next step is neither the last nor a restart:
-//        W = Z R + a R  (full product: P R is not symmetric once rounded), R = W Z + a W
+//        W = Z R + a R, R = W Z + a W
 //   restart at step i: X <- Q X, R = X X^T, Q reset;   finally U = Q X / KX
-// The reference writes the R update as (R P) P on triangle tiles; the congruence P (R P) keeps R
-// the Gram matrix of P X to rounding (positive semi-definite), which in fp16 emulation roughly
-// halves the error against the exact polar-factor polynomial. fp16 as in the reference (bf16
+// Every symmetric product (R, Z, W, a fresh Q) is computed on the upper-triangle tiles and
+// stored exactly symmetric (diagonal tiles included), so R R^T = R R and Z R^T = Z R hold to the
+// bit; an R that is symmetric only to rounding costs up to 10x accuracy in fp16 emulation. Q's
+// update is a full product: Q is a product of polynomials that no longer commute once rounded,
+// and symmetrising it costs 3-8x accuracy on square matrices. fp16 as in the reference (bf16
 // loses the small eigenvalues of R). Power-of-two scales keep every operand normal in fp16:
 // X carries KX = 2^12 throughout, the first R (eigenvalues ~1/m) carries kr = 2^floor(log2 m)
 // (at most 2^12) until its first update; all scale changes are folded into alpha / beta.
@@ -301,7 +303,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
       qs = 1 - qs;
     }
     if (evolve) {
-      if (sq(Z, R, R, W, 1.f, ca, 0.f, false)) return 1;              // rs * (P R)
+      if (sq(Z, R, R, W, 1.f, ca, 0.f, true)) return 1;               // rs * (P R)
       if (sq(W, Z, W, R, 1.f / rs, ca / rs, 0.f, true)) return 1;     // P R P
       rs = 1.f;
     }

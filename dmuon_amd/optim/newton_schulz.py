@@ -326,9 +326,9 @@ def ns_useful_flops(rows: int, cols: int, steps: int = 5, backend: str = "direct
 
     direct: T*[m(m+1)n + m(m+1)m + 2 m^2 n].
     gram: (1 + r) m(m+1)n Gram products and r + 1 Q X products (2 m^2 n), r = the restarts
-    inside (0, T); per step m(m+1)m for Z, m(m+1)m for Q <- P Q except right after a (re)start,
-    and, unless the next step is the last or a restart, the R update P R P: 2 m^3 for the full
-    product W = P R plus m(m+1)m for W P."""
+    inside (0, T); per step m(m+1)m for Z, 2 m^3 for Q <- P Q except right after a (re)start,
+    and, unless the next step is the last or a restart, the R update P R P: m(m+1)m each for
+    W = P R and W P. The Q update is a full product: 2 m^3."""
     m, n = min(rows, cols), max(rows, cols)
     sq, gram_mn, qx = m * (m + 1) * m, m * (m + 1) * n, 2.0 * m * m * n
     if backend == "direct":
@@ -338,9 +338,9 @@ def ns_useful_flops(rows: int, cols: int, steps: int = 5, backend: str = "direct
     for i in range(steps):
         total += sq
         if i != 0 and i not in rs:
-            total += sq
+            total += 2.0 * m * m * m
         if i + 1 < steps and (i + 1) not in rs:
-            total += 2.0 * m * m * m + sq
+            total += 2 * sq
     return float(total)
 
 

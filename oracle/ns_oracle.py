@@ -223,7 +223,7 @@ def syrk_emulated_gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
     product of polynomials that no longer commute once rounded, and its order must match R's);
     unless the next step is the last or a restart W = rnd(Z R^T + a R),
     R = rnd(W Z^T / rs + a/rs W), rs = 1; restart: X = rnd(Q X), R = rnd(X X^T / kx^2), rs = 1;
-    U = fp32(Q X / kx). Symmetric results (R, Z, a fresh Q) keep their upper triangle,
+    U = fp32(Q X / kx). Symmetric results (R, Z, W, a fresh Q) keep their upper triangle,
     mirrored."""
     if restart_iterations is None:
         restart_iterations = DEFAULT_RESTART
@@ -272,7 +272,7 @@ def syrk_emulated_gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
         else:
             Q = rnd(epi(_mm(Z, Q, "fp32"), 1.0, Q, a), op_dtype)
         if evolve:
-            W = rnd(epi(_mm(Z, R.T, "fp32"), 1.0, R, a), op_dtype)
+            W = sym(rnd(epi(_mm(Z, R.T, "fp32"), 1.0, R, a), op_dtype))
             R = sym(rnd(epi(_mm(W, Z.T, "fp32"), f32(1.0) / rs, W, f32(a) / rs), op_dtype))
             rs = f32(1.0)
     U = (f32(1.0 / kx) * _mm(Q, Xq, "fp32")).astype(np.float32)

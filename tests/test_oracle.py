@@ -186,12 +186,12 @@ def test_gram_useful_flops_count_the_schedule():
     from dmuon_amd.optim.newton_schulz import ns_useful_flops
     m, n = 4096, 14336
     sq, mn, qx = m * (m + 1) * m, m * (m + 1) * n, 2.0 * m * m * n
-    ev = 2.0 * m ** 3 + sq
-    # restart at 2, T = 5: 2 Gram and 2 Q X products; Z x5; Q <- P Q at 1, 3, 4; R evolve
-    # after steps 0, 2, 3
-    expect = 2 * (mn + qx) + 5 * sq + 3 * sq + 3 * ev
+    ev, qu = 2 * sq, 2.0 * m ** 3
+    # restart at 2, T = 5: 2 Gram and 2 Q X products; Z x5; Q <- P Q (full) at 1, 3, 4;
+    # R evolve (two triangle products) after steps 0, 2, 3
+    expect = 2 * (mn + qx) + 5 * sq + 3 * qu + 3 * ev
     assert ns_useful_flops(m, n, 5, "gram", [2]) == expect
-    assert ns_useful_flops(m, n, 5, "gram", [0, 7]) == (mn + qx) + 5 * sq + 4 * sq + 4 * ev
+    assert ns_useful_flops(m, n, 5, "gram", [0, 7]) == (mn + qx) + 5 * sq + 4 * qu + 4 * ev
     assert ns_useful_flops(m, n, 5) == 5 * (mn + sq + qx)
 
 
