@@ -4,15 +4,18 @@
 Workload (BASELINE config c5): 32 layers x {q, o 4096x4096; k, v 1024x4096; gate, up
 14336x4096; down 4096x14336} = 224 matrices, bf16 weights and gradients ~N(0, 0.02^2), fp32
 momentum, all owned by the single rank; dmuon_amd.Muon(lr=0.02, momentum=0.95 Nesterov,
-weight_decay=0.1) with 5 direct Newton-Schulz steps of Keller's (3.4445, -4.7750, 2.0315).
-A "step" is one optimizer.step() over the set (momentum, normalisation, 5 NS steps, update).
-Synthetic data is generated on the GPU (values do not affect timing).
+weight_decay=0.1) with the reference Muon's default Newton-Schulz: gram_newton_schulz, 5
+Polar-Express steps, restart at step 2, fp16 operands (--ns direct: 5 direct steps of Keller's
+(3.4445, -4.7750, 2.0315) in bf16 instead). A "step" is one optimizer.step() over the set
+(momentum, normalisation, 5 NS steps, update). Synthetic data is generated on the GPU (values
+do not affect timing).
 
 Prints ONE JSON line. Extra fields: per-kernel-class breakdown from the library's hipEvent
 profiler (a second, separately timed pass), the roofline of the dominant kernel family (the
-bf16 MFMA NT kernels: SYRK, SYRK-poly, GEMM) and of the fused momentum kernel, the AdamW
-step for the embeddings/norms (reported separately), and a CPU baseline: the numpy restatement
-of the reference math on the host cores, over a bounded sample of the same workload.
+MFMA NT kernels: Gram / SYRK products, polynomial and Q products, NS GEMM) and of the fused
+momentum kernel, the gradient clip and the AdamW step for the embeddings/norms (reported
+separately), and a CPU baseline: the numpy restatement of the reference math on the host cores,
+over a bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -292,11 +295,15 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp16" if args.ns == "gram" else "bf16",
         "data": "synthetic",
         "config": {"workload": f"Llama-3-8B matrix set: {args.layers} layers x 7 matrices "
                                f"({n_mats} bf16 matrices, {n_elems / 1e9:.2f} G elements), "
-                               "fp32 momentum, 5 direct NS steps (Keller)",
+                               "fp32 momentum, " + (
+                                   "Gram NS (5 Polar-Express steps, restart at 2, fp16 MFMA)"
+                                   if args.ns == "gram" else
+                                   "5 direct NS steps (Keller, bf16 MFMA)"),
+                   "ns_backend": args.ns,
                    "matrices": n_mats, "useful_ns_tflop_per_step": round(flops / 1e12, 2),
                    "master": ("bf16 weights updated in place" if args.master == "bf16" else
                               "fp32 master + bf16 forward copy published in the epilogue"),
@@ -304,7 +311,10 @@ def main():
         "ns_tflops": round(flops / (ms_per_step * 1e-3) / 1e12, 1),
         "ns_frac_mfma_peak_step": round(flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "roofline": {
-            "kernel": "nt_mfma_kernel (SYRK X X^T, SYRK-poly, NS GEMM, final GEMM+update)",
+            "kernel": ("nt_mfma_kernel<..., fp16> (Gram X X^T, R/Z/W triangle products, "
+                       "Q update, restart Q X, final Q X + update)" if args.ns == "gram" else
+                       "nt_mfma_kernel<..., bf16> (SYRK X X^T, SYRK-poly, NS GEMM, final "
+                       "GEMM+update)"),
             "bound": "mfma", "achieved": round(achieved_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved_tf / MFMA_BF16_PEAK_TFLOPS, 4),
             "traffic": traffic,
@@ -312,11 +322,13 @@ def main():
             "launches_per_step": mf_launch // prof_steps,
         },
         "roofline_elementwise": {
-            "kernel": "muon_pre_kernel (momentum + Nesterov + bf16 staging + norm partials)",
+            "kernel": ("muon_pre_kernel: momentum + Nesterov + norm partials, then fp16 "
+                       "staging of ns_in / ||ns_in|| (two passes)" if args.ns == "gram" else
+                       "muon_pre_kernel (momentum + Nesterov + bf16 staging + norm partials)"),
             "bound": "hbm", "achieved": None if pre_gbs is None else round(pre_gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": None if pre_gbs is None else round(pre_gbs / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes_per_elem": 12,
+            "algorithmic_bytes_per_elem": 18 if args.ns == "gram" else 12,
         },
         "kernel_classes": classes,
         "grad_clip": clip,
