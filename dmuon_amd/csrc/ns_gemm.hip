@@ -13,13 +13,11 @@
 // blocks (v_mfma_f32_32x32x16_bf16 or _f16, fp32 accumulate). 256x256 tiles run 8 waves (two per SIMD,
 // so one wave's MFMAs cover the other's LDS and barrier waits); 128x128 tiles run 4 waves with
 // two blocks per CU. K is staged through LDS in
-// BK-wide slices by direct global->LDS DMA (global_load_lds_dwordx4: each wave instruction
+// BK-wide slices by direct global->LDS DMA (buffer_load_dwordx4 ... lds: each wave instruction
 // fills 1 KiB of LDS, no staging registers) into an S-deep ring, so S-1 slices are in flight
 // while one is consumed; the wave waits only for the slice it needs (s_waitcnt vmcnt(N)) and
 // then meets the others at a plain s_barrier. 16-byte chunks sit in LDS under an XOR swizzle
 // (chunk ^ f(row)) chosen so that every 16-lane pass of a fragment read covers all 64 banks.
-#include <stdlib.h>
-
 #include "dmuon_amd_internal.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -565,32 +563,41 @@ void nt_mfma_kernel(const NtArgs a) {
   // writes LDS slot l % CPR of row R0 + l / CPR, so it fetches the global chunk that the
   // swizzle places in that slot (slot() is an involution in its chunk argument).
   const int lrow = lane / T::CPR, lsl = lane % T::CPR;
-  // element offsets from the tile's first row (fixed-size arrays: a template-dependent array
+  // byte offsets from the tile's first row (fixed-size arrays: a template-dependent array
   // bound here makes clang drop the kernel's host launch stub)
   static_assert(T::A_INST <= 8 && T::B_INST <= 8, "DMA instructions per slice");
   unsigned offa[8], offb[8];
 #pragma unroll
   for (int q = 0; q < T::A_INST; ++q) {
     const int r = (T::NW * q + wave) * T::RPI + lrow;
-    offa[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8);
+    offa[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8) * 2u;
   }
 #pragma unroll
   for (int q = 0; q < T::B_INST; ++q) {
     const int r = (T::NW * q + wave) * T::RPI + lrow;
-    offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8);
+    offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
   }
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  // The loads are MUBUF buffer loads into LDS (buffer_load_dwordx4 ... lds): one resource per
+  // operand panel of this tile (SGPR base, range = the panel's rows), 32-bit lane offsets, the
+  // slice offset in soffset. Cheaper to issue than 64-bit-address global loads (measured 1-3%
+  // on the full kernel) and range-checked by the hardware: an offset past the panel reads 0.
+  // Word 3 0x00020000: 32-bit data format, as gfx9 raw buffers use.
+  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(Ab), (short)0, (int)((long long)BM * a.lda * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(Bb), (short)0, (int)((long long)BN * a.ldb * 2), 0x00020000);
   // slice sl_ of A and B into ring slot slot_ (this wave's share)
 #define DMUON_ISSUE(slice_, slot_)                                                             \
   do {                                                                                         \
     char* st_ = smem + (slot_) * T::STAGE + wave * 1024;                                       \
-    const uint16_t* ak_ = Ab + (slice_) * BK;                                                  \
-    const uint16_t* bk_ = Bb + (slice_) * BK;                                                  \
+    const unsigned so_ = (unsigned)((slice_) * BK * 2);                                        \
     _Pragma("unroll") for (int q = 0; q < T::A_INST; ++q)                                      \
-        __builtin_amdgcn_global_load_lds(ak_ + offa[q], (lds_ptr_t)(st_ + q * 1024 * T::NW), 16, 0, 0); \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsA, (lds_ptr_t)(st_ + q * 1024 * T::NW), 16, \
+                                                 offa[q], so_, 0, 0);                          \
     _Pragma("unroll") for (int q = 0; q < T::B_INST; ++q)                                      \
-        __builtin_amdgcn_global_load_lds(bk_ + offb[q], (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * T::NW), \
-                                         16, 0, 0);                                            \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                              \
+            rsB, (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * T::NW), 16, offb[q], so_, 0, 0);    \
   } while (0)
 
   f32x16_t acc[T::TI][T::TJ];
@@ -675,25 +682,12 @@ void nt_mfma_kernel(const NtArgs a) {
   nt_epilogue<T, MODE, E>(a, smem, acc, l, bi, bj, i0, j0, lane, wave, wi, wj);
 }
 
-// K-slice pipeline of the NT kernel: BK-wide slices in an S-deep LDS ring. The default is
-// 64-wide slices double-buffered (one barrier per 64 MFMAs per SIMD); DMUON_NT_PIPE=32x4 selects
-// 32-wide slices four deep (three slices of prefetch, twice the barriers) as a tuning aid.
-int nt_pipe_variant() {
-  static int v = -1;
-  if (v < 0) {
-    const char* e = getenv("DMUON_NT_PIPE");
-    v = (e && e[0] == '3') ? 0 : (e && e[0] == '4') ? 2 : 1;
-  }
-  return v;
-}
-
 }  // namespace
 
 hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   const long long nb = (long long)a.tiles_per_mat * a.L;
   if (nb <= 0) return hipSuccess;
   dim3 grid((unsigned)nb);
-  const int v = nt_pipe_variant();
 #define DMUON_NT(TILE, BK, S, WM, WN, E)                                                       \
   do {                                                                                         \
     dim3 block(64 * WM * WN);                                                                  \
@@ -707,16 +701,14 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
       hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_FINAL, E>), grid,      \
                          block, 0, stream, a);                                                 \
   } while (0)
+  // 64-wide K slices double-buffered; 256-tiles with 8 waves, 128-tiles with 4 (two blocks per
+  // CU). Measured and not kept: 32-wide slices in 3-, 4- and 5-deep rings (the barriers they add
+  // cost what the deeper prefetch saves) and 256-tiles of 4 waves with 128x128 per wave.
   if (a.elt == ELT_F16) {
-    // fp16 operands (the Gram-space iteration): the default pipelines only
     if (tile == 256) DMUON_NT(256, 64, 2, 2, 4, ELT_F16);
     else DMUON_NT(128, 64, 2, 2, 2, ELT_F16);
-  } else if (tile == 256) {
-    if (v == 1) DMUON_NT(256, 64, 2, 2, 4, ELT_BF16);
-    else if (v == 2) DMUON_NT(256, 64, 2, 2, 2, ELT_BF16);
-    else DMUON_NT(256, 32, 4, 2, 4, ELT_BF16);
   } else {
-    if (v == 0) DMUON_NT(128, 32, 4, 2, 2, ELT_BF16);
+    if (tile == 256) DMUON_NT(256, 64, 2, 2, 4, ELT_BF16);
     else DMUON_NT(128, 64, 2, 2, 2, ELT_BF16);
   }
 #undef DMUON_NT
