@@ -62,10 +62,12 @@ def build_matrix_set(torch, device, dtype, n_layers):
     return m
 
 
-def cpu_baseline(budget_s: float = 60.0) -> dict:
+def cpu_baseline(budget_s: float = 60.0, ns: str = "gram") -> dict:
     """Times the oracle (numpy restatement of the reference math, fp32 compute) on the host:
-    momentum + Nesterov + 5 direct NS steps + update for every matrix of layer 0 (q, k, v, o,
-    gate, up, down); the 32-layer step is that time x 32 (all layers have the same shapes)."""
+    momentum + Nesterov + 5 NS steps (the same NS form as the GPU leg: gram_newton_schulz with
+    Polar-Express and a restart at 2, or direct Keller) + update for every matrix of layer 0
+    (q, k, v, o, gate, up, down); the 32-layer step is that time x 32 (all layers have the same
+    shapes)."""
     import numpy as np
 
     from oracle import ns_oracle as o
@@ -83,7 +85,8 @@ def cpu_baseline(budget_s: float = 60.0) -> dict:
         g = rng.standard_normal((rows, cols), dtype=np.float32) * 0.02
         buf = rng.standard_normal((rows, cols), dtype=np.float32) * 0.02
         t0 = time.perf_counter()
-        o.muon_step(W, g, buf, lr=0.02, mu=0.95, wd=0.1, coefficients=o.KELLER, ns="direct",
+        o.muon_step(W, g, buf, lr=0.02, mu=0.95, wd=0.1,
+                    coefficients=o.POLAR_EXPRESS if ns == "gram" else o.KELLER, ns=ns,
                     dtype="fp32")
         dt = time.perf_counter() - t0
         spent += dt
@@ -96,9 +99,9 @@ def cpu_baseline(budget_s: float = 60.0) -> dict:
         "unit": "ms",
         "cores": threads,
         "kind": "port",
-        "sample": ("oracle/ns_oracle.muon_step (numpy, fp32 compute; the reference's fp16 casts "
-                   f"are not emulated) on the 7 matrices of layer 0 = {spent:.1f} s of CPU work; "
-                   "the 32-layer step is extrapolated as 32 x layer 0"),
+        "sample": (f"oracle/ns_oracle.muon_step(ns={ns!r}) (numpy, fp32 compute; the "
+                   "reference's fp16 casts are not emulated) on the 7 matrices of layer 0 = "
+                   f"{spent:.1f} s of CPU work; the 32-layer step is extrapolated as 32 x layer 0"),
         "per_matrix_s": per,
     }
 
@@ -274,7 +277,7 @@ def main():
                               "unit": "GB/s", "frac": round(a_gbs / HBM_PEAK_GBS, 4),
                               "algorithmic_bytes_per_elem": 14}}
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget, args.ns)
 
     # HBM (L2-miss) bytes per NT launch: counters cannot be read from inside this process, so
     # the figure comes from the committed rocprofv3 --pmc summary of this same workload
@@ -282,7 +285,9 @@ def main():
     tpath = os.path.join(HERE, "profiles", "nt_mfma_traffic.json")
     if os.path.exists(tpath) and args.layers == N_LAYERS:
         with open(tpath) as fh:
-            traffic = json.load(fh).get("traffic_bytes_per_launch")
+            tj = json.load(fh)
+        if tj.get("ns_backend") == args.ns:
+            traffic = tj.get("traffic_bytes_per_launch")
 
     out = {
         "metric": "Muon step ms (8B matrix set, 1 GPU); NS TFLOPS + % bf16 MFMA peak",

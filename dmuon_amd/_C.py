@@ -96,7 +96,7 @@ def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args))
 
 
-PROFILE_CLASSES = ("pre", "norm", "syrk", "poly", "gemm", "final", "adamw", "clip")
+PROFILE_CLASSES = ("pre", "norm", "syrk", "poly", "gemm", "final", "adamw", "clip", "diag")
 
 
 def profile_enable(on: bool) -> None:
@@ -105,7 +105,7 @@ def profile_enable(on: bool) -> None:
 
 def profile_collect() -> dict:
     """Per kernel class: {"ms", "launches", "flops", "bytes"} since the last collect."""
-    n = 8
+    n = len(PROFILE_CLASSES)
     ms, cnt = (c_d * n)(), (c_i64 * n)()
     fl, by = (c_d * n)(), (c_d * n)()
     check(lib().dmuon_profile_collect(ms, cnt, fl, by, n))

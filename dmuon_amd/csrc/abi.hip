@@ -87,7 +87,7 @@ Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch, int
 // Single-threaded use only (like the launch path itself). Events are host objects; no device
 // memory is allocated.
 enum ProfClass {
-  PC_PRE = 0, PC_NORM, PC_SYRK, PC_POLY, PC_GEMM, PC_FINAL, PC_ADAMW, PC_CLIP, PC_COUNT
+  PC_PRE = 0, PC_NORM, PC_SYRK, PC_POLY, PC_GEMM, PC_FINAL, PC_ADAMW, PC_CLIP, PC_DIAG, PC_COUNT
 };
 struct ProfRec {
   int cls;
@@ -293,7 +293,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     }
     if (sq(R, R, R, Z, zr2, zr1, 0.f, true)) return 1;   // Z = c R^2 + b R
     if (qs < 0) {
-      if (timed(PC_POLY, 0.0, 4.0 * batch * (double)m_pad * m_pad, stream, who,
+      if (timed(PC_DIAG, 0.0, 4.0 * batch * (double)m_pad * m_pad, stream, who,
                 [&] { return launch_diag_copy(Z, qbuf[0], m_pad, batch, ca, stream); }))
         return 1;
       qtbuf[0] = qbuf[0];
