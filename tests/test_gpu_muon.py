@@ -117,12 +117,18 @@ LLAMA_LAYER = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096),
                (14336, 4096), (14336, 4096), (4096, 14336)]
 
 
-def test_c5_layer_full_size_bit_exact_chain(gpu):
+@pytest.mark.parametrize("backend", ["direct", "gram"])
+def test_c5_layer_full_size_bit_exact_chain(gpu, backend):
     """One Llama-3-8B layer (q,k,v,o,gate,up,down) at full size: momentum bit-exact; the fused
-    weight update equals W*decay - lr*s*U bit for bit, with U from the stand-alone NS entry."""
+    weight update equals W*decay - lr*s*U bit for bit, with U from the stand-alone NS entry
+    (the same device algorithm: direct Keller, or Gram with the reference defaults)."""
     lr, mu, wd = 0.02, 0.95, 0.1
-    m, opt = _setup(LLAMA_LAYER, torch.bfloat16, gpu, BF16_MASTER, lr=lr, momentum=mu,
-                    weight_decay=wd)
+    m = Mats(LLAMA_LAYER, torch.bfloat16, gpu)
+    dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2, param_policy=BF16_MASTER)
+    dmuon.replicate(m)
+    ns = (dmuon.NewtonSchulz("direct", coefficients=dmuon.KELLER_COEFFICIENTS)
+          if backend == "direct" else dmuon.NewtonSchulz("gram"))
+    opt = dmuon.Muon(m, ns_backend=ns, lr=lr, momentum=mu, weight_decay=wd)
     ps = list(m.parameters())
     dps = dmuon.get_owned_params(m)
     # step 1 establishes the momentum buffers
@@ -141,7 +147,8 @@ def test_c5_layer_full_size_bit_exact_chain(gpu):
         for i, b in zip(idx, nb):
             assert torch.equal(opt.state[id(dps[i])]["momentum_buffer"], b), shape
         ns_in = [gs[i].float() + b * mu for i, b in zip(idx, nb)]
-        U = newton_schulz_batched(ns_in, dmuon.KELLER_COEFFICIENTS)
+        U = newton_schulz_batched(ns_in, ns.resolved_coefficients(), backend=ns.backend,
+                                  restart_iterations=ns.restart_iterations)
         rows, cols = shape
         decay = 1.0 - lr * wd
         lrs = lr * 0.2 * math.sqrt(max(rows, cols))

@@ -188,3 +188,52 @@ def test_full_size_properties(gpu, shape):
         err = _spectrum_check(G.float(), U)
         print(f"{shape}: spectrum error {err:.2e}")
         assert err < BF16_TOL
+
+
+def _closed_form_gpu(G, coeffs, eps=1e-7):
+    """Exact NS output in fp64 through an eigendecomposition of X X^T (X = the oriented,
+    normalised input): U = V diag(f(s)/s) V^T X, s = sqrt(eig), f the composed polynomial
+    (f(s)/s -> prod(a) as s -> 0). Independent of both device algorithms."""
+    X = G.double()
+    t = X.shape[0] > X.shape[1]
+    if t:
+        X = X.t()
+    X = X / (X.norm() + eps)
+    lam, V = torch.linalg.eigh(X @ X.t())
+    s = lam.clamp_min(0).sqrt()
+    f = torch.from_numpy(o.poly_compose(s.cpu().numpy(), coeffs)).to(X.device)
+    a0 = float(np.prod([c[0] for c in coeffs]))
+    ratio = torch.where(s > 1e-9, f / s.clamp_min(1e-300), torch.full_like(s, a0))
+    U = (V * ratio) @ (V.t() @ X)
+    return U.t() if t else U
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096), (1024, 16384), (16384, 1024), (2048, 8192),
+                                   (4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("backend", ["gram", "direct"])
+def test_full_size_vs_exact(gpu, shape, backend):
+    """c3 / c5 shapes at full size against the exact fp64 result of the same polynomial:
+    Gram NS with the reference defaults (Polar-Express, restart at 2), direct with Keller."""
+    G = _g(shape, seed=5).to(torch.bfloat16).to(gpu)
+    coeffs = o.POLAR_EXPRESS if backend == "gram" else o.KELLER
+    U = newton_schulz_batched([G.float()], coeffs, backend=backend, restart_iterations=[2])[0]
+    ref = _closed_form_gpu(G.float(), coeffs)
+    err = ((U.double() - ref).norm() / ref.norm()).item()
+    print(f"{backend} {shape}: vs exact {err:.2e}")
+    assert err < BF16_TOL
+
+
+def test_moe_batch_gram_full_size(gpu):
+    """c4: 64 gate/up (1408 x 2048) + 64 down (2048 x 1408) expert matrices through the grouped
+    Gram path; a sample of each bucket against the exact result, batched == single."""
+    Gs = [_g((1408, 2048), seed=100 + i).to(gpu) for i in range(64)]
+    Ds = [_g((2048, 1408), seed=200 + i).to(gpu) for i in range(64)]
+    for mats in (Gs, Ds):
+        outs = newton_schulz_batched(mats, o.POLAR_EXPRESS, backend="gram", restart_iterations=[2])
+        for i in (0, 37, 63):
+            ref = _closed_form_gpu(mats[i], o.POLAR_EXPRESS)
+            err = ((outs[i].double() - ref).norm() / ref.norm()).item()
+            assert err < BF16_TOL, (mats[i].shape, i, err)
+        single = newton_schulz_batched([mats[37]], o.POLAR_EXPRESS, backend="gram",
+                                       restart_iterations=[2])[0]
+        assert torch.equal(single, outs[37])
