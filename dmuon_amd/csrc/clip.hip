@@ -8,7 +8,8 @@
 // numels[t]); one 256-thread block per job. Tensor dtypes use the reference's codes
 // (0 fp32, 1 fp16, 2 bf16; fast_clip.py:31-35). Where the reference walks a job with one
 // scalar load per thread and reduces through a shared-memory tree, here the aligned middle of
-// the job is read in 16-byte vectors (4 fp32 / 8 half-precision values per lane), the partial
+// the job is read in 16-byte vectors (4 fp32 / 8 half-precision values per lane; the norm pass
+// keeps four non-temporal loads in flight per lane, the scale pass two vectors), the partial
 // sums are reduced across the wave with cross-lane shuffles and across the four waves through
 // a 16-byte LDS array, and one lane per block adds the block's sum into local_sq with a
 // global float atomic (so, as in the reference, the order of those additions -- and hence the
@@ -74,8 +75,36 @@ __device__ float job_sumsq(const void* p, long long begin, long long end) {
     vs = min((begin + V - 1) / V * V, end);
     ve = max(end / V * V, vs);
   }
-  float s = 0.f;
-  for (long long i = vs + (long long)V * threadIdx.x; i < ve; i += (long long)V * 256) {
+  // four 16-byte loads in flight per thread, four partial sums
+  float s4[4] = {0.f, 0.f, 0.f, 0.f};
+  long long i = vs + (long long)V * threadIdx.x;
+  for (; i + 3LL * V * 256 < ve; i += 4LL * V * 256) {
+    u32x4_t w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if constexpr (D == CF32) w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(static_cast<const float*>(p) + i + u * V * 256));
+      else w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + i + u * V * 256));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if constexpr (D == CF32) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float x = __uint_as_float(w[u][k]);
+          s4[u] += x * x;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float x0 = to_f<D>(w[u][k] & 0xffff), x1 = to_f<D>(w[u][k] >> 16);
+          s4[u] += x0 * x0;
+          s4[u] += x1 * x1;
+        }
+      }
+    }
+  }
+  float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  for (; i < ve; i += (long long)V * 256) {
     if constexpr (D == CF32) {
       const u32x4_t w = *reinterpret_cast<const u32x4_t*>(static_cast<const float*>(p) + i);
 #pragma unroll
@@ -110,21 +139,31 @@ __device__ void job_scale(void* p, long long begin, long long end, float c) {
     vs = min((begin + V - 1) / V * V, end);
     ve = max(end / V * V, vs);
   }
-  for (long long i = vs + (long long)V * threadIdx.x; i < ve; i += (long long)V * 256) {
+  // two 16-byte vectors per thread per iteration (both loads before either store)
+  auto sc = [&](u32x4_t w) {
     if constexpr (D == CF32) {
-      u32x4_t* q = reinterpret_cast<u32x4_t*>(static_cast<float*>(p) + i);
-      u32x4_t w = *q;
 #pragma unroll
       for (int k = 0; k < 4; ++k) w[k] = __float_as_uint(__uint_as_float(w[k]) * c);
-      *q = w;
     } else {
-      u32x4_t* q = reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p) + i);
-      u32x4_t w = *q;
 #pragma unroll
       for (int k = 0; k < 4; ++k)
         w[k] = from_f<D>(to_f<D>(w[k] & 0xffff) * c) | (from_f<D>(to_f<D>(w[k] >> 16) * c) << 16);
-      *q = w;
     }
+    return w;
+  };
+  u32x4_t* base = D == CF32 ? reinterpret_cast<u32x4_t*>(static_cast<float*>(p))
+                            : reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p));
+  long long i = vs + (long long)V * threadIdx.x;
+  for (; i + (long long)V * 256 < ve; i += 2LL * V * 256) {
+    u32x4_t* q0 = base + i / V;
+    u32x4_t* q1 = base + (i + (long long)V * 256) / V;
+    const u32x4_t w0 = *q0, w1 = *q1;
+    *q0 = sc(w0);
+    *q1 = sc(w1);
+  }
+  for (; i < ve; i += (long long)V * 256) {
+    u32x4_t* q = base + i / V;
+    *q = sc(*q);
   }
   const long long nh = vs - begin, nt = end - ve;
   for (long long k = threadIdx.x; k < nh + nt; k += 256)
