@@ -312,27 +312,37 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
 }
 
 // The whole Newton-Schulz + optional update sequence of one group; see dmuon_muon_step_group.
+// phases: PH_STAGE (momentum, norm, NS operand staging into the workspace), PH_APPLY (the NS
+// products and the fused update / output from a staged workspace), or both.
+enum { PH_STAGE = 1, PH_APPLY = 2 };
 int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* const* w_ptrs,
               int w_dtype, void* const* pub_ptrs, int pub_dtype, void* const* out_ptrs,
               int out_dtype, int rows, int cols, int batch,
               float mu, int nesterov, int first_step, float decay, float lrs, const float* coeffs,
               int T, int backend, const int* restarts, int n_restarts, float eps, void* workspace,
-              int64_t workspace_bytes, int tile_req, hipStream_t stream, const char* who) {
-  if (!g_ptrs) return fail("%s: g_ptrs is NULL", who);
-  if (g_dtype != DMUON_DTYPE_F32 && g_dtype != DMUON_DTYPE_BF16)
-    return fail("%s: unsupported gradient dtype code %d", who, g_dtype);
-  if (w_ptrs && w_dtype != DMUON_DTYPE_F32 && w_dtype != DMUON_DTYPE_BF16)
-    return fail("%s: unsupported weight dtype code %d", who, w_dtype);
-  if (out_ptrs && out_dtype != DMUON_DTYPE_F32 && out_dtype != DMUON_DTYPE_BF16)
-    return fail("%s: unsupported output dtype code %d", who, out_dtype);
-  if (pub_ptrs && !w_ptrs) return fail("%s: pub_ptrs needs w_ptrs (it copies the new W)", who);
-  if (pub_ptrs && pub_dtype != DMUON_DTYPE_F32 && pub_dtype != DMUON_DTYPE_BF16)
-    return fail("%s: unsupported publish dtype code %d", who, pub_dtype);
-  if (!coeffs || T <= 0) return fail("%s: need at least one (a, b, c) coefficient triple", who);
+              int64_t workspace_bytes, int tile_req, hipStream_t stream, const char* who,
+              int phases = PH_STAGE | PH_APPLY) {
+  const bool do_stage = phases & PH_STAGE, do_apply = phases & PH_APPLY;
+  if (do_stage) {
+    if (!g_ptrs) return fail("%s: g_ptrs is NULL", who);
+    if (g_dtype != DMUON_DTYPE_F32 && g_dtype != DMUON_DTYPE_BF16)
+      return fail("%s: unsupported gradient dtype code %d", who, g_dtype);
+  }
+  if (do_apply) {
+    if (w_ptrs && w_dtype != DMUON_DTYPE_F32 && w_dtype != DMUON_DTYPE_BF16)
+      return fail("%s: unsupported weight dtype code %d", who, w_dtype);
+    if (out_ptrs && out_dtype != DMUON_DTYPE_F32 && out_dtype != DMUON_DTYPE_BF16)
+      return fail("%s: unsupported output dtype code %d", who, out_dtype);
+    if (pub_ptrs && !w_ptrs) return fail("%s: pub_ptrs needs w_ptrs (it copies the new W)", who);
+    if (pub_ptrs && pub_dtype != DMUON_DTYPE_F32 && pub_dtype != DMUON_DTYPE_BF16)
+      return fail("%s: unsupported publish dtype code %d", who, pub_dtype);
+    if (!coeffs || T <= 0)
+      return fail("%s: need at least one (a, b, c) coefficient triple", who);
+    if (n_restarts < 0 || (n_restarts > 0 && !restarts))
+      return fail("%s: restart list NULL or of negative length", who);
+  }
   if (backend != DMUON_NS_DIRECT && backend != DMUON_NS_GRAM)
     return fail("%s: unknown NS backend %d", who, backend);
-  if (n_restarts < 0 || (n_restarts > 0 && !restarts))
-    return fail("%s: restart list NULL or of negative length", who);
   const int gram = backend == DMUON_NS_GRAM;
   if (!workspace || !aligned16(workspace)) return fail("%s: workspace NULL or misaligned", who);
   int tile, m_pad, n_pad;
@@ -369,6 +379,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
   p.stage = gram ? PRE_NORM : PRE_BF16;
   const double Ld = batch, md = m, nd = n, elems = (double)rows * cols * batch;
   const double gbytes = g_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0;
+  if (do_stage) {
   // algorithmic bytes: gradient read, fp32 momentum read (not on the first step) and write,
   // one 16-bit copy of ns_in (direct); the Gram staging has no copy in its first pass and
   // reads the gradient and the new momentum again in the second
@@ -387,6 +398,8 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
     if (timed(PC_PRE, 0.0, st_bytes, stream, who, [&] { return launch_pre(p, stream); }))
       return 1;
   }
+  }  // do_stage
+  if (!do_apply) return 0;
   const double syrk_flops = Ld * md * (md + 1) * nd, poly_flops = Ld * md * (md + 1) * md;
   const double gemm_flops = 2.0 * Ld * md * md * nd;
   const double wbytes = w_ptrs ? 2.0 * elems * (w_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0) : 0.0;
@@ -769,6 +782,36 @@ int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out
                    cols, batch, 0.f, 0, 1, 1.f, 0.f, coeffs, T, backend, restarts, n_restarts,
                    eps, workspace, workspace_bytes, tile,
                    static_cast<hipStream_t>(stream), who);
+}
+
+int dmuon_muon_stage_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, int rows,
+                           int cols, int batch, double mu, int nesterov, int first_step,
+                           int backend, float eps, void* workspace, int64_t workspace_bytes,
+                           int tile, void* stream) {
+  const char* who = "dmuon_muon_stage_group";
+  if (batch == 0) return 0;
+  if (!buf_ptrs) return fail("%s: buf_ptrs must be non-NULL", who);
+  return run_group(g_ptrs, g_dtype, buf_ptrs, nullptr, 0, nullptr, 0, nullptr, 0, rows, cols,
+                   batch, (float)mu, nesterov, first_step, 1.f, 0.f, nullptr, 0, backend,
+                   nullptr, 0, eps, workspace, workspace_bytes, tile,
+                   static_cast<hipStream_t>(stream), who, PH_STAGE);
+}
+
+int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_ptrs,
+                           int pub_dtype, int rows, int cols, int batch, double lr, double wd,
+                           const float* coeffs, int T, int backend, const int* restarts,
+                           int n_restarts, void* workspace, int64_t workspace_bytes, int tile,
+                           void* stream) {
+  const char* who = "dmuon_muon_apply_group";
+  if (batch == 0) return 0;
+  if (!w_ptrs) return fail("%s: w_ptrs must be non-NULL", who);
+  const double scale = 0.2 * sqrt((double)(rows > cols ? rows : cols));
+  const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
+  const float lrs = (float)(lr * scale);
+  return run_group(nullptr, 0, nullptr, w_ptrs, w_dtype, pub_ptrs, pub_dtype, nullptr, 0, rows,
+                   cols, batch, 0.f, 0, 0, decay, lrs, coeffs, T, backend, restarts, n_restarts,
+                   0.f, workspace, workspace_bytes, tile, static_cast<hipStream_t>(stream), who,
+                   PH_APPLY);
 }
 
 }  // extern "C"

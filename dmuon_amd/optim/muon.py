@@ -53,8 +53,11 @@ class Muon(torch.optim.Optimizer):
     Extra keyword arguments of the reference that concern multi-rank scheduling
     (``replicate_async``, ``group_prepare_ahead``, ``tp_distributed_gram*``,
     ``post_step_prefetch_*``, ``forward_prefetch_depth``, ...) are accepted and have no effect
-    at world_size=1. ``workspace_limit_bytes`` bounds the NS scratch (a bucket of same-shape
-    matrices is processed in chunks that fit).
+    at world_size=1. ``workspace_limit_bytes`` bounds the NS scratch of one chunk (a bucket of
+    same-shape matrices is processed in chunks that fit); ``overlap_staging=True`` stages the
+    next chunk on a side stream while the current chunk's NS runs, with two such workspaces
+    (bit-identical results; off by default: on MI355X the concurrent staging traffic slows the
+    MFMA kernels by about as much as it hides).
     """
 
     def __init__(
@@ -74,6 +77,7 @@ class Muon(torch.optim.Optimizer):
         record_step_profile: bool = False,
         workspace_limit_bytes: int = 8 << 30,
         ns_eps: float = 1e-7,
+        overlap_staging: bool = False,
         **kwargs,
     ):
         if isinstance(ns_backend, str):
@@ -94,7 +98,9 @@ class Muon(torch.optim.Optimizer):
         self._ns_eps = float(ns_eps)
         self._record_step_profile = bool(record_step_profile)
         self._workspace_limit = int(workspace_limit_bytes)
-        self._workspace: Optional[Tensor] = None
+        self._workspaces: list = [None, None]
+        self._overlap_staging = bool(overlap_staging)
+        self._side_streams: dict = {}
         self._last_step_profile: dict = {}
         self._optimizer_step_index = 0
 
@@ -260,52 +266,89 @@ class Muon(torch.optim.Optimizer):
         return buckets
 
     def _step_muon_group(self, group) -> tuple[int, int]:
+        """One Muon group: its same-shape buckets, each split into chunks that fit a workspace.
+
+        Each chunk is staged (momentum, norm, NS operands: bandwidth-bound) and then applied
+        (NS products + fused update: MFMA-bound). With ``overlap_staging`` the chunks run as a
+        two-slot pipeline: chunk k+1 is staged on a side stream into the other workspace while
+        chunk k's NS runs on the current stream. Events order every hand-over; the results are
+        bit-identical to the one-stream sequence.
+        """
         lr, mu, wd = float(group["lr"]), float(group["momentum"]), float(group["weight_decay"])
         coeffs, T = _coeff_array(self._ns.resolved_coefficients())
         backend = _backend_code(self._ns.backend)
         rst, n_rst = _C.restart_array(self._ns.restart_codes())
+        chunks = []
         count = numel = 0
         for (rows, cols, gdt, wdt, pdt, dev, first), items in self._buckets(group).items():
             _require_cuda(dev)
-            L_all = len(items)
             num_cus = torch.cuda.get_device_properties(dev).multi_processor_count
-            chunk = self._chunk_size(rows, cols, L_all, num_cus, backend)
-            for s in range(0, L_all, chunk):
-                part = items[s:s + chunk]
-                L = len(part)
-                tile, _, _, nbytes = _C.plan(rows, cols, L, 0, num_cus, backend)
-                ws = self._get_workspace(dev, nbytes)
-                gs, bufs, ws_, pubs = [], [], [], []
-                for dp, g in part:
+            chunk = self._chunk_size(rows, cols, len(items), num_cus, backend)
+            for s0 in range(0, len(items), chunk):
+                part = items[s0:s0 + chunk]
+                for dp, _ in part:
                     st = self.state[id(dp)]
                     if "momentum_buffer" not in st:
                         st["momentum_buffer"] = torch.zeros((rows, cols), dtype=torch.float32,
                                                             device=dev)
-                    if not g.is_contiguous():
-                        g = g.contiguous()
-                    W = dp._owned_data
-                    if not W.is_contiguous():
+                    if not dp._owned_data.is_contiguous():
                         raise RuntimeError(f"{dp.param_name}: Muon needs a contiguous weight")
-                    gs.append(g)
-                    bufs.append(st["momentum_buffer"])
-                    ws_.append(W)
-                    if pdt is not None:
-                        pubs.append(dp.publish_target())
-                ptrs = _pinned_ptrs([t.data_ptr() for t in gs] + [t.data_ptr() for t in bufs]
-                                    + [t.data_ptr() for t in ws_]
-                                    + [t.data_ptr() for t in pubs], dev)
-                base = ptrs.data_ptr()
-                stream = torch.cuda.current_stream(dev).cuda_stream
-                # the forward copies (master != parameter) are written by the same epilogue
-                pub_base = base + 24 * L if pubs else None
-                pub_code = _float_dtype_code(pubs[0]) if pubs else 0
-                _C.call("dmuon_muon_step_group", base, _float_dtype_code(gs[0]), base + 8 * L,
-                        base + 16 * L, _float_dtype_code(ws_[0]), pub_base, pub_code, rows, cols,
-                        L, lr, mu, wd, int(self._nesterov), int(first), coeffs, T, backend, rst,
-                        n_rst, self._ns_eps, ws.data_ptr(), ws.numel(), tile, stream)
-                count += L
-                numel += L * rows * cols
-            for dp, _ in items:
+                tile, _, _, nbytes = _C.plan(rows, cols, len(part), 0, num_cus, backend)
+                chunks.append((rows, cols, dev, first, pdt is not None, part, tile, nbytes))
+                count += len(part)
+                numel += len(part) * rows * cols
+        if not chunks:
+            return 0, 0
+        dev = chunks[0][2]
+        main = torch.cuda.current_stream(dev)
+        overlap = self._overlap_staging and len(chunks) > 1
+        side = self._side_stream(dev) if overlap else main
+        # both workspaces exist before the hand-over event, so no block the side stream writes
+        # can still be in use by later work on `main`
+        nslots = 2 if overlap else 1
+        wss = [self._get_workspace(dev, max(c[7] for k, c in enumerate(chunks)
+                                            if k % nslots == sl), sl)
+               for sl in range(min(nslots, len(chunks)))]
+        if overlap:
+            start = torch.cuda.Event()
+            start.record(main)           # gradients, buffers and weights are ready on `main`
+            side.wait_event(start)
+        free = [None, None]
+        for k, (rows, cols, dev, first, has_pub, part, tile, nbytes) in enumerate(chunks):
+            slot = k % nslots
+            ws = wss[slot]
+            L = len(part)
+            with torch.cuda.stream(side):
+                if free[slot] is not None:
+                    side.wait_event(free[slot])
+                # contiguous copies (if any) on the staging stream, ordered before the staging
+                gs = [g if g.is_contiguous() else g.contiguous() for _, g in part]
+                ptrs = _pinned_ptrs([t.data_ptr() for t in gs]
+                                    + [self.state[id(dp)]["momentum_buffer"].data_ptr()
+                                       for dp, _ in part], dev)
+                _C.call("dmuon_muon_stage_group", ptrs.data_ptr(), _float_dtype_code(gs[0]),
+                        ptrs.data_ptr() + 8 * L, rows, cols, L, mu, int(self._nesterov),
+                        int(first), backend, self._ns_eps, ws.data_ptr(), ws.numel(), tile,
+                        side.cuda_stream)
+                if overlap:
+                    staged = torch.cuda.Event()
+                    staged.record(side)
+            if overlap:
+                main.wait_event(staged)
+            W = [dp._owned_data for dp, _ in part]
+            pubs = [dp.publish_target() for dp, _ in part] if has_pub else []
+            wptrs = _pinned_ptrs([t.data_ptr() for t in W] + [t.data_ptr() for t in pubs], dev)
+            # the forward copies (master != parameter) are written by the same epilogue
+            _C.call("dmuon_muon_apply_group", wptrs.data_ptr(), _float_dtype_code(W[0]),
+                    wptrs.data_ptr() + 8 * L if pubs else None,
+                    _float_dtype_code(pubs[0]) if pubs else 0, rows, cols, L, lr, wd, coeffs, T,
+                    backend, rst, n_rst, ws.data_ptr(), ws.numel(), tile, main.cuda_stream)
+            if overlap:
+                done = torch.cuda.Event()
+                done.record(main)
+                free[slot] = done
+        for _, _, _, _, _, part, _, _ in chunks:
+            for dp, _ in part:
                 dp._reduced_grad = None
         return count, numel
 
@@ -317,13 +360,20 @@ class Muon(torch.optim.Optimizer):
             chunk -= 1
         return chunk
 
-    def _get_workspace(self, device, nbytes: int) -> Tensor:
-        ws = self._workspace
+    def _get_workspace(self, device, nbytes: int, slot: int = 0) -> Tensor:
+        ws = self._workspaces[slot]
         if ws is None or ws.device != device or ws.numel() < nbytes:
-            self._workspace = None
+            self._workspaces[slot] = None
             ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
-            self._workspace = ws
+            self._workspaces[slot] = ws
         return ws
+
+    def _side_stream(self, device) -> "torch.cuda.Stream":
+        s = self._side_streams.get(device)
+        if s is None:
+            s = torch.cuda.Stream(device=device)       # default priority
+            self._side_streams[device] = s
+        return s
 
     # ------------------------------------------------------------------ AdamW
     def _step_adamw_group(self, group) -> None:

@@ -29,6 +29,7 @@
  *                                                                   orientation, cast, ||X||^2
  *   dmuon_norm_finalize      dmuon/optim/newton_schulz.py:265       X / (X.norm() + eps)
  *   dmuon_muon_update        dmuon/optim/muon.py:1728-1740          owned.mul_/add_ update
+ *   dmuon_muon_stage_group / dmuon_muon_apply_group  the two halves of dmuon_muon_step_group
  *   dmuon_muon_step_group    dmuon/optim/muon.py:1683-1740          one owner's per-param Muon
  *                                                                   math for `batch` same-shape
  *                                                                   params (direct NS, T steps)
@@ -179,6 +180,29 @@ int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_pt
                           int nesterov, int first_step, const float* coeffs, int T, int backend,
                           const int* restarts, int n_restarts, float eps, void* workspace,
                           int64_t workspace_bytes, int tile, void* stream);
+
+/*
+ * dmuon_muon_step_group in two halves, for callers that overlap the bandwidth-bound half of one
+ * group with the MFMA-bound half of another on two streams (each half enqueues on its own
+ * stream; order them with events):
+ *   stage: momentum (+Nesterov), the Frobenius norm and the NS operands of `batch` params,
+ *          written into `workspace`;
+ *   apply: the NS products from that staged workspace and the fused weight update (+ optional
+ *          forward copy), as dmuon_muon_step_group's second half.
+ * Both calls of one group must pass the same rows, cols, batch, backend, tile and workspace; the
+ * workspace must not be staged again before its apply has run. Results equal
+ * dmuon_muon_step_group's bit for bit. No reference counterpart (the reference runs the step
+ * per parameter on one stream); it serves the same seam, muon.py:1683-1740.
+ */
+int dmuon_muon_stage_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, int rows,
+                           int cols, int batch, double mu, int nesterov, int first_step,
+                           int backend, float eps, void* workspace, int64_t workspace_bytes,
+                           int tile, void* stream);
+int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_ptrs,
+                           int pub_dtype, int rows, int cols, int batch, double lr, double wd,
+                           const float* coeffs, int T, int backend, const int* restarts,
+                           int n_restarts, void* workspace, int64_t workspace_bytes, int tile,
+                           void* stream);
 
 /* direct_newton_schulz / gram_newton_schulz (by `backend`, as above) for `batch` same-shape
  * rows x cols matrices: out[l] <- NS(g[l]). */

@@ -192,6 +192,33 @@ def test_default_gram_backend_step(gpu, shapes, dtype):
             W[i] = Wg.copy()
 
 
+# ------------------------------------------- staged pipeline (side-stream staging) vs one stream
+@pytest.mark.parametrize("backend", ["gram", "direct"])
+def test_overlapped_staging_is_bit_identical(gpu, backend):
+    """Small workspaces force several chunks per bucket; the two-slot pipeline (staging on a
+    side stream) must give exactly the weights and momentum buffers of the one-stream run."""
+    shapes = [(256, 640)] * 5 + [(640, 256)] * 3 + [(512, 512)] * 4 + [(130, 250)] * 2
+    runs = []
+    for overlap in (False, True):
+        m = Mats(shapes, torch.bfloat16, gpu, seed=3)
+        dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2)        # fp32 masters + publish
+        dmuon.replicate(m)
+        opt = dmuon.Muon(m, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=backend,
+                         workspace_limit_bytes=6 << 20, overlap_staging=overlap)
+        assert opt._overlap_staging == overlap
+        for step in range(3):
+            _grads(m, seed=70 + step)
+            opt.step()
+        torch.cuda.synchronize()
+        dps = dmuon.get_owned_params(m)
+        runs.append(([p.detach().clone() for p in m.parameters()],
+                     [dp._owned_data.clone() for dp in dps],
+                     [opt.state[id(dp)]["momentum_buffer"].clone() for dp in dps]))
+    for a, b in zip(runs[0], runs[1]):
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+
+
 # ------------------------------------------------- fp32 master + fused publish (default policy)
 @pytest.mark.parametrize("shapes", [[(256, 512), (256, 512)], [(1000, 300)], [(130, 250)]])
 def test_fp32_master_publish_matches_fp32_weights(gpu, shapes):
