@@ -6,7 +6,7 @@ Workload (BASELINE config c5): 32 layers x {q, o 4096x4096; k, v 1024x4096; gate
 momentum, all owned by the single rank; dmuon_amd.Muon(lr=0.02, momentum=0.95 Nesterov,
 weight_decay=0.1) with the reference Muon's default Newton-Schulz: gram_newton_schulz, 5
 Polar-Express steps, restart at step 2, fp16 operands (--ns direct: 5 direct steps of Keller's
-(3.4445, -4.7750, 2.0315) in bf16 instead). A "step" is one optimizer.step() over the set
+(3.4445, -4.7750, 2.0315) instead, also fp16). A "step" is one optimizer.step() over the set
 (momentum, normalisation, 5 NS steps, update). Synthetic data is generated on the GPU (values
 do not affect timing).
 
@@ -118,7 +118,7 @@ def main():
     ap.add_argument("--ns", choices=("gram", "direct"), default="gram",
                     help="gram: the reference Muon's default NS (gram_newton_schulz, "
                          "Polar-Express coefficients, restart at step 2; fp16 operands); "
-                         "direct: direct_newton_schulz with Keller's constant quintic (bf16)")
+                         "direct: direct_newton_schulz with Keller's constant quintic (fp16)")
     ap.add_argument("--master", choices=("bf16", "fp32"), default="bf16",
                     help="owner master dtype: bf16 = the bf16 weights themselves (c5); fp32 = "
                          "the reference's default policy (fp32 master + fused bf16 publish)")
@@ -300,14 +300,14 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16" if args.ns == "gram" else "bf16",
+        "dtype": "fp16",
         "data": "synthetic",
         "config": {"workload": f"Llama-3-8B matrix set: {args.layers} layers x 7 matrices "
                                f"({n_mats} bf16 matrices, {n_elems / 1e9:.2f} G elements), "
                                "fp32 momentum, " + (
                                    "Gram NS (5 Polar-Express steps, restart at 2, fp16 MFMA)"
                                    if args.ns == "gram" else
-                                   "5 direct NS steps (Keller, bf16 MFMA)"),
+                                   "5 direct NS steps (Keller, fp16 MFMA)"),
                    "ns_backend": args.ns,
                    "matrices": n_mats, "useful_ns_tflop_per_step": round(flops / 1e12, 2),
                    "master": ("bf16 weights updated in place" if args.master == "bf16" else
@@ -318,7 +318,7 @@ def main():
         "roofline": {
             "kernel": ("nt_mfma_kernel<..., fp16> (Gram X X^T, R/Z/W triangle products, "
                        "Q update, restart Q X, final Q X + update)" if args.ns == "gram" else
-                       "nt_mfma_kernel<..., bf16> (SYRK X X^T, SYRK-poly, NS GEMM, final "
+                       "nt_mfma_kernel<..., fp16> (SYRK X X^T, SYRK-poly, NS GEMM, final "
                        "GEMM+update)"),
             "bound": "mfma", "achieved": round(achieved_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved_tf / MFMA_BF16_PEAK_TFLOPS, 4),
@@ -328,12 +328,11 @@ def main():
         },
         "roofline_elementwise": {
             "kernel": ("muon_pre_kernel: momentum + Nesterov + norm partials, then fp16 "
-                       "staging of ns_in / ||ns_in|| (two passes)" if args.ns == "gram" else
-                       "muon_pre_kernel (momentum + Nesterov + bf16 staging + norm partials)"),
+                       "staging of ns_in / ||ns_in|| (two passes)"),
             "bound": "hbm", "achieved": None if pre_gbs is None else round(pre_gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": None if pre_gbs is None else round(pre_gbs / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes_per_elem": 18 if args.ns == "gram" else 12,
+            "algorithmic_bytes_per_elem": 18,
         },
         "kernel_classes": classes,
         "grad_clip": clip,

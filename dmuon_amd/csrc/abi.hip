@@ -39,8 +39,9 @@ bool stride_ok(int64_t s, int batch) { return batch <= 1 || (s >= 0 && (s % 8) =
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 int64_t align256(int64_t b) { return round_up(b, 256); }
 
-// Power-of-two scale of the fp16 Gram-NS operand X (entries of the normalised X are at most 1)
-constexpr float kGramKx = 4096.f;
+// Power-of-two scale of the fp16 NS operand X, both backends (entries of the normalised X are at
+// most 1; the scale keeps the typical ~1/sqrt(mn) entries out of the fp16 subnormal range)
+constexpr float kNsKx = 4096.f;
 
 struct Workspace {
   uint16_t *X, *XT0, *XT1, *Am, *Pm;
@@ -235,7 +236,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
       uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
       return 0;
     }
-    g.alpha = 1.f / kGramKx;
+    g.alpha = 1.f / kNsKx;
     g.mode = EPI_FINAL;
     g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;
     g.w_ptrs = w_ptrs; g.w_dtype = w_dtype; g.decay = decay; g.lrs = lrs;
@@ -273,12 +274,12 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
   uint16_t* W = w.Wm;
   int qs = -1;               // slot of the current Q, -1: none since the last (re)start
   float rs = (float)kr;      // the stored R is rs * (X X^T of the normalised X)
-  if (gram_of_x(R, rs / (kGramKx * kGramKx))) return 1;
+  if (gram_of_x(R, rs / (kNsKx * kNsKx))) return 1;
   for (int it = 0; it < T; ++it) {
     if (it != 0 && is_restart(it) && qs >= 0) {
       if (qx(qbuf[qs], false)) return 1;
       rs = 1.f;
-      if (gram_of_x(R, 1.f / (kGramKx * kGramKx))) return 1;
+      if (gram_of_x(R, 1.f / (kNsKx * kNsKx))) return 1;
       qs = -1;
     }
     const float ca = coeffs[3 * it], cb = coeffs[3 * it + 1], cc = coeffs[3 * it + 2];
@@ -376,24 +377,24 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
   p.mu = mu;
   p.first_step = first_step;
   p.nesterov = nesterov;
-  p.stage = gram ? PRE_NORM : PRE_BF16;
+  p.stage = PRE_NORM;
   const double Ld = batch, md = m, nd = n, elems = (double)rows * cols * batch;
   const double gbytes = g_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0;
   if (do_stage) {
-  // algorithmic bytes: gradient read, fp32 momentum read (not on the first step) and write,
-  // one 16-bit copy of ns_in (direct); the Gram staging has no copy in its first pass and
-  // reads the gradient and the new momentum again in the second
+  // algorithmic bytes: gradient read, fp32 momentum read (not on the first step) and write;
+  // the second pass reads the gradient and the new momentum again and writes one fp16 copy of
+  // the normalised ns_in (fp16 cannot hold an un-normalised gradient safely)
   const double mom_bytes = buf_ptrs ? (first_step ? 4.0 : 8.0) : 0.0;
-  const double pre_bytes = elems * (gbytes + mom_bytes + (gram ? 0.0 : 2.0));
+  const double pre_bytes = elems * (gbytes + mom_bytes);
   if (timed(PC_PRE, 0.0, pre_bytes, stream, who, [&] { return launch_pre(p, stream); })) return 1;
   if (timed(PC_NORM, 0.0, (double)batch * w.nparts * 4, stream, who, [&] {
         return launch_norm_finalize(w.partials, w.nparts, batch, eps, w.scale, w.scale_sq, stream);
       }))
     return 1;
-  if (gram) {
+  {
     p.stage = PRE_F16;
     p.scale = w.scale;
-    p.kx = kGramKx;
+    p.kx = kNsKx;
     const double st_bytes = elems * (gbytes + (buf_ptrs ? 4.0 : 0.0) + 2.0);
     if (timed(PC_PRE, 0.0, st_bytes, stream, who, [&] { return launch_pre(p, stream); }))
       return 1;
@@ -412,37 +413,46 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
     return run_gram(w, m, n, m_pad, n_pad, tile, batch, tall, coeffs, T, restarts, n_restarts,
                     w_ptrs, w_dtype, pub_ptrs, pub_dtype, out_ptrs, out_dtype, decay, lrs,
                     syrk_flops, poly_flops, gemm_flops, wbytes + obytes + pbytes, stream, who);
+  // Direct NS on the same fp16 operands as the Gram form: X carries the power-of-two scale
+  // kNsKx throughout; the first A (eigenvalues ~1/m) carries kr until its polynomial.
+  int kr = 1;
+  while (kr * 2 <= m && kr < 4096) kr *= 2;
   for (int it = 0; it < T; ++it) {
     const float ca = coeffs[3 * it], cb = coeffs[3 * it + 1], cc = coeffs[3 * it + 2];
-    // A = s^2 X X^T (s only on the first step: X holds the un-normalised ns_in)
+    const float rs = it == 0 ? (float)kr : 1.f;   // the stored A is rs * (X X^T)
+    // A = X X^T of the normalised X (the stored X is kNsKx * X)
     NtArgs s{};
+    s.elt = ELT_F16;
     s.A = w.X; s.lda = n_pad; s.sA = xs;
     s.B = w.X; s.ldb = n_pad; s.sB = xs;
     s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch;
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
-    s.mode = EPI_SYM; s.alpha = 1.f; s.beta = 0.f; s.diag = 0.f;
-    s.alpha_dev = it == 0 ? w.scale_sq : nullptr;
+    s.sym_exact = 1;
+    s.mode = EPI_SYM; s.alpha = rs / (kNsKx * kNsKx); s.beta = 0.f; s.diag = 0.f;
     s.D = w.Am; s.ldd = m_pad; s.sD = as;
     if (timed(PC_SYRK, syrk_flops, 0.0, stream, who, [&] { return launch_nt(s, tile, stream); }))
       return 1;
     // P = c A A^T + b A
     NtArgs q{};
+    q.elt = ELT_F16;
     q.A = w.Am; q.lda = m_pad; q.sA = as;
     q.B = w.Am; q.ldb = m_pad; q.sB = as;
     q.M = m_pad; q.N = m_pad; q.K = m_pad; q.L = batch;
     q.mt = q.nt = m_pad / tile; q.tiles_per_mat = s.tiles_per_mat; q.tri = 1;
-    q.mode = EPI_SYM; q.alpha = cc; q.beta = cb; q.diag = 0.f;
+    q.sym_exact = 1;
+    q.mode = EPI_SYM; q.alpha = cc / (rs * rs); q.beta = cb / rs; q.diag = 0.f;
     q.C = w.Am; q.ldc = m_pad; q.sC = as;
     q.D = w.Pm; q.ldd = m_pad; q.sD = as;
     if (timed(PC_POLY, poly_flops, 0.0, stream, who, [&] { return launch_nt(q, tile, stream); }))
       return 1;
-    // X' = s (P X + a X)
+    // X' = P X + a X (scale kNsKx kept); the final step writes U = X' / kNsKx
     NtArgs g{};
+    g.elt = ELT_F16;
     g.A = w.Pm; g.lda = m_pad; g.sA = as;
     g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
     g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch;
     g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
-    g.alpha = 1.f; g.beta = ca; g.alpha_dev = it == 0 ? w.scale : nullptr;
+    g.alpha = it + 1 < T ? 1.f : 1.f / kNsKx; g.beta = ca;
     g.C = w.X; g.ldc = n_pad; g.sC = xs;
     if (it + 1 < T) {
       g.mode = EPI_NS;

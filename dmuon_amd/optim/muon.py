@@ -11,7 +11,7 @@ Constructor, ``step()`` and ``zero_grad()`` keep the reference's signature and e
 
 runs on the GPU as one C-ABI call per bucket of same-shape parameters
 (``dmuon_muon_step_group``): a fused momentum/Nesterov/staging kernel, a norm finalise, and
-the bf16 MFMA products of the chosen NS form (``ns_backend``: "gram", the default, or
+the fp16 MFMA products of the chosen NS form (``ns_backend``: "gram", the default, or
 "direct"), the last product applying the weight update in its epilogue. The momentum buffer is fp32 and lives in
 ``optimizer.state[id(dp)]["momentum_buffer"]`` shaped ``(rows, cols)`` like the reference's.
 

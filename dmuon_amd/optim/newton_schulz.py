@@ -5,7 +5,7 @@ coefficient sets (``:45-75``), the :class:`NewtonSchulz` configuration object (`
 ``direct_newton_schulz`` (``:225-273``), ``newton_schulz`` (``:299-327``) and
 ``gram_newton_schulz`` (``:333-448``).
 
-Two device algorithms, both on the bf16 MFMA NT kernels, for X = G / (||G||_F + eps) oriented
+Two device algorithms, both on the fp16 MFMA NT kernels, for X = G / (||G||_F + eps) oriented
 so that X has m = min(rows, cols) rows and n = max(rows, cols) columns:
 
 ``backend="direct"`` (``direct_newton_schulz``), per coefficient triple ``(a, b, c)``::
@@ -20,10 +20,11 @@ runs it: R = X X^T once, then per step only m x m products -- ``Z = c R R + b R`
 the last or a restart, ``R <- P R P`` -- with ``X <- Q X; R = X X^T`` at each restart index and
 ``U = Q X`` at the end (``newton_schulz.py:364-448``). For n > m this needs fewer flops than the
 direct form. bf16 is not accurate enough for this recurrence (R's small eigenvalues drown in
-its rounding), so X is staged as fp16 of the normalised input times a power of two.
+its rounding). Both backends stage X as fp16 of the normalised input times a power of two (the
+reference computes both in fp16 too, ``newton_schulz.py:266,391``).
 
-Results differ from the reference's fp16 pipeline by rounding (bf16 operands, fp32
-accumulation).
+Results differ from the reference's fp16 pipeline by rounding (fp32 accumulation and fp32
+epilogues here; exactly symmetric products).
 
 There is no CPU path: CPU tensors raise.
 """
@@ -300,7 +301,7 @@ class NewtonSchulz:
 def get_ns_backend() -> str:
     """One-line description of the NS kernel (``syrk_dispatch.py:42-66``)."""
     return ("Gram-space NS with restarts / direct NS in SYRK form · kernel=hip_gfx950 "
-            "(MI355X CDNA4, bf16 MFMA 32x32x16)")
+            "(MI355X CDNA4, fp16 MFMA 32x32x16)")
 
 
 def get_backend_status() -> dict:

@@ -13,9 +13,9 @@ It restates, in numpy, the reference algorithm of X-Square-Robot/dmuon on this p
                       schedule included; ``addmm`` rounds once per call.
 * ``closed_form_ns``  exact-arithmetic NS through an fp64 SVD: X0 = U S V^T gives
                       U f(S) V^T with f = p_T o ... o p_1, p(s) = a s + b s^3 + c s^5.
-* ``syrk_emulated_ns`` the build's own bf16 SYRK-form pipeline (bf16 operands, fp32
-                      accumulation, normalisation folded into the first SYRK/GEMM), used to
-                      bound the bf16-vs-fp16 gap and as a tight check of the GPU kernels.
+* ``syrk_emulated_ns`` the build's own direct pipeline (fp16 operands scaled by powers of two,
+                      fp32 accumulation, exactly symmetric A and P), a tight check of the GPU
+                      kernels.
 * ``syrk_emulated_gram_ns`` the same for the build's Gram-form pipeline.
 * ``muon_step``       ``dmuon/optim/muon.py:1683-1740``: sum-form momentum
                       (``buf.mul_(mu).add_(g)``, first step ``buf = g``), Nesterov
@@ -182,25 +182,32 @@ def closed_form_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
 
 
 def syrk_emulated_ns(G: np.ndarray, coefficients: Sequence = KELLER, eps: float = 1e-7,
-                     op_dtype: str = "bf16") -> np.ndarray:
-    """The build's device pipeline (not the reference's): X~ = bf16(ns_in) un-normalised,
-    s = 1/(||ns_in|| + eps); A = bf16(s^2 X~X~^T); P = bf16(c A A^T + b A);
-    X' = bf16(s (P X~ + a X~)) (s only on the first step); last step returns fp32 U."""
+                     op_dtype: str = "fp16", kx: float = 4096.0) -> np.ndarray:
+    """The build's direct device pipeline (not the reference's rounding), rnd = op_dtype:
+    X = rnd(kx s ns_in), s = 1/(||ns_in|| + eps); per step A = rnd(rs/kx^2 X X^T) with the
+    stored-A scale rs = 2^floor(log2 m) (at most 2^12) on the first step and 1 after,
+    P = rnd(c/rs^2 A A^T + b/rs A), X = rnd(P X + a X); the last step returns
+    U = fp32((P X + a X) / kx). A and P keep their upper triangle, mirrored."""
     X = np.asarray(G, dtype=np.float32)
     t = X.shape[0] > X.shape[1]
     if t:
         X = X.T
-    nrm = np.float32(np.sqrt(np.sum(X.astype(np.float64) ** 2)))
-    s = np.float32(1.0) / (nrm + np.float32(eps))
-    Xq = rnd(X, op_dtype)
+    f32 = np.float32
+    nrm = f32(np.sqrt(np.sum(X.astype(np.float64) ** 2)))
+    s = f32(1.0) / (nrm + f32(eps))
+    Xq = rnd((X * f32(s * f32(kx))).astype(np.float32), op_dtype)
+    m = Xq.shape[0]
+    kr = 1
+    while kr * 2 <= m and kr < 4096:
+        kr *= 2
     T = len(coefficients)
     for it, (a, b, c) in enumerate(coefficients):
-        sa = np.float32(s * s) if it == 0 else np.float32(1.0)
-        A = rnd(sa * _mm(Xq, Xq.T, "fp32"), op_dtype)
-        P = rnd(np.float32(c) * _mm(A, A, "fp32") + np.float32(b) * A, op_dtype)
-        sg = s if it == 0 else np.float32(1.0)
-        Xn = sg * (_mm(P, Xq, "fp32") + np.float32(a) * Xq)
-        Xq = Xn.astype(np.float32) if it == T - 1 else rnd(Xn, op_dtype)
+        rs = f32(kr) if it == 0 else f32(1.0)
+        A = _upper_mirror(rnd(f32(rs / f32(kx * kx)) * _mm(Xq, Xq.T, "fp32"), op_dtype))
+        P = _upper_mirror(rnd(f32(c) / (rs * rs) * _mm(A, A.T, "fp32") + f32(b) / rs * A,
+                              op_dtype))
+        Xn = _mm(P, Xq, "fp32") + f32(a) * Xq
+        Xq = (f32(1.0 / kx) * Xn).astype(np.float32) if it == T - 1 else rnd(Xn, op_dtype)
     if t:
         Xq = Xq.T
     return np.ascontiguousarray(Xq)
@@ -321,8 +328,8 @@ def muon_step(W, g, buf, lr=0.02, mu=0.95, wd=0.0, nesterov=True, coefficients=K
         U = gram_ns(x2, coefficients, None, eps, dtype)
     elif ns == "closed":
         U = closed_form_ns(x2, coefficients, eps)
-    elif ns == "syrk_bf16":
-        U = syrk_emulated_ns(x2, coefficients, eps, "bf16")
+    elif ns == "syrk":
+        U = syrk_emulated_ns(x2, coefficients, eps)
     else:
         raise ValueError(ns)
     U = np.asarray(U, dtype=np.float32).reshape(np.shape(g))

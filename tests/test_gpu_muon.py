@@ -83,7 +83,7 @@ def test_multi_step_momentum_and_update(gpu):
         opt.step()
         for i, (p, g) in enumerate(zip(m.parameters(), gs)):
             Wn, bufs[i], _ = o.muon_step(W[i], g.numpy(), bufs[i], lr=0.02, mu=0.95, wd=0.05,
-                                         coefficients=o.KELLER, ns="syrk_bf16")
+                                         coefficients=o.KELLER, ns="syrk")
             dp = dmuon.get_owned_params(m)[i]
             gb = opt.state[id(dp)]["momentum_buffer"].cpu().numpy()
             assert np.array_equal(gb, bufs[i]), f"step {step} param {i}: momentum not bit-exact"
