@@ -170,16 +170,20 @@ def main():
     torch.cuda.synchronize()
 
     # ---- timed region: exactly K optimizer steps ---------------------------------------------
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
+    evs[0].record()
+    for k in range(args.steps):
         opt.step()
-    ev1.record()
+        evs[k + 1].record()          # one event between steps: per-step times for the spread
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    ms_per_step = evs[0].elapsed_time(evs[-1]) / args.steps
+    per_step = sorted(evs[k].elapsed_time(evs[k + 1]) for k in range(args.steps))
+
+    def pct(q):
+        return per_step[min(len(per_step) - 1, int(round(q * (len(per_step) - 1))))]
 
     # ---- kernel breakdown: the same steps with the library's per-launch hipEvents -------------
     prof_steps = max(1, min(3, args.steps))
@@ -297,6 +301,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 3),
+        "ms_per_step_p10_median_p90": [round(pct(0.1), 3), round(pct(0.5), 3), round(pct(0.9), 3)],
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
