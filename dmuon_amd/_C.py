@@ -100,7 +100,7 @@ def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args))
 
 
-PROFILE_CLASSES = ("pre", "norm", "syrk", "poly", "gemm", "final", "adamw", "clip", "diag")
+PROFILE_CLASSES = ("pre", "norm", "syrk", "poly", "gemm", "final", "adamw", "clip")
 
 
 def profile_enable(on: bool) -> None:

@@ -88,7 +88,7 @@ Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch, int
 // Single-threaded use only (like the launch path itself). Events are host objects; no device
 // memory is allocated.
 enum ProfClass {
-  PC_PRE = 0, PC_NORM, PC_SYRK, PC_POLY, PC_GEMM, PC_FINAL, PC_ADAMW, PC_CLIP, PC_DIAG, PC_COUNT
+  PC_PRE = 0, PC_NORM, PC_SYRK, PC_POLY, PC_GEMM, PC_FINAL, PC_ADAMW, PC_CLIP, PC_COUNT
 };
 struct ProfRec {
   int cls;
@@ -187,7 +187,8 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
   };
   // D = alpha * A B^T + beta * C + diag * I, m x m; tri: upper tiles mirrored (symmetric result)
   auto sq = [&](const uint16_t* A, const uint16_t* B, const uint16_t* C, uint16_t* D, float alpha,
-                float beta, float diag, bool tri) -> int {
+                float beta, float diag, bool tri, uint16_t* D2 = nullptr,
+                float diag2 = 0.f) -> int {
     NtArgs s{};
     s.elt = ELT_F16;
     s.A = A; s.lda = m_pad; s.sA = as;
@@ -199,6 +200,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     s.mode = EPI_SYM; s.alpha = alpha; s.beta = C ? beta : 0.f; s.diag = diag;
     s.C = C; s.ldc = m_pad; s.sC = as;
     s.D = D; s.ldd = m_pad; s.sD = as;
+    s.D2 = D2; s.diag2 = diag2;
     return timed(PC_POLY, tri ? tri_sq_flops : full_sq_flops, 0.0, stream, who,
                  [&] { return launch_nt(s, tile, stream); });
   };
@@ -292,14 +294,13 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
       qs = 0;
       continue;
     }
-    if (sq(R, R, R, Z, zr2, zr1, 0.f, true)) return 1;   // Z = c R^2 + b R
     if (qs < 0) {
-      if (timed(PC_DIAG, 0.0, 4.0 * batch * (double)m_pad * m_pad, stream, who,
-                [&] { return launch_diag_copy(Z, qbuf[0], m_pad, batch, ca, stream); }))
-        return 1;
+      // Z = c R^2 + b R, and Q = Z + a I written by the same epilogue
+      if (sq(R, R, R, Z, zr2, zr1, 0.f, true, qbuf[0], ca)) return 1;
       qtbuf[0] = qbuf[0];
       qs = 0;
     } else {
+      if (sq(R, R, R, Z, zr2, zr1, 0.f, true)) return 1;   // Z = c R^2 + b R
       if (q_update(Z, qs, ca)) return 1;   // Q <- Z Q + a Q
       qs = 1 - qs;
     }

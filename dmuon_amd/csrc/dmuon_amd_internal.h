@@ -37,6 +37,7 @@ struct NtArgs {
   int m_real, n_real, transposed;         // true NS dims; transposed: original = X^T (n_real x m_real)
   int elt;                                // ELT_BF16 / ELT_F16 (A, B, C, D, DT)
   int sym_exact;                          // EPI_SYM + tri: diagonal tiles stored exactly symmetric
+  uint16_t* D2; float diag2;              // EPI_SYM + tri + sym_exact: also D2 = D + diag2 * I
 };
 
 // Launches the NT MFMA kernel; picks the tile configuration from args (tile = 256 or 128).
@@ -63,9 +64,6 @@ struct PreArgs {
 hipError_t launch_pre(const PreArgs& a, hipStream_t stream);
 int pre_blocks_per_mat(int Rp, int Cp);
 
-// Gram NS: Q = Z + diag * I over L matrices of m x m fp16 (ld m), Z the polynomial part
-hipError_t launch_diag_copy(const uint16_t* Z, uint16_t* Q, int m, int L, float diag,
-                            hipStream_t stream);
 
 // scale[l] = 1/(sqrt(sum partials[l]) + eps), scale_sq[l] = scale^2
 hipError_t launch_norm_finalize(const float* partials, int nparts, int L, float eps,

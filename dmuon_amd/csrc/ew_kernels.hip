@@ -4,11 +4,10 @@
 //           writes bf16(ns_in) twice -- in the gradient's own layout and transposed (LDS-tiled
 //           64x64 transpose) -- into zero-padded NS operands, plus per-block partial sums of
 //           ns_in^2 for the Frobenius norm. One pass: 2 (g) + 4 + 4 (buf) + 2 + 2 (copies) B/elt.
-//           The Gram NS stages in two passes instead: PRE_NORM (momentum + partials), then,
+//           The fp16 NS stages in two passes instead: PRE_NORM (momentum + partials), then,
 //           once the norm is known, PRE_F16 recomputes ns_in and writes fp16(kx * ns_in / norm)
 //           (fp16 cannot hold an un-normalised gradient safely). 2+4+4, then 2+4+2+2 B/elt.
 //  finalize scale = 1/(||ns_in||_F + eps) per matrix, fixed-order (deterministic) reduction.
-//  diag     Q = Z + a I for the Gram iteration's first polynomial after a (re)start.
 //  update   W <- W*(1 - lr*wd) - lr*scale*U   for callers holding a materialised U.
 #include <algorithm>
 
@@ -200,28 +199,6 @@ __global__ __launch_bounds__(256) void muon_update_kernel(const UpdateArgs a) {
   }
 }
 
-// Q = Z + diag * I, fp16, 16-byte vectors; each matrix holds m*m/8 vectors and a vector holds
-// a diagonal element iff its row's diagonal column falls inside it.
-__global__ __launch_bounds__(256) void diag_copy_kernel(const uint16_t* __restrict__ Z,
-                                                        uint16_t* __restrict__ Q, int m,
-                                                        long long n8, float diag) {
-  const long long per = (long long)m * m / 8;
-  for (long long v = (long long)blockIdx.x * 256 + threadIdx.x; v < n8;
-       v += (long long)gridDim.x * 256) {
-    uint4 t = reinterpret_cast<const uint4*>(Z)[v];
-    const long long e = (v % per) * 8;           // element index within the matrix
-    const int row = (int)(e / m), col = (int)(e % m);
-    const int d = row - col;                     // diagonal at lane d of this vector
-    if (d >= 0 && d < 8) {
-      unsigned* w = reinterpret_cast<unsigned*>(&t) + (d >> 1);
-      const unsigned h = (d & 1) ? (*w >> 16) : (*w & 0xffff);
-      const unsigned r = f2h(h2f((uint16_t)h) + diag);
-      *w = (d & 1) ? ((*w & 0xffffu) | (r << 16)) : ((*w & 0xffff0000u) | r);
-    }
-    reinterpret_cast<uint4*>(Q)[v] = t;
-  }
-}
-
 }  // namespace
 
 int pre_blocks_per_mat(int Rp, int Cp) { return (Rp / kTile) * (Cp / kTile); }
@@ -234,14 +211,6 @@ hipError_t launch_pre(const PreArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(muon_pre_kernel<PRE_F16>, grid, block, 0, stream, a);
   else
     hipLaunchKernelGGL(muon_pre_kernel<PRE_BF16>, grid, block, 0, stream, a);
-  return hipGetLastError();
-}
-
-hipError_t launch_diag_copy(const uint16_t* Z, uint16_t* Q, int m, int L, float diag,
-                            hipStream_t stream) {
-  const long long n8 = (long long)m * m / 8 * L;   // m is a multiple of 128
-  const int blocks = (int)std::min<long long>((n8 + 255) / 256, 16384);
-  hipLaunchKernelGGL(diag_copy_kernel, dim3(blocks), dim3(256), 0, stream, Z, Q, m, n8, diag);
   return hipGetLastError();
 }
 

@@ -262,6 +262,12 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
     // kept, stored at (i, j) and mirrored to (j, i) (a product of two different symmetric
     // factors is symmetric only to rounding otherwise)
     const bool exact = MODE == EPI_SYM && a.sym_exact && a.tri && bi == bj;
+    // optional second output of a triangle product: D2 = D + diag2 * I (same layout as D;
+    // the diagonal only lives in diagonal tiles, which take the exact path)
+    uint16_t* D2b = nullptr;
+    if constexpr (MODE == EPI_SYM) {
+      if (a.D2) D2b = a.D2 + (long long)l * a.sD;
+    }
     u32x2_t cbuf[2][T::TJ * 4];
     if (Cb) load_c(0, cbuf[0]);
 #pragma unroll
@@ -310,6 +316,11 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
               const uint16_t h = (uint16_t)((e & 1) ? (word >> 16) : (word & 0xffff));
               if (i <= j) Db[(long long)i * a.ldd + j] = h;
               if (i < j) Db[(long long)j * a.ldd + i] = h;
+              if (D2b) {
+                const uint16_t h2 = i == j ? to_elt<E>(from_elt<E>(h) + a.diag2) : h;
+                if (i <= j) D2b[(long long)i * a.ldd + j] = h2;
+                if (i < j) D2b[(long long)j * a.ldd + i] = h2;
+              }
             }
         continue;
       }
@@ -317,11 +328,12 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
         constexpr int CPRW = T::WTN / 4;          // 8-byte chunks per slab row
         constexpr int RPIT = 64 / CPRW;           // slab rows per wave instruction
         const int cr = lane / CPRW, cc = lane % CPRW;
-        uint16_t* dst = Db + (long long)(iw + 32 * x + cr) * a.ldd + jw + 4 * cc;
+        const long long doff = (long long)(iw + 32 * x + cr) * a.ldd + jw + 4 * cc;
 #pragma unroll
         for (int r0 = 0; r0 < 32; r0 += RPIT) {
           const u32x2_t v = *reinterpret_cast<const u32x2_t*>(reg + (r0 + cr) * T::EPN + 8 * cc);
-          *reinterpret_cast<u32x2_t*>(dst + (long long)r0 * a.ldd) = v;
+          *reinterpret_cast<u32x2_t*>(Db + doff + (long long)r0 * a.ldd) = v;
+          if (D2b) *reinterpret_cast<u32x2_t*>(D2b + doff + (long long)r0 * a.ldd) = v;
         }
       }
       if (DTb) {
@@ -339,11 +351,13 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
             col[3 * T::EPT / 2] = (uint16_t)(p.y >> 16);
           }
         const int cr = lane >> 2, cc = lane & 3;  // 4 lanes x 16 B per 32-value row
-        uint16_t* dst = DTb + (long long)(jw + cr) * ldt + iw + 32 * x + 8 * cc;
+        const long long toff = (long long)(jw + cr) * ldt + iw + 32 * x + 8 * cc;
+        uint16_t* dst = DTb + toff;
 #pragma unroll
         for (int r0 = 0; r0 < T::WTN; r0 += 16) {
           const u32x4_t v = *reinterpret_cast<const u32x4_t*>(reg + (r0 + cr) * T::EPT + 16 * cc);
           *reinterpret_cast<u32x4_t*>(dst + (long long)r0 * ldt) = v;
+          if (D2b) *reinterpret_cast<u32x4_t*>(D2b + toff + (long long)r0 * ldt) = v;
         }
       }
     }
@@ -687,6 +701,8 @@ void nt_mfma_kernel(const NtArgs a) {
 hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   const long long nb = (long long)a.tiles_per_mat * a.L;
   if (nb <= 0) return hipSuccess;
+  // the second output relies on the exactly symmetric diagonal-tile path for its diagonal
+  if (a.D2 && !(a.mode == EPI_SYM && a.tri && a.sym_exact)) return hipErrorInvalidValue;
   dim3 grid((unsigned)nb);
 #define DMUON_NT(TILE, BK, S, WM, WN, E)                                                       \
   do {                                                                                         \

@@ -72,9 +72,9 @@ int dmuon_abi_version(void);
  * dmuon_adamw_multi / the segmented clip entry points is bracketed by hipEvents on its stream.
  * dmuon_profile_collect synchronises on those events and returns, per kernel class (0 pre,
  * 1 norm-finalize, 2 SYRK X X^T (Gram: R = X X^T), 3 SYRK-poly (Gram: the m x m products),
- * 4 NS GEMM (Gram: restart Q X), 5 final GEMM + update, 6 AdamW, 7 segmented clip, 8 Gram
- * Q = Z + a I copy), the summed milliseconds, launch counts, useful FLOPs and algorithmic
- * bytes, then clears the records. n_classes must be >= 9. Not thread-safe.
+ * 4 NS GEMM (Gram: restart Q X), 5 final GEMM + update, 6 AdamW, 7 segmented clip), the
+ * summed milliseconds, launch counts, useful FLOPs and algorithmic bytes, then clears the
+ * records. n_classes must be >= 8. Not thread-safe.
  */
 int dmuon_profile_enable(int on);
 int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* bytes,
