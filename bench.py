@@ -106,11 +106,48 @@ def cpu_baseline(budget_s: float = 60.0, ns: str = "gram") -> dict:
     }
 
 
+def library_compare(torch, dev, _C, reps: int = 5) -> dict:
+    """The NT kernel (EPI_NS: D = P X^T-form product + 0.5 X, with D^T) against torch's bf16
+    GEMM (hipBLASLt) on the same NT-form product, M = K = 4096, N = 57344 (14 waves of 256x256
+    tiles): milliseconds and TFLOP/s of each, for the rocprofv3 counter comparison."""
+    M, N = 4096, 57344
+    g = torch.Generator(device=dev).manual_seed(0)
+    P = (torch.randn(M, M, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    XT = (torch.randn(N, M, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    X = XT.t().contiguous()
+    XO, XTO = torch.empty_like(X), torch.empty_like(XT)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def ours():
+        _C.call("dmuon_ns_gemm_bf16", P.data_ptr(), M, 0, XT.data_ptr(), M, 0, X.data_ptr(), N,
+                0, XO.data_ptr(), N, 0, XTO.data_ptr(), M, 0, M, N, 1, 1.0, 0.5, None, 256,
+                stream)
+
+    def library():
+        return P @ XT.t()
+
+    out = {"metric": "NT kernel vs library GEMM", "shape": {"M": M, "N": N, "K": M},
+           "dtype": "bf16"}
+    for name, fn in (("library_hipblaslt", library), ("nt_mfma_kernel", ours)):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[name] = {"ms": round(ms, 3), "tflops": round(2.0 * M * N * M / (ms * 1e-3) / 1e12, 1)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=N_LAYERS, help="layers of the matrix set")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-adamw", action="store_true")
@@ -125,6 +162,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=60.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 1 GiB device-to-device copy (HBM counter scale)")
+    ap.add_argument("--library-compare", action="store_true",
+                    help="only time the NT MFMA kernel against torch's library GEMM "
+                         "(hipBLASLt) on one NT-form bf16 product and print that JSON line")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -140,6 +180,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.library_compare:
+        print(json.dumps(library_compare(torch, dev, _C)), flush=True)
+        return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)   # 1 GiB
         dst = torch.empty_like(src)

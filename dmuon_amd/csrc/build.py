@@ -58,8 +58,22 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if err.strip() and verbose:
         print(err, file=sys.stderr)
+    _check_launch_stubs(tmp)
     os.replace(tmp, out)
     return out
+
+
+def _check_launch_stubs(so: Path) -> None:
+    """clang can silently skip a kernel template's host launch stub (the library then fails
+    to load with an undefined __device_stub__ symbol); catch that at build time."""
+    nm = shutil.which("nm")
+    if not nm:
+        return
+    proc = subprocess.run([nm, "-D", "--undefined-only", str(so)], capture_output=True, text=True)
+    missing = [l.split()[-1] for l in proc.stdout.splitlines() if "__device_stub__" in l]
+    if missing:
+        so.unlink(missing_ok=True)
+        raise RuntimeError("hipcc dropped kernel launch stubs: " + ", ".join(missing[:4]))
 
 
 if __name__ == "__main__":
