@@ -177,9 +177,8 @@ struct TilePos {
   int l, bi, bj;
 };
 
-__device__ __forceinline__ TilePos decode_tile(const NtArgs& a) {
-  const int nblocks = gridDim.x;
-  const int lb = xcd_remap(blockIdx.x, nblocks);
+__device__ __forceinline__ TilePos decode_tile(const NtArgs& a, int hb, int nblocks) {
+  const int lb = xcd_remap(hb, nblocks);
   const int l = lb / a.tiles_per_mat;
   int t = lb - l * a.tiles_per_mat;
   int bi, bj;
@@ -252,18 +251,21 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
     uint16_t* Db = a.D + (long long)l * a.sD;
     uint16_t* DTb = nullptr;
     long long ldt = 0;
+    // diagonal tile of a result that must be exactly symmetric: each value computed for (i, j)
+    // with i <= j is stored at (i, j) by the row path and at (j, i) by the mirror path, and the
+    // values computed below the diagonal are dropped (a product of two different symmetric
+    // factors is symmetric only to rounding otherwise); both paths mask element-wise only in
+    // the chunks that straddle the diagonal
+    const bool diag = MODE == EPI_SYM && a.sym_exact && a.tri && bi == bj;
     if constexpr (MODE == EPI_SYM) {
-      if (a.tri && bi != bj) { DTb = Db; ldt = a.ldd; }   // mirror into the lower triangle
+      // mirror into the lower triangle
+      if (a.tri && (bi != bj || a.sym_exact)) { DTb = Db; ldt = a.ldd; }
     } else {
       if (a.DT) { DTb = a.DT + (long long)l * a.sDT; ldt = a.lddt; }
     }
     char* reg = smem + wave * T::EPI_REGION;
-    // diagonal tile of a result that must be exactly symmetric: only its upper triangle is
-    // kept, stored at (i, j) and mirrored to (j, i) (a product of two different symmetric
-    // factors is symmetric only to rounding otherwise)
-    const bool exact = MODE == EPI_SYM && a.sym_exact && a.tri && bi == bj;
-    // optional second output of a triangle product: D2 = D + diag2 * I (same layout as D;
-    // the diagonal only lives in diagonal tiles, which take the exact path)
+    // optional second output of a triangle product: D2 = D + diag2 * I (same layout as D; the
+    // diagonal only lives in the straddling chunks of diagonal tiles' row path)
     uint16_t* D2b = nullptr;
     if constexpr (MODE == EPI_SYM) {
       if (a.D2) D2b = a.D2 + (long long)l * a.sD;
@@ -300,30 +302,8 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
           }
           o2[y * 4 + g].x = (unsigned)o[0] | ((unsigned)o[1] << 16);
           o2[y * 4 + g].y = (unsigned)o[2] | ((unsigned)o[3] << 16);
-          if (!exact)
-            *reinterpret_cast<u32x2_t*>(reg + li * T::EPN + (jo + 4 * lh) * 2) = o2[y * 4 + g];
+          *reinterpret_cast<u32x2_t*>(reg + li * T::EPN + (jo + 4 * lh) * 2) = o2[y * 4 + g];
         }
-      if (exact) {
-        const int i = iw + 32 * x + li;
-#pragma unroll
-        for (int y = 0; y < T::TJ; ++y)
-#pragma unroll
-          for (int g = 0; g < 4; ++g)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int j = jw + 32 * y + 8 * g + 4 * lh + e;
-              const unsigned word = e < 2 ? o2[y * 4 + g].x : o2[y * 4 + g].y;
-              const uint16_t h = (uint16_t)((e & 1) ? (word >> 16) : (word & 0xffff));
-              if (i <= j) Db[(long long)i * a.ldd + j] = h;
-              if (i < j) Db[(long long)j * a.ldd + i] = h;
-              if (D2b) {
-                const uint16_t h2 = i == j ? to_elt<E>(from_elt<E>(h) + a.diag2) : h;
-                if (i <= j) D2b[(long long)i * a.ldd + j] = h2;
-                if (i < j) D2b[(long long)j * a.ldd + i] = h2;
-              }
-            }
-        continue;
-      }
       {
         constexpr int CPRW = T::WTN / 4;          // 8-byte chunks per slab row
         constexpr int RPIT = 64 / CPRW;           // slab rows per wave instruction
@@ -332,8 +312,22 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
 #pragma unroll
         for (int r0 = 0; r0 < 32; r0 += RPIT) {
           const u32x2_t v = *reinterpret_cast<const u32x2_t*>(reg + (r0 + cr) * T::EPN + 8 * cc);
-          *reinterpret_cast<u32x2_t*>(Db + doff + (long long)r0 * a.ldd) = v;
-          if (D2b) *reinterpret_cast<u32x2_t*>(D2b + doff + (long long)r0 * a.ldd) = v;
+          const long long o = doff + (long long)r0 * a.ldd;
+          // diagonal tile: row i keeps columns j >= i (chunk j0 .. j0+3)
+          const int di = iw + 32 * x + r0 + cr, dj = jw + 4 * cc;
+          if (!diag || dj > di) {
+            *reinterpret_cast<u32x2_t*>(Db + o) = v;
+            if (D2b) *reinterpret_cast<u32x2_t*>(D2b + o) = v;
+          } else if (dj + 3 >= di) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (dj + e < di) continue;
+              const unsigned word = e < 2 ? v.x : v.y;
+              const uint16_t h = (uint16_t)((e & 1) ? (word >> 16) : (word & 0xffff));
+              Db[o + e] = h;
+              if (D2b) D2b[o + e] = dj + e == di ? to_elt<E>(from_elt<E>(h) + a.diag2) : h;
+            }
+          }
         }
       }
       if (DTb) {
@@ -356,8 +350,21 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
 #pragma unroll
         for (int r0 = 0; r0 < T::WTN; r0 += 16) {
           const u32x4_t v = *reinterpret_cast<const u32x4_t*>(reg + (r0 + cr) * T::EPT + 16 * cc);
-          *reinterpret_cast<u32x4_t*>(dst + (long long)r0 * ldt) = v;
-          if (D2b) *reinterpret_cast<u32x4_t*>(D2b + toff + (long long)r0 * ldt) = v;
+          // diagonal tile: output row j keeps columns i < j (chunk i0 .. i0+7)
+          const int dj = jw + r0 + cr, di = iw + 32 * x + 8 * cc;
+          if (!diag || di + 7 < dj) {
+            *reinterpret_cast<u32x4_t*>(dst + (long long)r0 * ldt) = v;
+            if (D2b) *reinterpret_cast<u32x4_t*>(D2b + toff + (long long)r0 * ldt) = v;
+          } else if (di < dj) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              if (di + e >= dj) continue;
+              const unsigned word = v[e >> 1];
+              const uint16_t h = (uint16_t)((e & 1) ? (word >> 16) : (word & 0xffff));
+              dst[(long long)r0 * ldt + e] = h;
+              if (D2b) D2b[toff + (long long)r0 * ldt + e] = h;
+            }
+          }
         }
       }
     }
@@ -567,7 +574,7 @@ void nt_mfma_kernel(const NtArgs a) {
   const int wi = wave / WN, wj = wave % WN;
 
   // ---- tile decode -------------------------------------------------------------------
-  const TilePos tp = decode_tile(a);
+  const TilePos tp = decode_tile(a, blockIdx.x, gridDim.x);
   const int l = tp.l, bi = tp.bi, bj = tp.bj;
   const int i0 = bi * BM, j0 = bj * BN;
 
