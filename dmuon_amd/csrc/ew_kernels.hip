@@ -44,6 +44,21 @@ __device__ __forceinline__ float h2f(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+// The gradient and the momentum buffer are streamed once per pass: non-temporal loads (and the
+// buffer's non-temporal store) keep them from displacing cache lines the NS kernels reuse
+// (measured 26.6 -> 24.8 ms per c5 step over both passes). The NS operands X, X^T stay normal
+// stores: the products read them next (non-temporal there measured 7% slower).
+template <class V>
+__device__ __forceinline__ V ldg_nt(const V* p) {
+  return __builtin_nontemporal_load(p);
+}
+template <class V>
+__device__ __forceinline__ void stg_nt(V* p, V v) {
+  __builtin_nontemporal_store(v, p);
+}
+
 template <int ST>
 __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t tileT[kTile][kTile + kPad];
@@ -77,15 +92,17 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
     const long long base = (long long)row * a.cols + col;
     if (vec && in[3]) {
       if (a.g_dtype == DT_F32) {
-        const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(g) + base);
+        const f32x4_t t =
+            ldg_nt(reinterpret_cast<const f32x4_t*>(static_cast<const float*>(g) + base));
         gv[0] = t.x; gv[1] = t.y; gv[2] = t.z; gv[3] = t.w;
       } else {
-        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(g) + base);
+        const u32x2_t t =
+            ldg_nt(reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(g) + base));
         gv[0] = bf2f(t.x & 0xffff); gv[1] = bf2f(t.x >> 16);
         gv[2] = bf2f(t.y & 0xffff); gv[3] = bf2f(t.y >> 16);
       }
       if (read_buf) {
-        const float4 t = *reinterpret_cast<const float4*>(buf + base);
+        const f32x4_t t = ldg_nt(reinterpret_cast<const f32x4_t*>(buf + base));
         bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
       }
     } else {
@@ -114,7 +131,8 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
     }
     if (ST != PRE_F16 && buf) {
       if (vec && in[3]) {
-        *reinterpret_cast<float4*>(buf + base) = make_float4(nb[0], nb[1], nb[2], nb[3]);
+        f32x4_t t; t.x = nb[0]; t.y = nb[1]; t.z = nb[2]; t.w = nb[3];
+        stg_nt(reinterpret_cast<f32x4_t*>(buf + base), t);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
