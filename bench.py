@@ -162,6 +162,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=60.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 1 GiB device-to-device copy (HBM counter scale)")
+    ap.add_argument("--overlap-staging", action="store_true",
+                    help="Muon(overlap_staging=True): stage the next chunk on a second stream")
     ap.add_argument("--library-compare", action="store_true",
                     help="only time the NT MFMA kernel against torch's library GEMM "
                          "(hipBLASLt) on one NT-form bf16 product and print that JSON line")
@@ -202,7 +204,8 @@ def main():
         ns = dmuon.NewtonSchulz("gram")                   # Polar-Express, restarts [2]
     else:
         ns = dmuon.NewtonSchulz("direct", coefficients=KELLER)
-    opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=ns)
+    opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=ns,
+                     overlap_staging=args.overlap_staging)
     n_mats = sum(1 for _ in model.parameters())
     n_elems = sum(p.numel() for p in model.parameters())
     flops = sum(ns_useful_flops(*p.shape, 5, ns.backend, ns.restart_iterations)
