@@ -628,6 +628,39 @@ void nt_mfma_kernel(const NtArgs a) {
             rsB, (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * T::NW), 16, offb[q], so_, 0, 0);    \
   } while (0)
 
+  // 8-wave tiles alternate the DMA between the two halves of the block (waves w and w + 4 share
+  // a SIMD when waves are dealt round-robin): the waves of half kt & 1 issue the whole of slice
+  // kt + 2 while their SIMD partners keep issuing MFMAs (measured 1.1% on the c5 step, 2-3% on
+  // the full products). A wave then has at most one slice of loads in flight, so the vmcnt(0)
+  // at each slice barrier still waits for exactly the next slice.
+  constexpr bool PP = T::NW == 8;
+  constexpr int HW = T::NW / 2;
+  const int vw = wave % HW, half = wave / HW;
+  unsigned offa2[16], offb2[16];
+  if constexpr (PP) {
+#pragma unroll
+    for (int q = 0; q < 2 * T::A_INST; ++q) {
+      const int r = (HW * q + vw) * T::RPI + lrow;
+      offa2[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8) * 2u;
+    }
+#pragma unroll
+    for (int q = 0; q < 2 * T::B_INST; ++q) {
+      const int r = (HW * q + vw) * T::RPI + lrow;
+      offb2[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
+    }
+  }
+#define DMUON_ISSUE2(slice_, slot_)                                                            \
+  do {                                                                                         \
+    char* st_ = smem + (slot_) * T::STAGE + vw * 1024;                                         \
+    const unsigned so_ = (unsigned)((slice_) * BK * 2);                                        \
+    _Pragma("unroll") for (int q = 0; q < 2 * T::A_INST; ++q)                                  \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsA, (lds_ptr_t)(st_ + q * 1024 * HW), 16,    \
+                                                 offa2[q], so_, 0, 0);                         \
+    _Pragma("unroll") for (int q = 0; q < 2 * T::B_INST; ++q)                                  \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                              \
+            rsB, (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * HW), 16, offb2[q], so_, 0, 0);      \
+  } while (0)
+
   f32x16_t acc[T::TI][T::TJ];
 #pragma unroll
   for (int x = 0; x < T::TI; ++x)
@@ -666,10 +699,17 @@ void nt_mfma_kernel(const NtArgs a) {
   // and slot kt % S is free, so the DMA of slice kt+S and the reads of slice kt+1's first
   // fragments both run under the last substep's MFMAs and no wave starts a slice with an empty
   // pipeline. Past the end the DMA re-fetches the last slice into the free slot (never read),
-  // which keeps the number of loads per iteration, and so the vmcnt targets, uniform.
+  // which keeps the number of loads per iteration, and so the vmcnt targets, uniform. With the
+  // alternating halves, half 0 issues slice 0 and waits for it, half 1 only issues slice 1.
+  if constexpr (PP) {
+    static_assert(S == 2, "alternating DMA halves need the two-slot ring");
+    if (half == 0) { DMUON_ISSUE2(0, 0); wait_vmcnt<0>(); }
+    else DMUON_ISSUE2(min(1, KT - 1), 1);
+  } else {
 #pragma unroll
-  for (int s0 = 0; s0 < S; ++s0) DMUON_ISSUE(min(s0, KT - 1), s0);
-  wait_slices<T>(S - 1);
+    for (int s0 = 0; s0 < S; ++s0) DMUON_ISSUE(min(s0, KT - 1), s0);
+    wait_slices<T>(S - 1);
+  }
   bare_barrier();
   load_frags(smem, smem + T::A_BYTES, 0, af[0], bfr[0]);
 
@@ -700,7 +740,11 @@ void nt_mfma_kernel(const NtArgs a) {
       const char* na = smem + ((kt + 1) % S) * T::STAGE;
       load_frags(na, na + T::A_BYTES, 0, af[0], bfr[0]);
     }
-    DMUON_ISSUE(min(kt + S, KT - 1), kt % S);
+    if constexpr (PP) {
+      if (half == (kt & 1)) DMUON_ISSUE2(min(kt + S, KT - 1), kt % S);
+    } else {
+      DMUON_ISSUE(min(kt + S, KT - 1), kt % S);
+    }
 #pragma unroll
     for (int x = 0; x < T::TI; ++x)
 #pragma unroll
@@ -709,6 +753,7 @@ void nt_mfma_kernel(const NtArgs a) {
     sched_front<0, NM, NF, T::LPT>();
   }
 #undef DMUON_ISSUE
+#undef DMUON_ISSUE2
   wait_vmcnt<0>();
   bare_barrier();
 
