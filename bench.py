@@ -259,6 +259,10 @@ def main():
     achieved_tf = mf_flops / (mf_ms * 1e-3) / 1e12
     pre = prof["pre"]
     pre_gbs = pre["bytes"] / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
+    # what the two staging passes actually move: gradient (2 B) and momentum (4 + 4 B), then
+    # gradient and new momentum again (6 B) and the fp16 copy and its transpose (4 B)
+    pre_actual = n_elems * 20.0 * prof_steps
+    pre_actual_gbs = pre_actual / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
 
     # ---- gradient clipping of the same Muon gradients (segmented HIP kernels), reported apart --
     clip = None
@@ -383,7 +387,9 @@ def main():
             "bound": "hbm", "achieved": None if pre_gbs is None else round(pre_gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": None if pre_gbs is None else round(pre_gbs / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes_per_elem": 18,
+            "algorithmic_bytes_per_elem": 12,
+            "actual_bytes_per_elem": 20,
+            "actual_gbs": None if pre_actual_gbs is None else round(pre_actual_gbs, 1),
         },
         "kernel_classes": classes,
         "grad_clip": clip,
