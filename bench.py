@@ -162,6 +162,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=60.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run one plain 1 GiB device-to-device copy (HBM counter scale)")
+    ap.add_argument("--two-pass-staging", action="store_true",
+                    help="Muon(single_pass_staging=False): stage the NS operand after the norm, "
+                         "in a second pass")
     ap.add_argument("--overlap-staging", action="store_true",
                     help="Muon(overlap_staging=True): stage the next chunk on a second stream")
     ap.add_argument("--library-compare", action="store_true",
@@ -205,7 +208,8 @@ def main():
     else:
         ns = dmuon.NewtonSchulz("direct", coefficients=KELLER)
     opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=ns,
-                     overlap_staging=args.overlap_staging)
+                     overlap_staging=args.overlap_staging,
+                     single_pass_staging=not args.two_pass_staging)
     n_mats = sum(1 for _ in model.parameters())
     n_elems = sum(p.numel() for p in model.parameters())
     flops = sum(ns_useful_flops(*p.shape, 5, ns.backend, ns.restart_iterations)
@@ -259,9 +263,11 @@ def main():
     achieved_tf = mf_flops / (mf_ms * 1e-3) / 1e12
     pre = prof["pre"]
     pre_gbs = pre["bytes"] / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
-    # what the two staging passes actually move: gradient (2 B) and momentum (4 + 4 B), then
-    # gradient and new momentum again (6 B) and the fp16 copy and its transpose (4 B)
-    pre_actual = n_elems * 20.0 * prof_steps
+    # what the staging actually moves per element: gradient (2 B), momentum (4 + 4 B) and the
+    # fp16 copy and its transpose (4 B) in one pass with the kept scale (Muon's default); two
+    # passes re-read the gradient and the new momentum (6 B more)
+    actual_per_elem = 14.0 if opt._single_pass else 20.0
+    pre_actual = n_elems * actual_per_elem * prof_steps
     pre_actual_gbs = pre_actual / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
 
     # ---- gradient clipping of the same Muon gradients (segmented HIP kernels), reported apart --
@@ -382,13 +388,16 @@ def main():
             "launches_per_step": mf_launch // prof_steps,
         },
         "roofline_elementwise": {
-            "kernel": ("muon_pre_kernel: momentum + Nesterov + norm partials, then fp16 "
+            "kernel": ("muon_pre_kernel: momentum + Nesterov + norm partials + fp16 staging of "
+                       "ns_in with the kept scale in one pass (a second pass only for matrices "
+                       "whose scale moved by more than 4x)" if opt._single_pass else
+                       "muon_pre_kernel: momentum + Nesterov + norm partials, then fp16 "
                        "staging of ns_in / ||ns_in|| (two passes)"),
             "bound": "hbm", "achieved": None if pre_gbs is None else round(pre_gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": None if pre_gbs is None else round(pre_gbs / HBM_PEAK_GBS, 4),
             "algorithmic_bytes_per_elem": 12,
-            "actual_bytes_per_elem": 20,
+            "actual_bytes_per_elem": actual_per_elem,
             "actual_gbs": None if pre_actual_gbs is None else round(pre_actual_gbs, 1),
         },
         "kernel_classes": classes,

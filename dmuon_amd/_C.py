@@ -46,11 +46,11 @@ _SIGNATURES = {
     "dmuon_muon_update": (c_int, [c_vp, c_int, c_vp, c_int, c_i64, c_int, c_f, c_f, c_vp]),
     "dmuon_ns_plan": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int),
                               ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_i64)]),
-    "dmuon_muon_step_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_vp, c_int, c_int, c_int,
-                                      c_int, c_d, c_d, c_d, c_int, c_int, c_fp, c_int, c_int, c_ip,
-                                      c_int, c_f, c_vp, c_i64, c_int, c_vp]),
-    "dmuon_muon_stage_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_d, c_int, c_int,
-                                       c_int, c_f, c_vp, c_i64, c_int, c_vp]),
+    "dmuon_muon_step_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_int, c_int,
+                                      c_int, c_int, c_d, c_d, c_d, c_int, c_int, c_fp, c_int,
+                                      c_int, c_ip, c_int, c_f, c_vp, c_i64, c_int, c_vp]),
+    "dmuon_muon_stage_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_d, c_int,
+                                       c_int, c_int, c_f, c_vp, c_i64, c_int, c_vp]),
     "dmuon_muon_apply_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_d, c_d,
                                        c_fp, c_int, c_int, c_ip, c_int, c_vp, c_i64, c_int, c_vp]),
     "dmuon_newton_schulz_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_fp,

@@ -48,6 +48,10 @@ struct Workspace {
   // Gram backend only: the accumulated polynomial Q and its transpose (ping-pong), P R
   uint16_t *Q0, *Q1, *Q0T, *Q1T, *Wm;
   float *partials, *scale, *scale_sq;
+  // correction of a copy staged with an estimated scale (1 when staged exactly), and the
+  // per-matrix "stage again" flags
+  float *ratio, *ratio_sq;
+  int* restage;
   int nparts;
   int64_t bytes;
 };
@@ -80,6 +84,9 @@ Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch, int
   w.partials = reinterpret_cast<float*>(take(L * w.nparts * 4));
   w.scale = reinterpret_cast<float*>(take(L * 4));
   w.scale_sq = reinterpret_cast<float*>(take(L * 4));
+  w.ratio = reinterpret_cast<float*>(take(L * 4));
+  w.ratio_sq = reinterpret_cast<float*>(take(L * 4));
+  w.restage = reinterpret_cast<int*>(take(L * 4));
   w.bytes = off;
   return w;
 }
@@ -204,9 +211,14 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     return timed(PC_POLY, tri ? tri_sq_flops : full_sq_flops, 0.0, stream, who,
                  [&] { return launch_nt(s, tile, stream); });
   };
+  // The staged X may carry an estimated scale: the first products that read it multiply by the
+  // per-matrix correction (ratio for X, ratio_sq for X X^T; 1 after an exact staging). A
+  // restart rewrites X exactly scaled.
+  bool x_staged = true;
   // R = alpha X X^T
   auto gram_of_x = [&](uint16_t* R, float alpha) -> int {
     NtArgs s{};
+    s.alpha_dev = x_staged ? w.ratio_sq : nullptr;
     s.elt = ELT_F16;
     s.A = w.X; s.lda = n_pad; s.sA = xs;
     s.B = w.X; s.ldb = n_pad; s.sB = xs;
@@ -222,6 +234,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
   // X <- Q X (an NS restart), or the final U = Q X / KX with the Muon update in the epilogue
   auto qx = [&](const uint16_t* Q, bool last) -> int {
     NtArgs g{};
+    g.alpha_dev = x_staged ? w.ratio : nullptr;
     g.elt = ELT_F16;
     g.A = Q; g.lda = m_pad; g.sA = as;
     g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
@@ -236,6 +249,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
       if (timed(PC_GEMM, gemm_flops, 0.0, stream, who, [&] { return launch_nt(g, tile, stream); }))
         return 1;
       uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
+      x_staged = false;
       return 0;
     }
     g.alpha = 1.f / kNsKx;
@@ -317,8 +331,8 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
 // phases: PH_STAGE (momentum, norm, NS operand staging into the workspace), PH_APPLY (the NS
 // products and the fused update / output from a staged workspace), or both.
 enum { PH_STAGE = 1, PH_APPLY = 2 };
-int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* const* w_ptrs,
-              int w_dtype, void* const* pub_ptrs, int pub_dtype, void* const* out_ptrs,
+int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* const* est_ptrs,
+              void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype, void* const* out_ptrs,
               int out_dtype, int rows, int cols, int batch,
               float mu, int nesterov, int first_step, float decay, float lrs, const float* coeffs,
               int T, int backend, const int* restarts, int n_restarts, float eps, void* workspace,
@@ -386,18 +400,28 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
   // the first step) and write, one 2-byte copy of the normalised ns_in. The second pass's
   // re-read of the gradient and the new momentum (fp16 cannot hold an un-normalised gradient,
   // so the copy waits for the norm) and its transposed copy are overhead, not counted.
+  // With est_ptrs (a per-matrix scale kept from the previous step) the first pass also writes
+  // the fp16 copy as fp16(kx * est * ns_in); the norm finalize then keeps that copy when
+  // r = scale / est is within [1/4, 4] (the first products multiply by r or r^2, and every copy
+  // entry stays below kx / r <= 2^14) and otherwise flags the matrix for the second pass,
+  // which then stages exactly as without an estimate.
+  const bool est = est_ptrs != nullptr;
   const double mom_bytes = buf_ptrs ? (first_step ? 4.0 : 8.0) : 0.0;
-  const double pre_bytes = elems * (gbytes + mom_bytes);
+  const double pre_bytes = elems * (gbytes + mom_bytes + (est ? 2.0 : 0.0));
+  p.stage = est ? PRE_EST : PRE_NORM;
+  p.est_ptrs = est_ptrs;
+  p.kx = kNsKx;
   if (timed(PC_PRE, 0.0, pre_bytes, stream, who, [&] { return launch_pre(p, stream); })) return 1;
   if (timed(PC_NORM, 0.0, (double)batch * w.nparts * 4, stream, who, [&] {
-        return launch_norm_finalize(w.partials, w.nparts, batch, eps, w.scale, w.scale_sq, stream);
+        return launch_norm_finalize_est(w.partials, w.nparts, batch, eps, w.scale, w.scale_sq,
+                                        est_ptrs, w.ratio, w.ratio_sq, w.restage, stream);
       }))
     return 1;
   {
     p.stage = PRE_F16;
     p.scale = w.scale;
-    p.kx = kNsKx;
-    const double st_bytes = elems * 2.0;
+    p.restage = est ? w.restage : nullptr;
+    const double st_bytes = est ? 0.0 : elems * 2.0;
     if (timed(PC_PRE, 0.0, st_bytes, stream, who, [&] { return launch_pre(p, stream); }))
       return 1;
   }
@@ -431,6 +455,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
     s.sym_exact = 1;
     s.mode = EPI_SYM; s.alpha = rs / (kNsKx * kNsKx); s.beta = 0.f; s.diag = 0.f;
+    s.alpha_dev = it == 0 ? w.ratio_sq : nullptr;   // the staged X's scale correction
     s.D = w.Am; s.ldd = m_pad; s.sD = as;
     if (timed(PC_SYRK, syrk_flops, 0.0, stream, who, [&] { return launch_nt(s, tile, stream); }))
       return 1;
@@ -455,6 +480,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, void* co
     g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch;
     g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.alpha = it + 1 < T ? 1.f : 1.f / kNsKx; g.beta = ca;
+    g.alpha_dev = it == 0 ? w.ratio : nullptr;
     g.C = w.X; g.ldc = n_pad; g.sC = xs;
     if (it + 1 < T) {
       g.mode = EPI_NS;
@@ -514,7 +540,7 @@ int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* 
   return rc;
 }
 
-int dmuon_abi_version(void) { return 102; }
+int dmuon_abi_version(void) { return 103; }
 
 int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
                     int64_t strideB, const void* C, int64_t ldc, int64_t strideC, void* D,
@@ -765,11 +791,12 @@ int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int 
 }
 
 int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
-                          void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype,
-                          int rows, int cols, int batch, double lr, double mu, double wd,
-                          int nesterov, int first_step, const float* coeffs, int T, int backend,
-                          const int* restarts, int n_restarts, float eps, void* workspace,
-                          int64_t workspace_bytes, int tile, void* stream) {
+                          float* const* est_ptrs, void* const* w_ptrs, int w_dtype,
+                          void* const* pub_ptrs, int pub_dtype, int rows, int cols, int batch,
+                          double lr, double mu, double wd, int nesterov, int first_step,
+                          const float* coeffs, int T, int backend, const int* restarts,
+                          int n_restarts, float eps, void* workspace, int64_t workspace_bytes,
+                          int tile, void* stream) {
   const char* who = "dmuon_muon_step_group";
   if (batch == 0) return 0;
   if (!buf_ptrs || !w_ptrs) return fail("%s: buf_ptrs and w_ptrs must be non-NULL", who);
@@ -777,8 +804,9 @@ int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_pt
   const double scale = 0.2 * sqrt((double)(rows > cols ? rows : cols));
   const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
   const float lrs = (float)(lr * scale);
-  return run_group(g_ptrs, g_dtype, buf_ptrs, w_ptrs, w_dtype, pub_ptrs, pub_dtype, nullptr, 0,
-                   rows, cols, batch, (float)mu, nesterov, first_step, decay, lrs, coeffs, T,
+  return run_group(g_ptrs, g_dtype, buf_ptrs, est_ptrs, w_ptrs, w_dtype, pub_ptrs, pub_dtype,
+                   nullptr, 0, rows, cols, batch, (float)mu, nesterov, first_step, decay, lrs,
+                   coeffs, T,
                    backend, restarts, n_restarts, eps, workspace, workspace_bytes, tile,
                    static_cast<hipStream_t>(stream), who);
 }
@@ -790,21 +818,22 @@ int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out
   const char* who = "dmuon_newton_schulz_group";
   if (batch == 0) return 0;
   if (!out_ptrs) return fail("%s: out_ptrs must be non-NULL", who);
-  return run_group(g_ptrs, g_dtype, nullptr, nullptr, 0, nullptr, 0, out_ptrs, out_dtype, rows,
+  return run_group(g_ptrs, g_dtype, nullptr, nullptr, nullptr, 0, nullptr, 0, out_ptrs, out_dtype,
+                   rows,
                    cols, batch, 0.f, 0, 1, 1.f, 0.f, coeffs, T, backend, restarts, n_restarts,
                    eps, workspace, workspace_bytes, tile,
                    static_cast<hipStream_t>(stream), who);
 }
 
-int dmuon_muon_stage_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, int rows,
-                           int cols, int batch, double mu, int nesterov, int first_step,
+int dmuon_muon_stage_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
+                           float* const* est_ptrs, int rows, int cols, int batch, double mu, int nesterov, int first_step,
                            int backend, float eps, void* workspace, int64_t workspace_bytes,
                            int tile, void* stream) {
   const char* who = "dmuon_muon_stage_group";
   if (batch == 0) return 0;
   if (!buf_ptrs) return fail("%s: buf_ptrs must be non-NULL", who);
-  return run_group(g_ptrs, g_dtype, buf_ptrs, nullptr, 0, nullptr, 0, nullptr, 0, rows, cols,
-                   batch, (float)mu, nesterov, first_step, 1.f, 0.f, nullptr, 0, backend,
+  return run_group(g_ptrs, g_dtype, buf_ptrs, est_ptrs, nullptr, 0, nullptr, 0, nullptr, 0, rows,
+                   cols, batch, (float)mu, nesterov, first_step, 1.f, 0.f, nullptr, 0, backend,
                    nullptr, 0, eps, workspace, workspace_bytes, tile,
                    static_cast<hipStream_t>(stream), who, PH_STAGE);
 }
@@ -820,7 +849,8 @@ int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_pt
   const double scale = 0.2 * sqrt((double)(rows > cols ? rows : cols));
   const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
   const float lrs = (float)(lr * scale);
-  return run_group(nullptr, 0, nullptr, w_ptrs, w_dtype, pub_ptrs, pub_dtype, nullptr, 0, rows,
+  return run_group(nullptr, 0, nullptr, nullptr, w_ptrs, w_dtype, pub_ptrs, pub_dtype, nullptr, 0,
+                   rows,
                    cols, batch, 0.f, 0, 0, decay, lrs, coeffs, T, backend, restarts, n_restarts,
                    0.f, workspace, workspace_bytes, tile, static_cast<hipStream_t>(stream), who,
                    PH_APPLY);

@@ -47,8 +47,11 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream);
 //   PRE_BF16  momentum update, bf16 ns_in into Y / YT, norm partials (direct NS staging)
 //   PRE_NORM  momentum update and norm partials only
 //   PRE_F16   after PRE_NORM + norm finalise: recompute ns_in from g and the updated buffer
-//             and write fp16(kx * scale * ns_in) into Y / YT (Gram NS staging); no buffer write
-enum { PRE_BF16 = 0, PRE_NORM = 1, PRE_F16 = 2 };
+//             and write fp16(kx * scale * ns_in) into Y / YT; no buffer write. With `restage`,
+//             only the matrices whose flag is set (the others return at once)
+//   PRE_EST   momentum update, norm partials and fp16(kx * est * ns_in) into Y / YT, est being
+//             the matrix's previous 1/(||ns_in|| + eps) (*est_ptrs[l]); est <= 0: no copy
+enum { PRE_BF16 = 0, PRE_NORM = 1, PRE_F16 = 2, PRE_EST = 3 };
 
 struct PreArgs {
   void* const* g_ptrs; int g_dtype;       // per-matrix gradient (rows x cols, row-major)
@@ -60,6 +63,8 @@ struct PreArgs {
   float mu; int first_step, nesterov;
   int stage;                              // PRE_*
   const float* scale; float kx;           // PRE_F16: per-matrix 1/(||ns_in|| + eps), power of 2
+  float* const* est_ptrs;                 // PRE_EST: per-matrix scale estimate (device float)
+  const int* restage;                     // PRE_F16: optional per-matrix "copy needed" flags
 };
 hipError_t launch_pre(const PreArgs& a, hipStream_t stream);
 int pre_blocks_per_mat(int Rp, int Cp);
@@ -68,6 +73,15 @@ int pre_blocks_per_mat(int Rp, int Cp);
 // scale[l] = 1/(sqrt(sum partials[l]) + eps), scale_sq[l] = scale^2
 hipError_t launch_norm_finalize(const float* partials, int nparts, int L, float eps,
                                 float* scale, float* scale_sq, hipStream_t stream);
+
+// The same, plus the correction of a copy staged with an estimated scale: with est_ptrs and
+// est = *est_ptrs[l] > 0 and r = scale / est in [1/4, 4], ratio[l] = r, ratio_sq[l] = r^2 and
+// restage[l] = 0 (the staged copy times r is the exactly scaled one); otherwise ratio = 1,
+// ratio_sq = 1, restage = 1 (stage again with the exact scale). *est_ptrs[l] becomes scale.
+hipError_t launch_norm_finalize_est(const float* partials, int nparts, int L, float eps,
+                                    float* scale, float* scale_sq, float* const* est_ptrs,
+                                    float* ratio, float* ratio_sq, int* restage,
+                                    hipStream_t stream);
 
 struct UpdateArgs {
   void* const* w_ptrs; int w_dtype;

@@ -65,6 +65,9 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
   __shared__ float red[4];
 
   const int l = blockIdx.z;
+  if constexpr (ST == PRE_F16) {
+    if (a.restage && !a.restage[l]) return;   // the single-pass copy of this matrix stands
+  }
   const int r0 = blockIdx.y * kTile, c0 = blockIdx.x * kTile;
   const int tid = threadIdx.x;
   const int tc = tid & 15, tr = tid >> 4;
@@ -77,7 +80,11 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
   const bool vec = (a.cols & 3) == 0;
   // PRE_F16 reads the buffer PRE_NORM left (the new momentum) and only recomputes ns_in
   const bool read_buf = buf && (ST == PRE_F16 || !a.first_step);
-  const float sc = ST == PRE_F16 ? a.scale[l] * a.kx : 1.f;
+  float sc = 1.f;
+  if constexpr (ST == PRE_F16) sc = a.scale[l] * a.kx;
+  if constexpr (ST == PRE_EST) sc = *a.est_ptrs[l] * a.kx;
+  // PRE_EST without a usable estimate: momentum and partials only (the copy is staged later)
+  const bool copy = ST != PRE_NORM && (ST != PRE_EST || sc > 0.f);
 
   float ss = 0.f;
 #pragma unroll
@@ -129,7 +136,7 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
       if (!in[e]) ns[e] = 0.f;
       ss += ns[e] * ns[e];
     }
-    if (ST != PRE_F16 && buf) {
+    if (ST != PRE_F16 && buf) {   // PRE_BF16, PRE_NORM, PRE_EST write the new momentum
       if (vec && in[3]) {
         f32x4_t t; t.x = nb[0]; t.y = nb[1]; t.z = nb[2]; t.w = nb[3];
         stg_nt(reinterpret_cast<f32x4_t*>(buf + base), t);
@@ -139,10 +146,11 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
           if (in[e]) buf[base + e] = nb[e];
       }
     }
-    if constexpr (ST == PRE_NORM) continue;
+    if (!copy) continue;
     uint16_t o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = ST == PRE_F16 ? f2h(__fmul_rn(ns[e], sc)) : f2bf(ns[e]);
+    for (int e = 0; e < 4; ++e)
+      o[e] = ST == PRE_BF16 ? f2bf(ns[e]) : f2h(__fmul_rn(ns[e], sc));
     if (row < a.Rp) {
       uint2 p;
       p.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
@@ -152,7 +160,7 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) tileT[4 * tc + e][rl] = o[e];
   }
-  if constexpr (ST != PRE_NORM) {
+  if (copy) {   // block-uniform
     __syncthreads();
     // transposed write: row cl of YT gets 64 consecutive source rows (128 B)
     const int cl = tid >> 2, seg = tid & 3;
@@ -217,6 +225,41 @@ __global__ __launch_bounds__(256) void muon_update_kernel(const UpdateArgs a) {
   }
 }
 
+__global__ __launch_bounds__(256) void norm_finalize_est_kernel(
+    const float* partials, int nparts, float eps, float* scale, float* scale_sq,
+    float* const* est_ptrs, float* ratio, float* ratio_sq, int* restage) {
+  __shared__ double red[256];
+  const int l = blockIdx.x;
+  double s = 0.0;
+  for (int p = threadIdx.x; p < nparts; p += 256) s += (double)partials[(long long)l * nparts + p];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float nrm = (float)sqrt(red[0]);
+    const float sc = 1.0f / (nrm + eps);
+    scale[l] = sc;
+    scale_sq[l] = sc * sc;
+    float r = 1.f;
+    bool ok = false;
+    if (est_ptrs) {
+      const float est = *est_ptrs[l];
+      if (est > 0.f) {
+        r = sc / est;
+        ok = r >= 0.25f && r <= 4.f;   // false for NaN / inf too
+      }
+      *est_ptrs[l] = sc;
+    }
+    if (!ok) r = 1.f;
+    ratio[l] = r;
+    ratio_sq[l] = r * r;
+    restage[l] = ok ? 0 : 1;
+  }
+}
+
 }  // namespace
 
 int pre_blocks_per_mat(int Rp, int Cp) { return (Rp / kTile) * (Cp / kTile); }
@@ -227,8 +270,19 @@ hipError_t launch_pre(const PreArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(muon_pre_kernel<PRE_NORM>, grid, block, 0, stream, a);
   else if (a.stage == PRE_F16)
     hipLaunchKernelGGL(muon_pre_kernel<PRE_F16>, grid, block, 0, stream, a);
+  else if (a.stage == PRE_EST)
+    hipLaunchKernelGGL(muon_pre_kernel<PRE_EST>, grid, block, 0, stream, a);
   else
     hipLaunchKernelGGL(muon_pre_kernel<PRE_BF16>, grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_norm_finalize_est(const float* partials, int nparts, int L, float eps,
+                                    float* scale, float* scale_sq, float* const* est_ptrs,
+                                    float* ratio, float* ratio_sq, int* restage,
+                                    hipStream_t stream) {
+  hipLaunchKernelGGL(norm_finalize_est_kernel, dim3(L), dim3(256), 0, stream, partials, nparts,
+                     eps, scale, scale_sq, est_ptrs, ratio, ratio_sq, restage);
   return hipGetLastError();
 }
 

@@ -57,7 +57,13 @@ class Muon(torch.optim.Optimizer):
     same-shape matrices is processed in chunks that fit); ``overlap_staging=True`` stages the
     next chunk on a side stream while the current chunk's NS runs, with two such workspaces
     (bit-identical results; off by default: on MI355X the concurrent staging traffic slows the
-    MFMA kernels by about as much as it hides).
+    MFMA kernels by about as much as it hides). ``single_pass_staging=True`` (the default) keeps
+    each parameter's last NS input scale ``1/(||ns_in|| + eps)`` in
+    ``state[id(dp)]["ns_scale"]`` and stages the fp16 NS operand with it in the momentum pass;
+    the first NS products correct the estimate exactly when it is within a factor of 4 of the
+    new scale, and the operand is staged again otherwise (always on a parameter's first step).
+    This saves the second pass over the gradient and the momentum buffer; results differ from
+    ``single_pass_staging=False`` by the fp16 rounding of that operand.
     """
 
     def __init__(
@@ -78,6 +84,7 @@ class Muon(torch.optim.Optimizer):
         workspace_limit_bytes: int = 8 << 30,
         ns_eps: float = 1e-7,
         overlap_staging: bool = False,
+        single_pass_staging: bool = True,
         **kwargs,
     ):
         if isinstance(ns_backend, str):
@@ -100,6 +107,7 @@ class Muon(torch.optim.Optimizer):
         self._workspace_limit = int(workspace_limit_bytes)
         self._workspaces: list = [None, None]
         self._overlap_staging = bool(overlap_staging)
+        self._single_pass = bool(single_pass_staging)
         self._side_streams: dict = {}
         self._last_step_profile: dict = {}
         self._optimizer_step_index = 0
@@ -291,6 +299,8 @@ class Muon(torch.optim.Optimizer):
                     if "momentum_buffer" not in st:
                         st["momentum_buffer"] = torch.zeros((rows, cols), dtype=torch.float32,
                                                             device=dev)
+                    if self._single_pass and "ns_scale" not in st:
+                        st["ns_scale"] = torch.zeros(1, dtype=torch.float32, device=dev)
                     if not dp._owned_data.is_contiguous():
                         raise RuntimeError(f"{dp.param_name}: Muon needs a contiguous weight")
                 tile, _, _, nbytes = _C.plan(rows, cols, len(part), 0, num_cus, backend)
@@ -323,11 +333,15 @@ class Muon(torch.optim.Optimizer):
                     side.wait_event(free[slot])
                 # contiguous copies (if any) on the staging stream, ordered before the staging
                 gs = [g if g.is_contiguous() else g.contiguous() for _, g in part]
+                ests = ([self.state[id(dp)]["ns_scale"].data_ptr() for dp, _ in part]
+                        if self._single_pass else [])
                 ptrs = _pinned_ptrs([t.data_ptr() for t in gs]
                                     + [self.state[id(dp)]["momentum_buffer"].data_ptr()
-                                       for dp, _ in part], dev)
+                                       for dp, _ in part] + ests, dev)
                 _C.call("dmuon_muon_stage_group", ptrs.data_ptr(), _float_dtype_code(gs[0]),
-                        ptrs.data_ptr() + 8 * L, rows, cols, L, mu, int(self._nesterov),
+                        ptrs.data_ptr() + 8 * L,
+                        ptrs.data_ptr() + 16 * L if ests else None, rows, cols, L, mu,
+                        int(self._nesterov),
                         int(first), backend, self._ns_eps, ws.data_ptr(), ws.numel(), tile,
                         side.cuda_stream)
                 if overlap:

@@ -154,7 +154,7 @@ int dmuon_muon_update(void* const* w_ptrs, int w_dtype, const void* const* u_ptr
  * Planning for a group of `batch` same-shape rows x cols matrices: NS dims m = min, n = max,
  * chosen output tile (tile_req 0 = automatic, else 128 or 256), padded m_pad / n_pad and the
  * workspace bytes dmuon_muon_step_group / dmuon_newton_schulz_group need for `backend`
- * (DMUON_NS_GRAM needs three more m_pad x m_pad bf16 matrices per group member). Host-only.
+ * (DMUON_NS_GRAM needs five more m_pad x m_pad fp16 matrices per group member). Host-only.
  */
 int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int backend,
                   int* tile, int* m_pad, int* n_pad, int64_t* workspace_bytes);
@@ -167,19 +167,28 @@ int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int 
  * and, when pub_ptrs != NULL, pub[l] <- round_to_pub_dtype(new W[l]) in the same epilogue (the
  * owner's forward copy when W is a master in another dtype; NULL when W is the forward tensor).
  * backend DMUON_NS_DIRECT: each step is SYRK (A = X X^T) -> SYRK-poly (b*A + c*A A^T) -> GEMM
- *   (a*X + P X) on bf16 MFMA (direct_newton_schulz, newton_schulz.py:225-273).
+ *   (a*X + P X) on fp16 MFMA (direct_newton_schulz, newton_schulz.py:225-273).
  * backend DMUON_NS_GRAM: gram_newton_schulz (newton_schulz.py:333-448): R = X X^T once; per step
  *   P = a I + b R + c R R, Q <- P Q, R <- (R P) P, all m x m; at each step index listed in
  *   restarts[0 .. n_restarts-1] (HOST array; index 0 ignored) X <- Q X and R = X X^T again;
  *   finally U = Q X. Fewer flops than direct when n > m.
+ * est_ptrs (optional, device array of `batch` pointers to one fp32 each, kept by the caller per
+ *   param across steps, initially 0): single-pass staging. Each holds the param's previous
+ *   1 / (||ns_in|| + eps); the momentum pass then also writes the fp16 NS operand with that
+ *   scale, the first products correct it by r = scale / est when r is within [1/4, 4], and a
+ *   param outside that range (or with est <= 0) is staged again exactly; *est_ptrs[l] is
+ *   updated in place. NULL: two staging passes, the operand always exactly scaled. The results
+ *   of the two modes differ by the fp16 rounding of that operand. No reference counterpart
+ *   (the reference stages per param with torch ops).
  * workspace: device memory of at least the planned bytes; its contents need no initialisation.
  */
 int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
-                          void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype,
-                          int rows, int cols, int batch, double lr, double mu, double wd,
-                          int nesterov, int first_step, const float* coeffs, int T, int backend,
-                          const int* restarts, int n_restarts, float eps, void* workspace,
-                          int64_t workspace_bytes, int tile, void* stream);
+                          float* const* est_ptrs, void* const* w_ptrs, int w_dtype,
+                          void* const* pub_ptrs, int pub_dtype, int rows, int cols, int batch,
+                          double lr, double mu, double wd, int nesterov, int first_step,
+                          const float* coeffs, int T, int backend, const int* restarts,
+                          int n_restarts, float eps, void* workspace, int64_t workspace_bytes,
+                          int tile, void* stream);
 
 /*
  * dmuon_muon_step_group in two halves, for callers that overlap the bandwidth-bound half of one
@@ -194,8 +203,8 @@ int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_pt
  * dmuon_muon_step_group's bit for bit. No reference counterpart (the reference runs the step
  * per parameter on one stream); it serves the same seam, muon.py:1683-1740.
  */
-int dmuon_muon_stage_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, int rows,
-                           int cols, int batch, double mu, int nesterov, int first_step,
+int dmuon_muon_stage_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
+                           float* const* est_ptrs, int rows, int cols, int batch, double mu, int nesterov, int first_step,
                            int backend, float eps, void* workspace, int64_t workspace_bytes,
                            int tile, void* stream);
 int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_ptrs,

@@ -181,13 +181,28 @@ def closed_form_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
     return out.T.copy() if t else out
 
 
+def staged_scale(s: np.float32, scale_est: Optional[float]):
+    """The device's choice between an estimated and the exact operand scale (fp32 arithmetic as
+    the norm-finalize kernel): (scale used for the staged copy, correction r) — the estimate
+    with r = s / est when est > 0 and r is within [1/4, 4], else the exact s with r = 1."""
+    f32 = np.float32
+    if scale_est is not None and f32(scale_est) > 0:
+        r = f32(s) / f32(scale_est)
+        if f32(0.25) <= r <= f32(4.0):
+            return f32(scale_est), r
+    return f32(s), f32(1.0)
+
+
 def syrk_emulated_ns(G: np.ndarray, coefficients: Sequence = KELLER, eps: float = 1e-7,
-                     op_dtype: str = "fp16", kx: float = 4096.0) -> np.ndarray:
+                     op_dtype: str = "fp16", kx: float = 4096.0,
+                     scale_est: Optional[float] = None) -> np.ndarray:
     """The build's direct device pipeline (not the reference's rounding), rnd = op_dtype:
     X = rnd(kx s ns_in), s = 1/(||ns_in|| + eps); per step A = rnd(rs/kx^2 X X^T) with the
     stored-A scale rs = 2^floor(log2 m) (at most 2^12) on the first step and 1 after,
     P = rnd(c/rs^2 A A^T + b/rs A), X = rnd(P X + a X); the last step returns
-    U = fp32((P X + a X) / kx). A and P keep their upper triangle, mirrored."""
+    U = fp32((P X + a X) / kx). A and P keep their upper triangle, mirrored. scale_est: the
+    single-pass staging, X = rnd(kx est ns_in) and the first A and X products multiplied by
+    r^2 and r (`staged_scale`)."""
     X = np.asarray(G, dtype=np.float32)
     t = X.shape[0] > X.shape[1]
     if t:
@@ -195,7 +210,8 @@ def syrk_emulated_ns(G: np.ndarray, coefficients: Sequence = KELLER, eps: float 
     f32 = np.float32
     nrm = f32(np.sqrt(np.sum(X.astype(np.float64) ** 2)))
     s = f32(1.0) / (nrm + f32(eps))
-    Xq = rnd((X * f32(s * f32(kx))).astype(np.float32), op_dtype)
+    sx, r = staged_scale(s, scale_est)
+    Xq = rnd((X * f32(sx * f32(kx))).astype(np.float32), op_dtype)
     m = Xq.shape[0]
     kr = 1
     while kr * 2 <= m and kr < 4096:
@@ -203,11 +219,16 @@ def syrk_emulated_ns(G: np.ndarray, coefficients: Sequence = KELLER, eps: float 
     T = len(coefficients)
     for it, (a, b, c) in enumerate(coefficients):
         rs = f32(kr) if it == 0 else f32(1.0)
-        A = _upper_mirror(rnd(f32(rs / f32(kx * kx)) * _mm(Xq, Xq.T, "fp32"), op_dtype))
+        ra, rx = (f32(r * r), r) if it == 0 else (f32(1.0), f32(1.0))
+        A = _upper_mirror(rnd(f32(f32(rs / f32(kx * kx)) * ra) * _mm(Xq, Xq.T, "fp32"),
+                              op_dtype))
         P = _upper_mirror(rnd(f32(c) / (rs * rs) * _mm(A, A.T, "fp32") + f32(b) / rs * A,
                               op_dtype))
         Xn = _mm(P, Xq, "fp32") + f32(a) * Xq
-        Xq = (f32(1.0 / kx) * Xn).astype(np.float32) if it == T - 1 else rnd(Xn, op_dtype)
+        if it == T - 1:
+            Xq = (f32(f32(1.0 / kx) * rx) * Xn).astype(np.float32)
+        else:
+            Xq = rnd(rx * Xn if rx != 1 else Xn, op_dtype)
     if t:
         Xq = Xq.T
     return np.ascontiguousarray(Xq)
@@ -221,7 +242,8 @@ def _upper_mirror(D: np.ndarray) -> np.ndarray:
 
 def syrk_emulated_gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
                           restart_iterations: Optional[Sequence[int]] = None, eps: float = 1e-7,
-                          op_dtype: str = "fp16", kx: float = 4096.0) -> np.ndarray:
+                          op_dtype: str = "fp16", kx: float = 4096.0,
+                          scale_est: Optional[float] = None) -> np.ndarray:
     """The build's device Gram pipeline (the reference's recurrence, newton_schulz.py:364-448,
     with the build's product forms and roundings), rnd = op_dtype:
     X = rnd(kx s ns_in), s = 1/(||ns_in|| + eps); R = rnd(kr/kx^2 X X^T) with the stored-R
@@ -231,7 +253,8 @@ def syrk_emulated_gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
     unless the next step is the last or a restart W = rnd(Z R^T + a R),
     R = rnd(W Z^T / rs + a/rs W), rs = 1; restart: X = rnd(Q X), R = rnd(X X^T / kx^2), rs = 1;
     U = fp32(Q X / kx). Symmetric results (R, Z, W, a fresh Q) keep their upper triangle,
-    mirrored."""
+    mirrored. scale_est: the single-pass staging, X = rnd(kx est ns_in) and the first R and
+    Q X products multiplied by r^2 and r (`staged_scale`)."""
     if restart_iterations is None:
         restart_iterations = DEFAULT_RESTART
     X = np.asarray(G, dtype=np.float32)
@@ -241,7 +264,8 @@ def syrk_emulated_gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
     nrm = np.float32(np.sqrt(np.sum(X.astype(np.float64) ** 2)))
     s = np.float32(1.0) / (nrm + np.float32(eps))
     f32 = np.float32
-    Xq = rnd((X * f32(s * f32(kx))).astype(np.float32), op_dtype)
+    sx, r = staged_scale(s, scale_est)
+    Xq = rnd((X * f32(sx * f32(kx))).astype(np.float32), op_dtype)
     m = Xq.shape[0]
     kr = 1
     while kr * 2 <= m and kr < 4096:
@@ -258,12 +282,14 @@ def syrk_emulated_gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
         return r
 
     rs = f32(kr)
-    R = sym(rnd(epi(_mm(Xq, Xq.T, "fp32"), rs / f32(kx * kx)), op_dtype))
+    R = sym(rnd(epi(_mm(Xq, Xq.T, "fp32"), f32(f32(rs / f32(kx * kx)) * f32(r * r))), op_dtype))
     Q = None
     n_it = len(coefficients)
+    rx = r                       # the staged X's correction until a restart rewrites X
     for i, (a, b, c) in enumerate(coefficients):
         if i in restart_iterations and i != 0:
-            Xq = rnd(_mm(Q, Xq, "fp32"), op_dtype)
+            Xq = rnd(epi(_mm(Q, Xq, "fp32"), rx), op_dtype)
+            rx = f32(1.0)
             rs = f32(1.0)
             R = sym(rnd(epi(_mm(Xq, Xq.T, "fp32"), f32(1.0) / f32(kx * kx)), op_dtype))
             Q = None
@@ -282,7 +308,7 @@ def syrk_emulated_gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
             W = sym(rnd(epi(_mm(Z, R.T, "fp32"), 1.0, R, a), op_dtype))
             R = sym(rnd(epi(_mm(W, Z.T, "fp32"), f32(1.0) / rs, W, f32(a) / rs), op_dtype))
             rs = f32(1.0)
-    U = (f32(1.0 / kx) * _mm(Q, Xq, "fp32")).astype(np.float32)
+    U = (f32(f32(1.0 / kx) * rx) * _mm(Q, Xq, "fp32")).astype(np.float32)
     if t:
         U = U.T
     return np.ascontiguousarray(U)

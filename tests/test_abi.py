@@ -87,34 +87,34 @@ def test_group_validation_without_gpu():
     coeff = (ctypes.c_float * 15)(*([3.4445, -4.7750, 2.0315] * 5))
     p = ctypes.c_void_p(4096)
     # workspace too small
-    msg = _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1, 0.02, 0.95, 0.0,
+    msg = _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1, 0.02, 0.95, 0.0,
                                          1, 1, coeff, 5, 0, None, 0, 1e-7, p, 16, 0, None))
     assert "workspace" in msg
     # unsupported dtype code
-    assert "dtype" in _err(lib.dmuon_muon_step_group(p, 7, p, p, 1, None, 0, 512, 1024, 1, 0.02,
+    assert "dtype" in _err(lib.dmuon_muon_step_group(p, 7, p, None, p, 1, None, 0, 512, 1024, 1, 0.02,
                                                      0.95, 0.0, 1, 1, coeff, 5, 0, None, 0, 1e-7, p,
                                                      1 << 40, 0, None))
     # unsupported publish dtype
-    assert "publish" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 0, p, 9, 512, 1024, 1, 0.02,
+    assert "publish" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 0, p, 9, 512, 1024, 1, 0.02,
                                                        0.95, 0.0, 1, 1, coeff, 5, 0, None, 0, 1e-7,
                                                        p, 1 << 40, 0, None))
     # no coefficients
-    assert "coefficient" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1,
+    assert "coefficient" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1,
                                                            0.02, 0.95, 0.0, 1, 1, coeff, 0, 0, None,
                                                            0, 1e-7, p, 1 << 40, 0, None))
     # NS group needs outputs
     assert "out_ptrs" in _err(lib.dmuon_newton_schulz_group(p, 1, None, 1, 64, 64, 1, coeff, 5,
                                                             0, None, 0, 1e-7, p, 1 << 30, 0, None))
     # unknown backend, restart list missing
-    assert "backend" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1, 0.02,
+    assert "backend" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1, 0.02,
                                                        0.95, 0.0, 1, 1, coeff, 5, 5, None, 0,
                                                        1e-7, p, 1 << 40, 0, None))
-    assert "restart" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1, 0.02,
+    assert "restart" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1, 0.02,
                                                        0.95, 0.0, 1, 1, coeff, 5, 1, None, 2,
                                                        1e-7, p, 1 << 40, 0, None))
     # gram workspace is larger than direct's
     ws_direct = _C.plan(512, 1024, 1)[3]
-    assert "workspace" in _err(lib.dmuon_muon_step_group(p, 1, p, p, 1, None, 0, 512, 1024, 1,
+    assert "workspace" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1,
                                                          0.02, 0.95, 0.0, 1, 1, coeff, 5, 1, None,
                                                          0, 1e-7, p, ws_direct, 0, None))
 

@@ -128,7 +128,9 @@ def test_c5_layer_full_size_bit_exact_chain(gpu, backend):
     dmuon.replicate(m)
     ns = (dmuon.NewtonSchulz("direct", coefficients=dmuon.KELLER_COEFFICIENTS)
           if backend == "direct" else dmuon.NewtonSchulz("gram"))
-    opt = dmuon.Muon(m, ns_backend=ns, lr=lr, momentum=mu, weight_decay=wd)
+    # the stand-alone NS stages its operand exactly: compare against the two-pass staging
+    opt = dmuon.Muon(m, ns_backend=ns, lr=lr, momentum=mu, weight_decay=wd,
+                     single_pass_staging=False)
     ps = list(m.parameters())
     dps = dmuon.get_owned_params(m)
     # step 1 establishes the momentum buffers
@@ -190,6 +192,78 @@ def test_default_gram_backend_step(gpu, shapes, dtype):
             err = o.rel_fro(Wg - base, Wr - base)
             assert err < (3e-2 if wdt == "bf16" else 2e-2), (step, p.shape, err)
             W[i] = Wg.copy()
+
+
+# ------------------------------------------- single-pass staging with the carried-over scale
+@pytest.mark.parametrize("backend", ["gram", "direct"])
+def test_single_pass_staging(gpu, backend):
+    """Single-pass staging (the default) against two passes. A first step and a step whose
+    gradient norm jumps by 20x (outside [1/4, 4] of the kept scale) are staged exactly:
+    bit-identical to the two-pass run. A step within range stages with the kept scale and
+    matches the oracle's device pipeline given that scale; state["ns_scale"] tracks
+    1/(||ns_in|| + eps)."""
+    shapes = [(256, 640), (640, 256), (384, 384)]
+    lr, mu, wd, eps = 0.02, 0.95, 0.1, 1e-7
+    coeffs = o.POLAR_EXPRESS if backend == "gram" else o.KELLER
+
+    def make(single):
+        m = Mats(shapes, torch.float32, gpu, seed=5)
+        dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2)
+        dmuon.replicate(m)
+        ns = (dmuon.NewtonSchulz("gram") if backend == "gram" else
+              dmuon.NewtonSchulz("direct", coefficients=dmuon.KELLER_COEFFICIENTS))
+        return m, dmuon.Muon(m, lr=lr, momentum=mu, weight_decay=wd, ns_backend=ns,
+                             single_pass_staging=single)
+
+    (m1, opt1), (m2, opt2) = make(True), make(False)
+    dps1 = dmuon.get_owned_params(m1)
+
+    def step(scale, seed):
+        gen = torch.Generator().manual_seed(seed)
+        gs = [(torch.randn(p.shape, generator=gen) * 0.02 * scale) for p in m1.parameters()]
+        for mm in (m1, m2):
+            for p, g in zip(mm.parameters(), gs):
+                p.grad = g.to(gpu)
+        opt1.step()
+        opt2.step()
+        torch.cuda.synchronize()
+        return gs
+
+    def same():
+        return all(torch.equal(a, b) for a, b in zip(m1.parameters(), m2.parameters()))
+
+    step(1.0, 11)                       # no kept scale yet: exact staging
+    assert same()
+    g2 = step(20.0, 12)                 # the norm jumps 20x: staged again exactly
+    assert same()
+    for dp, g in zip(dps1, g2):         # the kept scale is this step's 1/(||ns_in|| + eps)
+        st = opt1.state[id(dp)]
+        ns_in = g.double() + mu * st["momentum_buffer"].cpu().double()
+        assert st["ns_scale"].item() == pytest.approx(
+            1.0 / (torch.linalg.vector_norm(ns_in).item() + eps), rel=1e-5)
+    W = [p.detach().cpu().numpy().copy() for p in m1.parameters()]
+    bufs = [opt1.state[id(dp)]["momentum_buffer"].cpu().numpy().copy() for dp in dps1]
+    est = [opt1.state[id(dp)]["ns_scale"].item() for dp in dps1]
+    gs = step(25.0, 13)                 # within range: the kept scale stages the operand
+    assert not same()
+    for i, (p, g) in enumerate(zip(m1.parameters(), gs)):
+        nb, ns_in = o.momentum_nesterov(g.numpy(), bufs[i], mu, True)
+        if backend == "gram":
+            U = o.syrk_emulated_gram_ns(ns_in, coeffs, o.DEFAULT_RESTART, eps, scale_est=est[i])
+            U0 = o.syrk_emulated_gram_ns(ns_in, coeffs, o.DEFAULT_RESTART, eps)
+        else:
+            U = o.syrk_emulated_ns(ns_in, coeffs, eps, scale_est=est[i])
+            U0 = o.syrk_emulated_ns(ns_in, coeffs, eps)
+        r = (1.0 / (np.sqrt(np.sum(ns_in.astype(np.float64) ** 2)) + eps)) / est[i]
+        assert 0.25 <= r <= 4 and abs(r - 1) > 0.05     # the estimate is used, and not exact
+        assert not np.array_equal(U, U0)
+        Wr = o.apply_update(W[i], U, lr, wd, "fp32")
+        Wg = p.detach().cpu().numpy()
+        dec = np.float32(1 - lr * wd)
+        assert o.rel_fro(Wg - W[i] * dec, Wr - W[i] * dec) < 1e-2, (p.shape, backend)
+        # and the two-pass run lands within the same fp16-rounding distance
+        Wt = list(m2.parameters())[i].detach().cpu().numpy()
+        assert o.rel_fro(Wg - W[i] * dec, Wt - W[i] * dec) < 1e-2
 
 
 # ------------------------------------------- staged pipeline (side-stream staging) vs one stream

@@ -257,3 +257,47 @@ def test_bf16_rounding_helper():
     assert r[1] == 1.0              # halfway 1 + 2^-8 rounds to even (1.0)
     assert r[2] == np.float32(1.0078125)
     assert np.isinf(r[4]) and r[5] == 0.0
+
+
+# ------------------------------------------------------ single-pass staging (carried-over scale)
+def test_staged_scale_choice():
+    f32 = np.float32
+    s = f32(3.0e-3)
+    assert o.staged_scale(s, None) == (s, f32(1.0))
+    assert o.staged_scale(s, 0.0) == (s, f32(1.0))
+    assert o.staged_scale(s, -1.0) == (s, f32(1.0))
+    assert o.staged_scale(s, float(s) * 4) == (f32(float(s) * 4), f32(s) / f32(float(s) * 4))
+    assert o.staged_scale(s, float(s) / 4) == (f32(float(s) / 4), f32(s) / f32(float(s) / 4))
+    assert o.staged_scale(s, float(s) * 4.01) == (s, f32(1.0))      # r just below 1/4
+    assert o.staged_scale(s, float(s) / 4.01) == (s, f32(1.0))      # r just above 4
+
+
+@pytest.mark.parametrize("shape", [(48, 96), (96, 48), (64, 64)])
+def test_emulation_with_scale_estimate(shape):
+    """The device pipelines with an operand staged at an estimated scale: an estimate equal to
+    the exact scale, an out-of-range one and none are all the exact staging bit for bit; one
+    within range rounds the operand differently but lands on the closed form as closely, and
+    dropping its correction (a planted mistake: the products not multiplied by r) does not."""
+    G = _g(shape, seed=21)
+    X = G.T if shape[0] > shape[1] else G
+    s = np.float32(1.0) / (np.float32(np.sqrt(np.sum(X.astype(np.float64) ** 2)))
+                           + np.float32(1e-7))
+    for emu, coeffs, kw in ((o.syrk_emulated_ns, o.KELLER, {}),
+                            (o.syrk_emulated_gram_ns, o.POLAR_EXPRESS,
+                             {"restart_iterations": [2]})):
+        cf = o.closed_form_ns(G, coeffs)
+        U0 = emu(G, coeffs, **kw)
+        assert np.array_equal(emu(G, coeffs, scale_est=float(s), **kw), U0)
+        assert np.array_equal(emu(G, coeffs, scale_est=float(s) * 8, **kw), U0)
+        assert np.array_equal(emu(G, coeffs, scale_est=0.0, **kw), U0)
+        U1 = emu(G, coeffs, scale_est=float(s) * 1.7, **kw)
+        assert not np.array_equal(U1, U0)
+        e0, e1 = o.rel_fro(U0, cf), o.rel_fro(U1, cf)
+        assert e1 < 2e-2 and e1 < 2 * e0 + 2e-3, (emu.__name__, e0, e1)
+        # the planted mistake, in closed form: the operand staged at 1.7 s and used without
+        # its correction is NS of 1.7 x the normalised input
+        Xn = X.astype(np.float64) / np.linalg.norm(X.astype(np.float64))
+        u_, s_, vt_ = np.linalg.svd(Xn, full_matrices=False)
+        bad = (u_ * o.poly_compose(s_ * 1.7, coeffs)) @ vt_
+        bad = bad.T if shape[0] > shape[1] else bad
+        assert o.rel_fro(bad, cf) > 5 * e1, (emu.__name__, o.rel_fro(bad, cf), e1)
