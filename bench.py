@@ -266,7 +266,8 @@ def main():
     # what the staging actually moves per element: gradient (2 B), momentum (4 + 4 B) and the
     # fp16 copy and its transpose (4 B) in one pass with the kept scale (Muon's default); two
     # passes re-read the gradient and the new momentum (6 B more)
-    actual_per_elem = 14.0 if opt._single_pass else 20.0
+    single_pass = opt._single_pass
+    actual_per_elem = 14.0 if single_pass else 20.0
     pre_actual = n_elems * actual_per_elem * prof_steps
     pre_actual_gbs = pre_actual / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
 
@@ -390,7 +391,7 @@ def main():
         "roofline_elementwise": {
             "kernel": ("muon_pre_kernel: momentum + Nesterov + norm partials + fp16 staging of "
                        "ns_in with the kept scale in one pass (a second pass only for matrices "
-                       "whose scale moved by more than 4x)" if opt._single_pass else
+                       "whose scale moved by more than 4x)" if single_pass else
                        "muon_pre_kernel: momentum + Nesterov + norm partials, then fp16 "
                        "staging of ns_in / ||ns_in|| (two passes)"),
             "bound": "hbm", "achieved": None if pre_gbs is None else round(pre_gbs, 1),
