@@ -50,25 +50,23 @@ typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 // buffer's non-temporal store) keep them from displacing cache lines the NS kernels reuse
 // (measured 26.6 -> 24.8 ms per c5 step over both passes). The NS operands X, X^T stay normal
 // stores: the products read them next (non-temporal there measured 7% slower).
+// The pointers come from device pointer tables, so the compiler cannot tell they are global
+// memory and would emit flat accesses (which also count against lgkmcnt); cast to the global
+// address space.
 template <class V>
 __device__ __forceinline__ V ldg_nt(const V* p) {
-  return __builtin_nontemporal_load(p);
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) V*)p);
 }
 template <class V>
 __device__ __forceinline__ void stg_nt(V* p, V v) {
-  __builtin_nontemporal_store(v, p);
+  __builtin_nontemporal_store(v, (__attribute__((address_space(1))) V*)p);
 }
 
+// One 64x64 tile (rows r0.., columns c0..) of matrix l; returns this thread's share of the
+// tile's sum of squares of ns_in. The caller synchronises before tileT is used again.
 template <int ST>
-__global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t tileT[kTile][kTile + kPad];
-  __shared__ float red[4];
-
-  const int l = blockIdx.z;
-  if constexpr (ST == PRE_F16) {
-    if (a.restage && !a.restage[l]) return;   // the single-pass copy of this matrix stands
-  }
-  const int r0 = blockIdx.y * kTile, c0 = blockIdx.x * kTile;
+__device__ __forceinline__ float pre_tile(const PreArgs& a, int l, int r0, int c0,
+                                          uint16_t (*tileT)[kTile + kPad]) {
   const int tid = threadIdx.x;
   const int tc = tid & 15, tr = tid >> 4;
 
@@ -86,52 +84,87 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
   // PRE_EST without a usable estimate: momentum and partials only (the copy is staged later)
   const bool copy = ST != PRE_NORM && (ST != PRE_EST || sc > 0.f);
 
+  // All loads of the thread's four rows are issued before any of them is used (raw words in
+  // registers, converted afterwards): interior tiles take one block-uniform vector path.
+  float gv[4][4], bv[4][4];
+  const int col0 = c0 + 4 * tc;
+  if (vec && r0 + kTile <= a.rows && c0 + kTile <= a.cols) {
+    const long long base0 = (long long)(r0 + tr) * a.cols + col0, rs = 16LL * a.cols;
+    if (a.g_dtype == DT_F32) {
+      f32x4_t t[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        t[q] = ldg_nt(reinterpret_cast<const f32x4_t*>(static_cast<const float*>(g) + base0 +
+                                                       q * rs));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        gv[q][0] = t[q].x; gv[q][1] = t[q].y; gv[q][2] = t[q].z; gv[q][3] = t[q].w;
+      }
+    } else {
+      u32x2_t t[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        t[q] = ldg_nt(reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(g) + base0 +
+                                                       q * rs));
+      f32x4_t b[4];
+      if (read_buf) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          b[q] = ldg_nt(reinterpret_cast<const f32x4_t*>(buf + base0 + q * rs));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        gv[q][0] = bf2f(t[q].x & 0xffff); gv[q][1] = bf2f(t[q].x >> 16);
+        gv[q][2] = bf2f(t[q].y & 0xffff); gv[q][3] = bf2f(t[q].y >> 16);
+        bv[q][0] = read_buf ? b[q].x : 0.f; bv[q][1] = read_buf ? b[q].y : 0.f;
+        bv[q][2] = read_buf ? b[q].z : 0.f; bv[q][3] = read_buf ? b[q].w : 0.f;
+      }
+    }
+    if (a.g_dtype == DT_F32) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4_t b = {0.f, 0.f, 0.f, 0.f};
+        if (read_buf) b = ldg_nt(reinterpret_cast<const f32x4_t*>(buf + base0 + q * rs));
+        bv[q][0] = b.x; bv[q][1] = b.y; bv[q][2] = b.z; bv[q][3] = b.w;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = r0 + tr + 16 * q;
+      const long long base = (long long)row * a.cols + col0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        gv[q][e] = bv[q][e] = 0.f;
+        if (row < a.rows && col0 + e < a.cols) {
+          gv[q][e] = load_any(g, a.g_dtype, base + e);
+          if (read_buf) bv[q][e] = buf[base + e];
+        }
+      }
+    }
+  }
+
   float ss = 0.f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int rl = tr + 16 * q;
     const int row = r0 + rl;
     const int col = c0 + 4 * tc;
-    float gv[4] = {0.f, 0.f, 0.f, 0.f}, bv[4] = {0.f, 0.f, 0.f, 0.f};
     bool in[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) in[e] = (row < a.rows) && (col + e < a.cols);
     const long long base = (long long)row * a.cols + col;
-    if (vec && in[3]) {
-      if (a.g_dtype == DT_F32) {
-        const f32x4_t t =
-            ldg_nt(reinterpret_cast<const f32x4_t*>(static_cast<const float*>(g) + base));
-        gv[0] = t.x; gv[1] = t.y; gv[2] = t.z; gv[3] = t.w;
-      } else {
-        const u32x2_t t =
-            ldg_nt(reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(g) + base));
-        gv[0] = bf2f(t.x & 0xffff); gv[1] = bf2f(t.x >> 16);
-        gv[2] = bf2f(t.y & 0xffff); gv[3] = bf2f(t.y >> 16);
-      }
-      if (read_buf) {
-        const f32x4_t t = ldg_nt(reinterpret_cast<const f32x4_t*>(buf + base));
-        bv[0] = t.x; bv[1] = t.y; bv[2] = t.z; bv[3] = t.w;
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (in[e]) {
-          gv[e] = load_any(g, a.g_dtype, base + e);
-          if (read_buf) bv[e] = buf[base + e];
-        }
-      }
-    }
     float nb[4], ns[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       // buf.mul_(mu).add_(g): two roundings, as the reference does them
       if (buf) {
-        if constexpr (ST == PRE_F16) nb[e] = bv[e];
-        else nb[e] = a.first_step ? gv[e] : __fadd_rn(__fmul_rn(bv[e], mu), gv[e]);
-        ns[e] = a.nesterov ? __fadd_rn(gv[e], __fmul_rn(mu, nb[e])) : nb[e];
+        if constexpr (ST == PRE_F16) nb[e] = bv[q][e];
+        else nb[e] = a.first_step ? gv[q][e] : __fadd_rn(__fmul_rn(bv[q][e], mu), gv[q][e]);
+        ns[e] = a.nesterov ? __fadd_rn(gv[q][e], __fmul_rn(mu, nb[e])) : nb[e];
       } else {
-        nb[e] = gv[e];
-        ns[e] = gv[e];
+        nb[e] = gv[q][e];
+        ns[e] = gv[q][e];
       }
       if (!in[e]) ns[e] = 0.f;
       ss += ns[e] * ns[e];
@@ -172,14 +205,38 @@ __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
       dst[1] = src[1];
     }
   }
+  return ss;
+}
+
+template <int ST>
+__global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t tileT[kTile][kTile + kPad];
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  float ss = pre_tile<ST>(a, blockIdx.z, blockIdx.y * kTile, blockIdx.x * kTile, tileT);
   if constexpr (ST == PRE_F16) return;
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   if (tid == 0) {
     const int nparts = gridDim.x * gridDim.y;
-    a.partials[(long long)l * nparts + blockIdx.y * gridDim.x + blockIdx.x] =
+    a.partials[(long long)blockIdx.z * nparts + blockIdx.y * gridDim.x + blockIdx.x] =
         (red[0] + red[1]) + (red[2] + red[3]);
+  }
+}
+
+// The exact-scale copy for the matrices flagged in a.restage (a scale that moved by more than
+// 4x, or none kept yet). Rarely any are, so the grid is small and strides over the tiles of
+// the flagged matrices only; with nothing flagged each block reads L flags and exits.
+__global__ __launch_bounds__(256) void muon_restage_kernel(const PreArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t tileT[kTile][kTile + kPad];
+  const int tx = a.Cp / kTile, per = tx * (a.Rp / kTile);
+  for (int l = 0; l < a.L; ++l) {
+    if (!a.restage[l]) continue;   // block-uniform
+    for (int t = blockIdx.x; t < per; t += gridDim.x) {
+      __syncthreads();   // the previous tile's transposed read of tileT is done
+      pre_tile<PRE_F16>(a, l, (t / tx) * kTile, (t % tx) * kTile, tileT);
+    }
   }
 }
 
@@ -268,6 +325,9 @@ hipError_t launch_pre(const PreArgs& a, hipStream_t stream) {
   dim3 grid(a.Cp / kTile, a.Rp / kTile, a.L), block(256);
   if (a.stage == PRE_NORM)
     hipLaunchKernelGGL(muon_pre_kernel<PRE_NORM>, grid, block, 0, stream, a);
+  else if (a.stage == PRE_F16 && a.restage)
+    hipLaunchKernelGGL(muon_restage_kernel, dim3(std::min(pre_blocks_per_mat(a.Rp, a.Cp), 2048)),
+                       block, 0, stream, a);
   else if (a.stage == PRE_F16)
     hipLaunchKernelGGL(muon_pre_kernel<PRE_F16>, grid, block, 0, stream, a);
   else if (a.stage == PRE_EST)
