@@ -22,9 +22,11 @@ stays rank-uniform.
 from __future__ import annotations
 
 import os
+from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
+import numpy as np
 import torch
 import torch.distributed as dist
 
@@ -110,40 +112,74 @@ def _kernel_eligible(g: torch.Tensor, device: torch.device) -> bool:
             and g.is_contiguous() and g.dtype in _DTYPE_CODES)
 
 
+def _job_lists(numels, chunk: int):
+    """Jobs of `chunk` elements over tensors of the given sizes, tensor by tensor: the tensor
+    index and element offset of each job (the list ``fast_clip.py:190-196`` builds)."""
+    numels = np.asarray(numels, dtype=np.int64)
+    per = (numels + chunk - 1) // chunk                      # jobs per tensor
+    job_t = np.repeat(np.arange(numels.size, dtype=np.int64), per)
+    first = np.repeat(np.cumsum(per) - per, per)             # index of each tensor's first job
+    return job_t, (np.arange(job_t.size, dtype=np.int64) - first) * chunk
+
+
 class _JobTable:
     """Device-resident job table of the kernel-eligible tensors: int64 [ptrs | numels |
     job_offsets] and int32 [dtypes | segments | job_tensor_ids | zeros]."""
 
     def __init__(self, tensors, segments, device, chunk):
         n = len(tensors)
-        job_t, job_off = [], []
-        for t, g in enumerate(tensors):
-            for off in range(0, g.numel(), chunk):
-                job_t.append(t)
-                job_off.append(off)
-        self.n, self.n_jobs, self.chunk = n, len(job_t), chunk
-        i64 = [g.data_ptr() for g in tensors] + [g.numel() for g in tensors] + job_off
-        i32 = [_DTYPE_CODES[g.dtype] for g in tensors] + list(segments) + job_t + [0] * n
-        self._d64 = torch.tensor(i64, dtype=torch.int64, pin_memory=True).to(device,
-                                                                            non_blocking=True)
-        self._d32 = torch.tensor(i32, dtype=torch.int32, pin_memory=True).to(device,
-                                                                            non_blocking=True)
+        numels = np.array([g.numel() for g in tensors], dtype=np.int64)
+        job_t, job_off = _job_lists(numels, chunk)
+        self.n, self.n_jobs, self.chunk = n, int(job_t.size), chunk
+        i64 = np.concatenate([np.array([g.data_ptr() for g in tensors], dtype=np.int64), numels,
+                              job_off])
+        i32 = np.concatenate([np.array([_DTYPE_CODES[g.dtype] for g in tensors], dtype=np.int32),
+                              np.asarray(segments, dtype=np.int32), job_t.astype(np.int32),
+                              np.zeros(n, dtype=np.int32)])
+        self._d64 = torch.from_numpy(i64).pin_memory().to(device, non_blocking=True)
+        self._d32 = torch.from_numpy(i32).pin_memory().to(device, non_blocking=True)
         b64, b32 = self._d64.data_ptr(), self._d32.data_ptr()
         self.ptrs, self.numels, self.job_offsets = b64, b64 + 8 * n, b64 + 16 * n
         self.dtypes, self.segments = b32, b32 + 4 * n
         self.job_tensor_ids = b32 + 8 * n
         self.zero_segments = b32 + 8 * n + 4 * self.n_jobs
-        self.stream = torch.cuda.current_stream(device).cuda_stream
+        self.device = device
+
+    def _stream(self):
+        return torch.cuda.current_stream(self.device).cuda_stream
 
     def sumsq(self, local_sq: torch.Tensor, segments=None) -> None:
         _C.call("dmuon_segmented_l2_norm_sq", self.ptrs, self.numels, self.dtypes,
                 self.segments if segments is None else segments, self.job_tensor_ids,
-                self.job_offsets, self.n_jobs, self.chunk, local_sq.data_ptr(), self.stream)
+                self.job_offsets, self.n_jobs, self.chunk, local_sq.data_ptr(), self._stream())
 
     def scale(self, coefs: torch.Tensor, segments=None) -> None:
         _C.call("dmuon_segmented_scale", self.ptrs, self.numels, self.dtypes,
                 self.segments if segments is None else segments, self.job_tensor_ids,
-                self.job_offsets, self.n_jobs, self.chunk, coefs.data_ptr(), self.stream)
+                self.job_offsets, self.n_jobs, self.chunk, coefs.data_ptr(), self._stream())
+
+
+# Tables keyed on everything they hold (addresses, sizes, dtypes, segments, chunk): gradients
+# usually keep their storage from step to step, so later calls reuse the device table instead
+# of rebuilding it on the host (for the c5 Muon gradients ~26.6k jobs, longer on the host than
+# the two kernels take). A key that matches describes the same table, whatever tensors now sit
+# at those addresses.
+_TABLE_CACHE: "OrderedDict[tuple, _JobTable]" = OrderedDict()
+_TABLE_CACHE_SIZE = 4
+
+
+def _job_table(tensors, segments, device, chunk) -> _JobTable:
+    key = (str(device), chunk, tuple(segments),
+           tuple((g.data_ptr(), g.numel(), g.dtype) for g in tensors))
+    table = _TABLE_CACHE.get(key)
+    if table is None:
+        table = _JobTable(tensors, segments, device, chunk)
+        _TABLE_CACHE[key] = table
+        while len(_TABLE_CACHE) > _TABLE_CACHE_SIZE:
+            _TABLE_CACHE.popitem(last=False)
+    else:
+        _TABLE_CACHE.move_to_end(key)
+    return table
 
 
 def _split(buckets, device, ext):
@@ -201,7 +237,7 @@ def clip_grad_norm_buckets_(buckets: Sequence[GradClipBucket], max_norm: Optiona
     local_sq = torch.zeros(len(buckets), device=device, dtype=torch.float32)
     for g, s in rest:
         local_sq[s] += g.detach().float().pow(2).sum().to(device=device, dtype=torch.float32)
-    table = _JobTable(kt, ks, device, chunk) if kt else None
+    table = _job_table(kt, ks, device, chunk) if kt else None
     if table is not None:
         table.sumsq(local_sq)
 

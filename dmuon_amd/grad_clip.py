@@ -21,7 +21,7 @@ from typing import Any, Optional, Protocol, Union
 import torch
 import torch.distributed as dist
 
-from .fast_clip import _JobTable, _kernel_eligible, _load_fast_clip_extension, _resolve_chunk_size
+from .fast_clip import _job_table, _kernel_eligible, _load_fast_clip_extension, _resolve_chunk_size
 
 
 @dataclass(frozen=True)
@@ -81,7 +81,7 @@ class GlobalNormMuonClipStrategy:
         device = _accumulator_device(context.optimizer, entries)
         ext = _load_fast_clip_extension()
         eligible = [t for t in tensors if ext is not None and _kernel_eligible(t, device)]
-        table = (_JobTable(eligible, list(range(len(eligible))), device, _resolve_chunk_size(None))
+        table = (_job_table(eligible, list(range(len(eligible))), device, _resolve_chunk_size(None))
                  if eligible and context.norm_type == 2.0 else None)
         total = _total_norm(tensors, eligible, table, context.norm_type, device)
         if context.error_if_nonfinite and bool(torch.logical_or(total.isnan(), total.isinf())):
@@ -143,7 +143,7 @@ def _scale_all(tensors, eligible, table, coef, device) -> None:
         table.scale(coef.reshape(1).to(device=device, dtype=torch.float32),
                     segments=table.zero_segments)
     elif eligible:
-        t0 = _JobTable(eligible, [0] * len(eligible), device, _resolve_chunk_size(None))
+        t0 = _job_table(eligible, [0] * len(eligible), device, _resolve_chunk_size(None))
         t0.scale(coef.reshape(1).to(device=device, dtype=torch.float32))
     for t in tensors:
         if id(t) not in eid:

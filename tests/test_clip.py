@@ -150,6 +150,22 @@ def test_noncontiguous_grad_is_clipped():
     assert float(res.stats_by_name["muon"].total_norm) == pytest.approx(norm, rel=1e-6)
 
 
+def test_job_lists_match_the_plain_loop():
+    """The vectorised job list equals the reference's per-tensor loop (fast_clip.py:190-196),
+    with empty, single-element, exact-multiple and ragged tensors."""
+    for chunk in (1, 3, 7, 262144):
+        sizes = [0, 1, chunk, chunk + 1, 3 * chunk, 0, 2 * chunk - 1, 5]
+        want_t, want_o = [], []
+        for t, n in enumerate(sizes):
+            for off in range(0, n, chunk):
+                want_t.append(t)
+                want_o.append(off)
+        got_t, got_o = fast_clip._job_lists(sizes, chunk)
+        assert got_t.tolist() == want_t and got_o.tolist() == want_o, chunk
+    got_t, got_o = fast_clip._job_lists([], 16)
+    assert got_t.size == 0 and got_o.size == 0
+
+
 def test_entry_point_validation_without_gpu():
     lib = _C.lib()
     q = ctypes.c_void_p(4096)
@@ -218,6 +234,30 @@ def test_kernels_match_oracle_reference_buckets(gpu):
 @pytest.mark.parametrize("chunk", [1, 1000, 4097, 65536])
 def test_kernels_ragged_chunks_and_unaligned(gpu, chunk):
     _check_against_oracle(_mixed_buckets(gpu), gpu, 2.0, chunk_size=chunk, unaligned=True)
+
+
+@pytest.mark.gpu
+def test_cached_job_table_follows_new_values(gpu):
+    """Gradients that keep their storage reuse the cached device table; every call still
+    reads the values the tensors hold now."""
+    gen = torch.Generator().manual_seed(11)
+    grads = [torch.empty(300_001, device=gpu),
+             torch.empty(4096 * 33, device=gpu, dtype=torch.bfloat16)]
+    fast_clip._TABLE_CACHE.clear()
+    tables = []
+    for it in range(3):
+        host = [torch.randn(g.numel(), generator=gen).to(g.dtype) * (it + 1) for g in grads]
+        for d, h in zip(grads, host):
+            d.copy_(h.to(gpu))
+        res = clip_grad_norm_buckets_((GradClipBucket("muon", grads, reduce=True),), 1.0)
+        tables.append(next(reversed(fast_clip._TABLE_CACHE.values())))
+        norm = float(co.segment_sumsq([[_np(h) for h in host]])[0] ** 0.5)
+        st = _stats(res)["muon"]
+        assert float(st.total_norm) == pytest.approx(norm, rel=1e-5), it
+        coef = np.float32(float(st.clip_coef))
+        for d, h in zip(grads, host):
+            assert np.array_equal(_np(d), co.scale(_np(h), coef, _DTS[h.dtype])), it
+    assert tables[0] is tables[1] is tables[2] and len(fast_clip._TABLE_CACHE) == 1
 
 
 @pytest.mark.gpu
