@@ -139,7 +139,6 @@ __device__ void job_scale(void* p, long long begin, long long end, float c) {
     vs = min((begin + V - 1) / V * V, end);
     ve = max(end / V * V, vs);
   }
-  // two 16-byte vectors per thread per iteration (both loads before either store)
   auto sc = [&](u32x4_t w) {
     if constexpr (D == CF32) {
 #pragma unroll
@@ -154,12 +153,13 @@ __device__ void job_scale(void* p, long long begin, long long end, float c) {
   u32x4_t* base = D == CF32 ? reinterpret_cast<u32x4_t*>(static_cast<float*>(p))
                             : reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p));
   long long i = vs + (long long)V * threadIdx.x;
-  for (; i + (long long)V * 256 < ve; i += 2LL * V * 256) {
-    u32x4_t* q0 = base + i / V;
-    u32x4_t* q1 = base + (i + (long long)V * 256) / V;
-    const u32x4_t w0 = *q0, w1 = *q1;
-    *q0 = sc(w0);
-    *q1 = sc(w1);
+  // four vectors in flight per thread; the gradient is streamed once (non-temporal both ways)
+  for (; i + 3LL * V * 256 < ve; i += 4LL * V * 256) {
+    u32x4_t w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) w[u] = __builtin_nontemporal_load(base + i / V + u * 256);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) __builtin_nontemporal_store(sc(w[u]), base + i / V + u * 256);
   }
   for (; i < ve; i += (long long)V * 256) {
     u32x4_t* q = base + i / V;
