@@ -101,6 +101,38 @@ __device__ __forceinline__ void adamw_elt(float& p, float g, float& m, float& v,
   p = rnd<D>(p + a.neg_step * (m / d));
 }
 
+// Two elements at once, the same operations as adamw_elt: bf16 roundings of a pair share one
+// v_cvt_pk_bf16_f32 (each half rounded to nearest even on its own, as f2bf does).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+template <int D>
+__device__ __forceinline__ void rnd2(float& x, float& y) {
+  if constexpr (D == DT_BF16) {
+    const f32x2_t v = {x, y};
+    const unsigned w = __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2_t));
+    x = __uint_as_float(w << 16);
+    y = __uint_as_float(w & 0xffff0000u);
+  }
+}
+template <int D>
+__device__ __forceinline__ void adamw_elt2(float* p, const float* g, float* m, float* v,
+                                           const AdamWArgs& a) {
+  if (a.apply_wd) {
+    p[0] = p[0] * a.wd_scale; p[1] = p[1] * a.wd_scale; rnd2<D>(p[0], p[1]);
+  }
+  m[0] = m[0] * a.beta1; m[1] = m[1] * a.beta1; rnd2<D>(m[0], m[1]);
+  m[0] = m[0] + a.alpha1 * g[0]; m[1] = m[1] + a.alpha1 * g[1]; rnd2<D>(m[0], m[1]);
+  v[0] = v[0] * a.beta2; v[1] = v[1] * a.beta2; rnd2<D>(v[0], v[1]);
+  v[0] = v[0] + a.alpha2 * (g[0] * g[0]); v[1] = v[1] + a.alpha2 * (g[1] * g[1]);
+  rnd2<D>(v[0], v[1]);
+  float d0 = sqrtf(v[0]), d1 = sqrtf(v[1]);
+  rnd2<D>(d0, d1);
+  d0 = d0 / a.bc2_sqrt; d1 = d1 / a.bc2_sqrt; rnd2<D>(d0, d1);
+  d0 = d0 + a.eps; d1 = d1 + a.eps; rnd2<D>(d0, d1);
+  p[0] = p[0] + a.neg_step * (m[0] / d0); p[1] = p[1] + a.neg_step * (m[1] / d1);
+  rnd2<D>(p[0], p[1]);
+}
+
 template <int PD, int GD>
 __global__ __launch_bounds__(256) void adamw_kernel(const AdamWArgs a) {
   const long long lo = (long long)blockIdx.x * a.per_block;
@@ -137,7 +169,7 @@ __global__ __launch_bounds__(256) void adamw_kernel(const AdamWArgs a) {
       ld8<PD>(M, i, m);
       ld8<PD>(V, i, v);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) adamw_elt<PD>(p[k], g[k], m[k], v[k], a);
+      for (int k = 0; k < 8; k += 2) adamw_elt2<PD>(p + k, g + k, m + k, v + k, a);
       st8<PD>(P, i, p);
       st8<PD>(M, i, m);
       st8<PD>(V, i, v);
