@@ -204,9 +204,9 @@ int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_pt
  * per parameter on one stream); it serves the same seam, muon.py:1683-1740.
  */
 int dmuon_muon_stage_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
-                           float* const* est_ptrs, int rows, int cols, int batch, double mu, int nesterov, int first_step,
-                           int backend, float eps, void* workspace, int64_t workspace_bytes,
-                           int tile, void* stream);
+                           float* const* est_ptrs, int rows, int cols, int batch, double mu,
+                           int nesterov, int first_step, int backend, float eps, void* workspace,
+                           int64_t workspace_bytes, int tile, void* stream);
 int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_ptrs,
                            int pub_dtype, int rows, int cols, int batch, double lr, double wd,
                            const float* coeffs, int T, int backend, const int* restarts,
