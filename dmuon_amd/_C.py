@@ -15,6 +15,7 @@ _lib: Optional[ctypes.CDLL] = None
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2          # 16-bit product operands only
 
 c_int, c_i64, c_f, c_d, c_vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
 c_fp = ctypes.POINTER(ctypes.c_float)
@@ -30,6 +31,19 @@ _SIGNATURES = {
     "dmuon_profile_enable": (c_int, [c_int]),
     "dmuon_profile_collect": (c_int, [ctypes.POINTER(c_d), ctypes.POINTER(c_i64),
                                       ctypes.POINTER(c_d), ctypes.POINTER(c_d), c_int]),
+    "dmuon_syrk": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
+                           c_vp, c_i64, c_i64, c_int, c_int, c_int, c_f, c_f, c_f, c_vp, c_int,
+                           c_vp, c_i64, c_vp]),
+    "dmuon_syrk_workspace_size": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp,
+                                          c_i64, c_i64, c_vp, c_i64, c_i64, c_int, c_int, c_int,
+                                          c_int, ctypes.POINTER(c_i64)]),
+    "dmuon_ns_gemm": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
+                              c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_int, c_int, c_int,
+                              c_f, c_f, c_vp, c_int, c_vp]),
+    "dmuon_ns_gemm_final": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64,
+                                    c_i64, c_int, c_int, c_int, c_f, c_f, c_vp, c_int, c_int,
+                                    c_int, c_vp, c_int, c_vp, c_int, c_vp, c_int, c_f, c_f,
+                                    c_int, c_vp]),
     "dmuon_syrk_bf16": (c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp,
                                 c_i64, c_i64, c_int, c_int, c_int, c_f, c_f, c_f, c_vp, c_int, c_vp]),
     "dmuon_ns_gemm_bf16": (c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,

@@ -1,4 +1,5 @@
-from .param import DedicatedParam, DedicatedParamGroup, DedicatedState, LocalCommContext, ReplicatedGroup
+from .param import (DedicatedParam, DedicatedParamGroup, DedicatedState, LocalCommContext,
+                    ReplicatedGroup, normalize_owner_rank)
 
 __all__ = ["DedicatedParam", "DedicatedParamGroup", "DedicatedState", "LocalCommContext",
-           "ReplicatedGroup"]
+           "ReplicatedGroup", "normalize_owner_rank"]

@@ -15,26 +15,57 @@ optimizer reads and writes (reference: ``dmuon/_backends/fsdp2/param.py:116-628`
 * ``_reduced_grad`` -- the reduced gradient the Muon step consumes (``group.py:1348-1352``);
   here the parameter's ``.grad``, set by :func:`dmuon_amd.prepare_muon_grads` or read directly
   by the optimizer; cleared after the update (``muon.py:1746-1747``).
-* ``is_owner``, ``full_shape``, ``tp_group`` (always None: no tensor parallelism here).
+* ``is_owner``, ``owner_rank`` (the ``(shard, replicate)`` coordinate, ``(0, 0)``),
+  ``owner_shard``, ``numel``, ``full_shape``, ``tp_group`` (always None: no tensor
+  parallelism here).
 """
 from __future__ import annotations
 
-from typing import Optional
+from typing import Optional, Tuple, Union
 
 import torch
 from torch import nn
 
 
+OwnerRankLike = Union[int, Tuple[int, int]]
+OwnerCoord = Tuple[int, int]
+
+
+def normalize_owner_rank(owner_rank: OwnerRankLike) -> OwnerCoord:
+    """An owner rank as the reference's ``(owner_shard, owner_replicate)`` coordinate
+    (``_core/owner_rank.py:19-49``): an ``int`` is the 1-D form ``(int, 0)``; a pair passes
+    through. ``bool`` and other types raise ``TypeError``, negative entries ``ValueError``."""
+    if isinstance(owner_rank, tuple):
+        if len(owner_rank) != 2:
+            raise TypeError(f"owner_rank tuple must be (shard, replicate); got {owner_rank!r}")
+        shard, rep = owner_rank
+        if not (isinstance(shard, int) and isinstance(rep, int)) or isinstance(shard, bool) \
+                or isinstance(rep, bool):
+            raise TypeError(f"owner_rank tuple entries must be int; got {owner_rank!r}")
+        if shard < 0 or rep < 0:
+            raise ValueError(f"owner_rank must be non-negative; got {owner_rank!r}")
+        return shard, rep
+    if isinstance(owner_rank, bool) or not isinstance(owner_rank, int):
+        raise TypeError(f"owner_rank must be int or Tuple[int, int]; got "
+                        f"{type(owner_rank).__name__} {owner_rank!r}")
+    if owner_rank < 0:
+        raise ValueError(f"owner_rank must be non-negative; got {owner_rank!r}")
+    return owner_rank, 0
+
+
 class DedicatedParam:
-    def __init__(self, param: nn.Parameter, name: str, owner_rank: int = 0,
+    def __init__(self, param: nn.Parameter, name: str, owner_rank: OwnerRankLike = 0,
                  param_dtype: Optional[torch.dtype] = None,
                  master_dtype: Optional[torch.dtype] = None):
         self.param = param
         self._orig_param = param
         self.param_name = name
-        self.owner_rank = owner_rank
+        coord = normalize_owner_rank(owner_rank)
+        self.owner_rank: OwnerCoord = coord            # (owner_shard, owner_replicate)
+        self.owner_shard: int = coord[0]
         self.is_owner = True
         self.full_shape = tuple(param.shape)
+        self.numel: int = param.numel()                # fsdp2/param.py:214
         self.tp_group = None
         self.is_dtensor = False
         self.is_tp_owner = False

@@ -60,7 +60,7 @@ def dedicate_params(
         if not p.requires_grad or not predicate(name, p):
             continue
         pdt, mdt = _resolve_policy(name, compute_dtype, kwargs.get("param_policy"))
-        p._dedicated_owner_rank = 0
+        p._dedicated_owner_rank = (0, 0)      # the owner coordinate, as api.py tags it
         assignment[p] = 0
         dps.append(DedicatedParam(p, name, 0, param_dtype=pdt, master_dtype=mdt))
     if not assignment:

@@ -540,7 +540,165 @@ int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* 
   return rc;
 }
 
-int dmuon_abi_version(void) { return 103; }
+int dmuon_abi_version(void) { return 104; }
+
+}  // extern "C"
+
+namespace {
+
+// 16-bit operand type of the product entry points: DMUON_DTYPE_BF16 or DMUON_DTYPE_F16
+int elt_of(const char* who, int dtype, int* elt) {
+  if (dtype == DMUON_DTYPE_BF16) { *elt = ELT_BF16; return 0; }
+  if (dtype == DMUON_DTYPE_F16) { *elt = ELT_F16; return 0; }
+  return fail("%s: operand dtype code %d is not a 16-bit type (bf16 %d, fp16 %d)", who, dtype,
+              DMUON_DTYPE_BF16, DMUON_DTYPE_F16);
+}
+
+// The SYRK seam (syrk_or_cublas) for any M and K. The NT kernel reads whole tiles (M a
+// multiple of the tile, K of the 64-wide slice) from 16-byte aligned rows; a call that does
+// not meet that runs on zero-padded copies in the caller's workspace -- A [L][Mp][Kp], B (when
+// it is another matrix), C [L][Mp][Mp] and D [L][Mp][Mp] -- and the M x M corner of the padded
+// result is copied into D. Zero rows and columns of A and B leave the corner unchanged.
+struct SyrkPlan {
+  int tile, Mp, Kp;
+  bool direct;                 // the caller's operands are used in place
+  bool b_copy;
+  int64_t offB, offC, offD, bytes;
+};
+
+int syrk_plan(const char* who, const void* A, int64_t lda, int64_t strideA, const void* B,
+              int64_t ldb, int64_t strideB, const void* C, int64_t ldc, int64_t strideC,
+              const void* D, int64_t ldd, int64_t strideD, int M, int K, int batch, int tile_req,
+              SyrkPlan* pl) {
+  if (tile_req != 0 && tile_req != 128 && tile_req != 256)
+    return fail("%s: tile must be 0 (automatic), 128 or 256, got %d", who, tile_req);
+  if (M < 0 || K < 0 || batch < 0) return fail("%s: bad sizes M=%d K=%d batch=%d", who, M, K, batch);
+  if (!A || !D) return fail("%s: A and D must be non-NULL", who);
+  if (lda < K || ldb < K || ldd < M || (C && ldc < M))
+    return fail("%s: leading dimension smaller than the row length", who);
+  if (batch > 1 && (strideA < 0 || strideB < 0 || strideD < 0 || (C && strideC < 0)))
+    return fail("%s: batch strides must be non-negative", who);
+  if (D == A || D == B || (C && D == C)) return fail("%s: D must not alias A, B or C", who);
+  int t = tile_req;
+  if (t == 0) {
+    // 256-tiles when they add no padding over 128 and the triangle fills 256 CUs once
+    const int64_t m256 = round_up(M, 256);
+    t = (m256 == round_up(M, 128) && (int64_t)batch * tri_tiles((int)m256, 256) >= 256) ? 256 : 128;
+  }
+  pl->tile = t;
+  pl->Mp = (int)round_up(M, t);
+  pl->Kp = (int)round_up(K > 0 ? K : 1, 64);
+  const bool b_same = B == A && ldb == lda && strideB == strideA;
+  pl->direct = M % t == 0 && K % 64 == 0 && K > 0 && aligned16(A) && aligned16(B) &&
+               aligned16(D) && (!C || aligned16(C)) && ld_ok(lda) && ld_ok(ldb) && ld_ok(ldd) &&
+               (!C || ld_ok(ldc)) && stride_ok(strideA, batch) && stride_ok(strideB, batch) &&
+               stride_ok(strideD, batch) && (!C || stride_ok(strideC, batch));
+  pl->b_copy = !b_same;
+  const int64_t L = batch, xa = L * pl->Mp * (int64_t)pl->Kp * 2, xd = L * pl->Mp * (int64_t)pl->Mp * 2;
+  int64_t off = align256(xa);
+  pl->offB = pl->b_copy ? off : 0;
+  if (pl->b_copy) off += align256(xa);
+  pl->offC = C ? off : 0;
+  if (C) off += align256(xd);
+  pl->offD = off;
+  off += align256(xd);
+  pl->bytes = pl->direct ? 0 : off;
+  return 0;
+}
+
+int syrk_impl(const char* who, int elt, const void* A, int64_t lda, int64_t strideA,
+              const void* B, int64_t ldb, int64_t strideB, const void* C, int64_t ldc,
+              int64_t strideC, void* D, int64_t ldd, int64_t strideD, int M, int K, int batch,
+              float alpha, float beta, float diag_add, const float* alpha_dev, int tile_req,
+              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  if (batch == 0 || M == 0) return 0;
+  if (!B) { B = A; ldb = lda; strideB = strideA; }
+  SyrkPlan pl;
+  if (syrk_plan(who, A, lda, strideA, B, ldb, strideB, C, ldc, strideC, D, ldd, strideD, M, K,
+                batch, tile_req, &pl))
+    return 1;
+  NtArgs s{};
+  s.elt = elt;
+  s.M = pl.Mp; s.N = pl.Mp; s.K = pl.Kp; s.L = batch;
+  s.mt = s.nt = pl.Mp / pl.tile; s.tiles_per_mat = tri_tiles(pl.Mp, pl.tile); s.tri = 1;
+  s.mode = EPI_SYM; s.alpha = alpha; s.beta = C ? beta : 0.f; s.diag = diag_add;
+  s.alpha_dev = alpha_dev;
+  if (pl.direct) {
+    s.A = static_cast<const uint16_t*>(A); s.lda = lda; s.sA = strideA;
+    s.B = static_cast<const uint16_t*>(B); s.ldb = ldb; s.sB = strideB;
+    s.C = static_cast<const uint16_t*>(C); s.ldc = ldc; s.sC = strideC;
+    s.D = static_cast<uint16_t*>(D); s.ldd = ldd; s.sD = strideD;
+    return check_launch(launch_nt(s, pl.tile, stream), who);
+  }
+  if (!workspace)
+    return fail("%s: M=%d, K=%d or the operand layout needs the padded path (M a multiple of "
+                "the tile %d, K of 64, 16-byte aligned rows otherwise), which needs a workspace "
+                "of %lld bytes (dmuon_syrk_workspace_size)", who, M, K, pl.tile,
+                (long long)pl.bytes);
+  if (!aligned16(workspace) || workspace_bytes < pl.bytes)
+    return fail("%s: workspace misaligned or smaller than the %lld bytes of the padded path", who,
+                (long long)pl.bytes);
+  char* ws = static_cast<char*>(workspace);
+  const long long sa = (long long)pl.Mp * pl.Kp, sd = (long long)pl.Mp * pl.Mp;
+  uint16_t* Ap = reinterpret_cast<uint16_t*>(ws);
+  uint16_t* Bp = pl.b_copy ? reinterpret_cast<uint16_t*>(ws + pl.offB) : Ap;
+  uint16_t* Cp = C ? reinterpret_cast<uint16_t*>(ws + pl.offC) : nullptr;
+  uint16_t* Dp = reinterpret_cast<uint16_t*>(ws + pl.offD);
+  if (check_launch(launch_pad_copy(static_cast<const uint16_t*>(A), lda, strideA, Ap, pl.Kp, sa,
+                                   M, K, pl.Mp, pl.Kp, batch, stream), who))
+    return 1;
+  if (pl.b_copy &&
+      check_launch(launch_pad_copy(static_cast<const uint16_t*>(B), ldb, strideB, Bp, pl.Kp, sa,
+                                   M, K, pl.Mp, pl.Kp, batch, stream), who))
+    return 1;
+  if (C && check_launch(launch_pad_copy(static_cast<const uint16_t*>(C), ldc, strideC, Cp, pl.Mp,
+                                        sd, M, M, pl.Mp, pl.Mp, batch, stream), who))
+    return 1;
+  s.A = Ap; s.lda = pl.Kp; s.sA = sa;
+  s.B = Bp; s.ldb = pl.Kp; s.sB = sa;
+  s.C = Cp; s.ldc = pl.Mp; s.sC = sd;
+  s.D = Dp; s.ldd = pl.Mp; s.sD = sd;
+  if (check_launch(launch_nt(s, pl.tile, stream), who)) return 1;
+  return check_launch(launch_pad_copy(Dp, pl.Mp, sd, static_cast<uint16_t*>(D), ldd, strideD, M,
+                                      M, M, M, batch, stream), who);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dmuon_syrk_workspace_size(int dtype, const void* A, int64_t lda, int64_t strideA,
+                              const void* B, int64_t ldb, int64_t strideB, const void* C,
+                              int64_t ldc, int64_t strideC, const void* D, int64_t ldd,
+                              int64_t strideD, int M, int K, int batch, int tile,
+                              int64_t* workspace_bytes) {
+  const char* who = "dmuon_syrk_workspace_size";
+  int elt;
+  if (!workspace_bytes) return fail("%s: NULL output", who);
+  *workspace_bytes = 0;
+  if (elt_of(who, dtype, &elt)) return 1;
+  if (batch == 0 || M == 0) return 0;
+  if (!B) { B = A; ldb = lda; strideB = strideA; }
+  SyrkPlan pl;
+  if (syrk_plan(who, A, lda, strideA, B, ldb, strideB, C, ldc, strideC, D, ldd, strideD, M, K,
+                batch, tile, &pl))
+    return 1;
+  *workspace_bytes = pl.bytes;
+  return 0;
+}
+
+int dmuon_syrk(int dtype, const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
+               int64_t strideB, const void* C, int64_t ldc, int64_t strideC, void* D, int64_t ldd,
+               int64_t strideD, int M, int K, int batch, float alpha, float beta, float diag_add,
+               const float* alpha_dev, int tile, void* workspace, int64_t workspace_bytes,
+               void* stream) {
+  const char* who = "dmuon_syrk";
+  int elt;
+  if (elt_of(who, dtype, &elt)) return 1;
+  return syrk_impl(who, elt, A, lda, strideA, B, ldb, strideB, C, ldc, strideC, D, ldd, strideD,
+                   M, K, batch, alpha, beta, diag_add, alpha_dev, tile, workspace,
+                   workspace_bytes, static_cast<hipStream_t>(stream));
+}
 
 int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
                     int64_t strideB, const void* C, int64_t ldc, int64_t strideC, void* D,
@@ -549,31 +707,13 @@ int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, 
   const char* who = "dmuon_syrk_bf16";
   if (batch == 0 || M == 0) return 0;
   if (tile != 128 && tile != 256) return fail("%s: tile must be 128 or 256, got %d", who, tile);
-  if (M < 0 || K <= 0 || batch < 0) return fail("%s: bad sizes M=%d K=%d batch=%d", who, M, K, batch);
-  if (M % tile) return fail("%s: M=%d is not a multiple of the tile %d", who, M, tile);
-  if (K % 64) return fail("%s: K=%d is not a multiple of 64", who, K);
-  if (!B) { B = A; ldb = lda; strideB = strideA; }
-  if (!A || !D) return fail("%s: A and D must be non-NULL", who);
-  if (!aligned16(A) || !aligned16(B) || !aligned16(D) || (C && !aligned16(C)))
+  if (M > 0 && M % tile) return fail("%s: M=%d is not a multiple of the tile %d", who, M, tile);
+  if (K > 0 && K % 64) return fail("%s: K=%d is not a multiple of 64", who, K);
+  if (!aligned16(A) || (B && !aligned16(B)) || !aligned16(D) || (C && !aligned16(C)))
     return fail("%s: operands must be 16-byte aligned", who);
-  if (!ld_ok(lda) || !ld_ok(ldb) || !ld_ok(ldd) || (C && !ld_ok(ldc)))
-    return fail("%s: leading dimensions must be positive multiples of 8", who);
-  if (lda < K || ldb < K || ldd < M || (C && ldc < M))
-    return fail("%s: leading dimension smaller than the row length", who);
-  if (!stride_ok(strideA, batch) || !stride_ok(strideB, batch) || !stride_ok(strideD, batch) ||
-      (C && !stride_ok(strideC, batch)))
-    return fail("%s: batch strides must be non-negative multiples of 8", who);
-  if (D == A || D == B || (C && D == C)) return fail("%s: D must not alias A, B or C", who);
-  NtArgs s{};
-  s.A = static_cast<const uint16_t*>(A); s.lda = lda; s.sA = strideA;
-  s.B = static_cast<const uint16_t*>(B); s.ldb = ldb; s.sB = strideB;
-  s.M = M; s.N = M; s.K = K; s.L = batch;
-  s.mt = s.nt = M / tile; s.tiles_per_mat = tri_tiles(M, tile); s.tri = 1;
-  s.mode = EPI_SYM; s.alpha = alpha; s.beta = C ? beta : 0.f; s.diag = diag_add;
-  s.alpha_dev = alpha_dev;
-  s.C = static_cast<const uint16_t*>(C); s.ldc = ldc; s.sC = strideC;
-  s.D = static_cast<uint16_t*>(D); s.ldd = ldd; s.sD = strideD;
-  return check_launch(launch_nt(s, tile, static_cast<hipStream_t>(stream)), who);
+  return syrk_impl(who, ELT_BF16, A, lda, strideA, B, ldb, strideB, C, ldc, strideC, D, ldd,
+                   strideD, M, K, batch, alpha, beta, diag_add, alpha_dev, tile, nullptr, 0,
+                   static_cast<hipStream_t>(stream));
 }
 
 static int gemm_common_checks(const char* who, const void* P, int64_t ldp, int64_t strideP,
@@ -592,12 +732,11 @@ static int gemm_common_checks(const char* who, const void* P, int64_t ldp, int64
   return 0;
 }
 
-int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT, int64_t ldxt,
+static int ns_gemm_impl(const char* who, int elt, const void* P, int64_t ldp, int64_t strideP, const void* XT, int64_t ldxt,
                        int64_t strideXT, const void* X, int64_t ldx, int64_t strideX, void* Xout,
                        int64_t ldxo, int64_t strideXo, void* XTout, int64_t ldxto,
                        int64_t strideXTo, int M, int N, int batch, float alpha, float beta,
                        const float* alpha_dev, int tile, void* stream) {
-  const char* who = "dmuon_ns_gemm_bf16";
   if (batch == 0) return 0;
   if (gemm_common_checks(who, P, ldp, strideP, XT, ldxt, strideXT, X, ldx, strideX, M, N, batch, tile))
     return 1;
@@ -608,6 +747,7 @@ int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* 
   if (XTout == XT) return fail("%s: XTout must not alias XT", who);
   if (Xout == P || Xout == XT) return fail("%s: Xout must not alias P or XT", who);
   NtArgs g{};
+  g.elt = elt;
   g.A = static_cast<const uint16_t*>(P); g.lda = ldp; g.sA = strideP;
   g.B = static_cast<const uint16_t*>(XT); g.ldb = ldxt; g.sB = strideXT;
   g.M = M; g.N = N; g.K = M; g.L = batch;
@@ -619,14 +759,13 @@ int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* 
   return check_launch(launch_nt(g, tile, static_cast<hipStream_t>(stream)), who);
 }
 
-int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT,
+static int ns_gemm_final_impl(const char* who, int elt, const void* P, int64_t ldp, int64_t strideP, const void* XT,
                              int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx,
                              int64_t strideX, int M, int N, int batch, float alpha, float beta,
                              const float* alpha_dev, int m_real, int n_real, int transposed,
                              void* const* out_ptrs, int out_dtype, void* const* w_ptrs,
                              int w_dtype, void* const* pub_ptrs, int pub_dtype, float decay,
                              float lrs, int tile, void* stream) {
-  const char* who = "dmuon_ns_gemm_final_bf16";
   if (batch == 0) return 0;
   if (gemm_common_checks(who, P, ldp, strideP, XT, ldxt, strideXT, X, ldx, strideX, M, N, batch, tile))
     return 1;
@@ -641,6 +780,7 @@ int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const 
   if (pub_ptrs && pub_dtype != DMUON_DTYPE_F32 && pub_dtype != DMUON_DTYPE_BF16)
     return fail("%s: unsupported publish dtype %d", who, pub_dtype);
   NtArgs g{};
+  g.elt = elt;
   g.A = static_cast<const uint16_t*>(P); g.lda = ldp; g.sA = strideP;
   g.B = static_cast<const uint16_t*>(XT); g.ldb = ldxt; g.sB = strideXT;
   g.M = M; g.N = N; g.K = M; g.L = batch;
@@ -652,6 +792,56 @@ int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const 
   g.pub_ptrs = pub_ptrs; g.pub_dtype = pub_dtype;
   g.m_real = m_real; g.n_real = n_real; g.transposed = transposed ? 1 : 0;
   return check_launch(launch_nt(g, tile, static_cast<hipStream_t>(stream)), who);
+}
+
+int dmuon_ns_gemm(int dtype, const void* P, int64_t ldp, int64_t strideP, const void* XT,
+                  int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx, int64_t strideX,
+                  void* Xout, int64_t ldxo, int64_t strideXo, void* XTout, int64_t ldxto,
+                  int64_t strideXTo, int M, int N, int batch, float alpha, float beta,
+                  const float* alpha_dev, int tile, void* stream) {
+  int elt;
+  if (elt_of("dmuon_ns_gemm", dtype, &elt)) return 1;
+  return ns_gemm_impl("dmuon_ns_gemm", elt, P, ldp, strideP, XT, ldxt, strideXT, X, ldx, strideX,
+                      Xout, ldxo, strideXo, XTout, ldxto, strideXTo, M, N, batch, alpha, beta,
+                      alpha_dev, tile, stream);
+}
+
+int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT, int64_t ldxt,
+                       int64_t strideXT, const void* X, int64_t ldx, int64_t strideX, void* Xout,
+                       int64_t ldxo, int64_t strideXo, void* XTout, int64_t ldxto,
+                       int64_t strideXTo, int M, int N, int batch, float alpha, float beta,
+                       const float* alpha_dev, int tile, void* stream) {
+  return ns_gemm_impl("dmuon_ns_gemm_bf16", ELT_BF16, P, ldp, strideP, XT, ldxt, strideXT, X, ldx,
+                      strideX, Xout, ldxo, strideXo, XTout, ldxto, strideXTo, M, N, batch, alpha,
+                      beta, alpha_dev, tile, stream);
+}
+
+int dmuon_ns_gemm_final(int dtype, const void* P, int64_t ldp, int64_t strideP, const void* XT,
+                        int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx,
+                        int64_t strideX, int M, int N, int batch, float alpha, float beta,
+                        const float* alpha_dev, int m_real, int n_real, int transposed,
+                        void* const* out_ptrs, int out_dtype, void* const* w_ptrs, int w_dtype,
+                        void* const* pub_ptrs, int pub_dtype, float decay, float lrs, int tile,
+                        void* stream) {
+  int elt;
+  if (elt_of("dmuon_ns_gemm_final", dtype, &elt)) return 1;
+  return ns_gemm_final_impl("dmuon_ns_gemm_final", elt, P, ldp, strideP, XT, ldxt, strideXT, X,
+                            ldx, strideX, M, N, batch, alpha, beta, alpha_dev, m_real, n_real,
+                            transposed, out_ptrs, out_dtype, w_ptrs, w_dtype, pub_ptrs, pub_dtype,
+                            decay, lrs, tile, stream);
+}
+
+int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT,
+                             int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx,
+                             int64_t strideX, int M, int N, int batch, float alpha, float beta,
+                             const float* alpha_dev, int m_real, int n_real, int transposed,
+                             void* const* out_ptrs, int out_dtype, void* const* w_ptrs,
+                             int w_dtype, void* const* pub_ptrs, int pub_dtype, float decay,
+                             float lrs, int tile, void* stream) {
+  return ns_gemm_final_impl("dmuon_ns_gemm_final_bf16", ELT_BF16, P, ldp, strideP, XT, ldxt,
+                            strideXT, X, ldx, strideX, M, N, batch, alpha, beta, alpha_dev, m_real,
+                            n_real, transposed, out_ptrs, out_dtype, w_ptrs, w_dtype, pub_ptrs,
+                            pub_dtype, decay, lrs, tile, stream);
 }
 
 int dmuon_muon_pre_partials(int Rp, int Cp) { return pre_blocks_per_mat(Rp, Cp); }

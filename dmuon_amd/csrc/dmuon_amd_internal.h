@@ -7,8 +7,9 @@
 
 namespace dmuon {
 
-// dtype codes used across the C-ABI (mirrors DMUON_DTYPE_* in dmuon_amd.h).
-enum DType : int { DT_F32 = 0, DT_BF16 = 1 };
+// dtype codes used across the C-ABI (mirrors DMUON_DTYPE_* in dmuon_amd.h); DT_F16 only names
+// 16-bit product operands (SYRK / NS-GEMM entry points).
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
 // Epilogue of the NT-form MFMA product  acc[i][j] = sum_k A[i][k] * B[j][k].
 //   EPI_SYM   D = s*acc + beta*C + diag*I          (symmetric result, upper tiles + mirror)
@@ -82,6 +83,11 @@ hipError_t launch_norm_finalize_est(const float* partials, int nparts, int L, fl
                                     float* scale, float* scale_sq, float* const* est_ptrs,
                                     float* ratio, float* ratio_sq, int* restage,
                                     hipStream_t stream);
+
+// dst[l][r][c] = r < rows && c < cols ? src[l][r][c] : 0 over rows_out x cols_out (16-bit)
+hipError_t launch_pad_copy(const uint16_t* src, long long lds, long long ss, uint16_t* dst,
+                           long long ldd, long long sd, int rows, int cols, int rows_out,
+                           int cols_out, int L, hipStream_t stream);
 
 struct UpdateArgs {
   void* const* w_ptrs; int w_dtype;

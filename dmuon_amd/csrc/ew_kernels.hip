@@ -161,7 +161,8 @@ __device__ __forceinline__ float pre_tile(const PreArgs& a, int l, int r0, int c
       if (buf) {
         if constexpr (ST == PRE_F16) nb[e] = bv[q][e];
         else nb[e] = a.first_step ? gv[q][e] : __fadd_rn(__fmul_rn(bv[q][e], mu), gv[q][e]);
-        ns[e] = a.nesterov ? __fadd_rn(gv[q][e], __fmul_rn(mu, nb[e])) : nb[e];
+        // grad.add(buf, alpha=mu): one op, one rounding (a fused multiply-add)
+        ns[e] = a.nesterov ? __builtin_fmaf(mu, nb[e], gv[q][e]) : nb[e];
       } else {
         nb[e] = gv[q][e];
         ns[e] = gv[q][e];
@@ -272,12 +273,12 @@ __global__ __launch_bounds__(256) void muon_update_kernel(const UpdateArgs a) {
       float* wp = static_cast<float*>(w) + i;
       float wv = *wp;
       if (a.decay != 1.f) wv = __fmul_rn(wv, a.decay);
-      *wp = __fadd_rn(wv, -a.lrs * uv);
+      *wp = __builtin_fmaf(-a.lrs, uv, wv);   // add_(U, alpha=-lrs): one rounding
     } else {
       uint16_t* wp = static_cast<uint16_t*>(w) + i;
       float wv = bf2f(*wp);
       if (a.decay != 1.f) wv = bf2f(f2bf(__fmul_rn(wv, a.decay)));
-      *wp = f2bf(__fadd_rn(wv, -a.lrs * uv));
+      *wp = f2bf(__builtin_fmaf(-a.lrs, uv, wv));
     }
   }
 }
@@ -317,7 +318,32 @@ __global__ __launch_bounds__(256) void norm_finalize_est_kernel(
   }
 }
 
+// dst[l][r][c] = src[l][r][c] for r < rows, c < cols, 0 elsewhere in the rows_out x cols_out
+// extent: the zero-padded operand copies of an unaligned or ragged SYRK call, and the copy of
+// its M x M corner back out. One block per output row; 16-bit elements of either type.
+__global__ __launch_bounds__(256) void pad_copy_kernel(const uint16_t* src, long long lds,
+                                                       long long ss, uint16_t* dst, long long ldd,
+                                                       long long sd, int rows, int cols,
+                                                       int rows_out, int cols_out) {
+  const long long row = blockIdx.x;
+  const int l = (int)(row / rows_out), r = (int)(row % rows_out);
+  uint16_t* d = dst + (long long)l * sd + (long long)r * ldd;
+  const uint16_t* s = src + (long long)l * ss + (long long)r * lds;
+  const bool live = r < rows;
+  for (int c = threadIdx.x; c < cols_out; c += 256) d[c] = (live && c < cols) ? s[c] : (uint16_t)0;
+}
+
 }  // namespace
+
+hipError_t launch_pad_copy(const uint16_t* src, long long lds, long long ss, uint16_t* dst,
+                           long long ldd, long long sd, int rows, int cols, int rows_out,
+                           int cols_out, int L, hipStream_t stream) {
+  const long long nb = (long long)L * rows_out;
+  if (nb <= 0 || cols_out <= 0) return hipSuccess;
+  hipLaunchKernelGGL(pad_copy_kernel, dim3((unsigned)nb), dim3(256), 0, stream, src, lds, ss, dst,
+                     ldd, sd, rows, cols, rows_out, cols_out);
+  return hipGetLastError();
+}
 
 int pre_blocks_per_mat(int Rp, int Cp) { return (Rp / kTile) * (Cp / kTile); }
 

@@ -485,7 +485,7 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
               for (int t = 0; t < 8; ++t) {
                 float wv = w[t];
                 if (a.decay != 1.f) wv = __fmul_rn(wv, a.decay);
-                wn[t] = __fadd_rn(wv, -a.lrs * u[t]);
+                wn[t] = __builtin_fmaf(-a.lrs, u[t], wv);
                 r[t] = __float_as_uint(wn[t]);
               }
               u32x4_t* q = reinterpret_cast<u32x4_t*>(static_cast<float*>(wp) + voff[v]);
@@ -498,7 +498,7 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
                 const unsigned word = wraw[v][0][t >> 1];
                 float wv = bf2f((t & 1) ? (word >> 16) : (word & 0xffff));
                 if (a.decay != 1.f) wv = bf2f(f2bf(__fmul_rn(wv, a.decay)));
-                r[t] = f2bf(__fadd_rn(wv, -a.lrs * u[t]));
+                r[t] = f2bf(__builtin_fmaf(-a.lrs, u[t], wv));
                 wn[t] = bf2f(r[t]);
               }
               *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(wp) + voff[v]) =
@@ -542,12 +542,12 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
               if (a.w_dtype == DT_F32) {
                 float wv = static_cast<const float*>(wp)[off];
                 if (a.decay != 1.f) wv = __fmul_rn(wv, a.decay);
-                wn = __fadd_rn(wv, -a.lrs * ut);
+                wn = __builtin_fmaf(-a.lrs, ut, wv);
                 static_cast<float*>(wp)[off] = wn;
               } else {
                 float wv = bf2f(static_cast<const uint16_t*>(wp)[off]);
                 if (a.decay != 1.f) wv = bf2f(f2bf(__fmul_rn(wv, a.decay)));
-                const uint16_t h = f2bf(__fadd_rn(wv, -a.lrs * ut));
+                const uint16_t h = f2bf(__builtin_fmaf(-a.lrs, ut, wv));
                 static_cast<uint16_t*>(wp)[off] = h;
                 wn = bf2f(h);
               }

@@ -14,10 +14,11 @@ from .newton_schulz import (
     newton_schulz,
     newton_schulz_batched,
 )
+from .syrk_dispatch import syrk_or_cublas
 
 __all__ = [
     "Muon", "fused_adamw_", "NewtonSchulz", "newton_schulz", "gram_newton_schulz", "direct_newton_schulz",
     "newton_schulz_batched", "get_ns_backend", "get_backend_status", "YOU_COEFFICIENTS",
     "POLAR_EXPRESS_COEFFICIENTS", "KELLER_COEFFICIENTS", "DEFAULT_COEFFICIENTS",
-    "DEFAULT_RESTART_ITERATIONS",
+    "DEFAULT_RESTART_ITERATIONS", "syrk_or_cublas",
 ]

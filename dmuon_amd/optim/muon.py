@@ -42,6 +42,24 @@ logger = logging.getLogger(__name__)
 _MUON_KEYS = ("lr", "momentum", "weight_decay")
 
 
+def _state_tensor(t, shape: tuple, device: torch.device, dtype: torch.dtype, key: str,
+                  name: str) -> Tensor:
+    """An optimizer-state tensor in the layout the kernels read: on ``device``, ``dtype``,
+    contiguous, shaped ``shape``. State restored by ``load_state_dict`` keeps whatever it was
+    saved with (the Muon state is keyed by ``id(dp)``, which torch does not cast): a CPU
+    ``map_location``, the reference's grad-dtype momentum (``grad.clone()``), a view. Those are
+    converted here, once; a tensor of the wrong size raises instead of reaching a kernel."""
+    if not torch.is_tensor(t):
+        raise TypeError(f"{name}: optimizer state {key!r} must be a tensor, got {type(t).__name__}")
+    numel = math.prod(shape)
+    if t.numel() != numel:
+        raise ValueError(f"{name}: optimizer state {key!r} has {t.numel()} elements, expected "
+                         f"{numel} (shape {tuple(shape)})")
+    if t.device != device or t.dtype != dtype or not t.is_contiguous() or tuple(t.shape) != shape:
+        t = t.detach().to(device=device, dtype=dtype).reshape(shape).contiguous()
+    return t
+
+
 def _pinned_ptrs(ptrs: list[int], device: torch.device) -> Tensor:
     host = torch.tensor(ptrs, dtype=torch.int64, pin_memory=True)
     return host.to(device, non_blocking=True)
@@ -299,8 +317,18 @@ class Muon(torch.optim.Optimizer):
                     if "momentum_buffer" not in st:
                         st["momentum_buffer"] = torch.zeros((rows, cols), dtype=torch.float32,
                                                             device=dev)
-                    if self._single_pass and "ns_scale" not in st:
-                        st["ns_scale"] = torch.zeros(1, dtype=torch.float32, device=dev)
+                    else:
+                        st["momentum_buffer"] = _state_tensor(
+                            st["momentum_buffer"], (rows, cols), dev, torch.float32,
+                            "momentum_buffer", dp.param_name)
+                    if self._single_pass:
+                        sc = st.get("ns_scale")
+                        if not torch.is_tensor(sc) or sc.numel() != 1:
+                            # no usable kept scale: 0 stages the operand exactly
+                            st["ns_scale"] = torch.zeros(1, dtype=torch.float32, device=dev)
+                        else:
+                            st["ns_scale"] = _state_tensor(sc, (1,), dev, torch.float32,
+                                                           "ns_scale", dp.param_name)
                     if not dp._owned_data.is_contiguous():
                         raise RuntimeError(f"{dp.param_name}: Muon needs a contiguous weight")
                 tile, _, _, nbytes = _C.plan(rows, cols, len(part), 0, num_cus, backend)
@@ -412,6 +440,12 @@ class Muon(torch.optim.Optimizer):
                 state["step"] = 0
                 state["exp_avg"] = torch.zeros_like(param)
                 state["exp_avg_sq"] = torch.zeros_like(param)
+            else:
+                name = dp.param_name if dp is not None else f"param{tuple(param.shape)}"
+                for k in ("exp_avg", "exp_avg_sq"):
+                    state[k] = _state_tensor(state[k], tuple(param.shape), param.device,
+                                             param.dtype, k, name)
+                state["step"] = int(state["step"])
             state["step"] += 1
             key = (state["step"], param.dtype, param.device, grad.dtype,
                    None if pub is None else pub.dtype)

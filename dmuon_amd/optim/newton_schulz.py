@@ -39,6 +39,7 @@ import torch
 from torch import Tensor
 
 from dmuon_amd import _C
+from dmuon_amd.optim.syrk_dispatch import KERNEL_NAME, get_backend_status, get_ns_backend  # noqa: F401
 
 logger = logging.getLogger(__name__)
 
@@ -75,7 +76,6 @@ KELLER_COEFFICIENTS = [(3.4445, -4.7750, 2.0315)] * 5
 DEFAULT_COEFFICIENTS = POLAR_EXPRESS_COEFFICIENTS
 DEFAULT_RESTART_ITERATIONS = [2]
 
-KERNEL_NAME = "hip_gfx950"
 _KERNEL_ALIASES = {"auto": KERNEL_NAME, "hip": KERNEL_NAME, KERNEL_NAME: KERNEL_NAME,
                    # the reference's bit-exact choice; the HIP kernels are deterministic
                    "cublas": KERNEL_NAME}
@@ -296,28 +296,6 @@ class NewtonSchulz:
     def __repr__(self) -> str:
         coeff = "default" if self.coefficients is None else f"{len(self.coefficients)}-step custom"
         return f"NewtonSchulz(backend={self.backend!r}, kernel={self.kernel!r}, coefficients={coeff})"
-
-
-def get_ns_backend() -> str:
-    """One-line description of the NS kernel (``syrk_dispatch.py:42-66``)."""
-    return ("Gram-space NS with restarts / direct NS in SYRK form · kernel=hip_gfx950 "
-            "(MI355X CDNA4, fp16 MFMA 32x32x16)")
-
-
-def get_backend_status() -> dict:
-    """Diagnostic snapshot (``syrk_dispatch.py:69-84``)."""
-    status = {
-        "arch": "gfx950",
-        "auto_choice": KERNEL_NAME,
-        "library": str(_C.lib_path()),
-        "library_built": _C.lib_path().exists(),
-        "quack_available": False,
-        "cute_sm80_available": False,
-        "gpu_visible": torch.cuda.is_available(),
-    }
-    if status["library_built"]:
-        status["abi_version"] = _C.lib().dmuon_abi_version()
-    return status
 
 
 def ns_useful_flops(rows: int, cols: int, steps: int = 5, backend: str = "direct",

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 from torch import nn
 
+from dmuon_amd._backends.local import normalize_owner_rank
 from dmuon_amd.api import iter_dedicated_states
 
 
@@ -22,12 +23,20 @@ def get_dedicated_params(model: nn.Module) -> list:
     return out
 
 
-def get_owned_params(model: nn.Module) -> list:
-    return [dp for dp in get_dedicated_params(model) if dp.is_owner]
+def get_owned_params(model: nn.Module, rank=0) -> list:
+    """``utils.py:51-60``: the dedicated params owned by ``rank`` -- a shard ``int`` (1-D form)
+    or a ``(shard, replicate)`` pair, matched against each param's owner coordinate. At
+    world_size=1 every dedicated param is owned by ``(0, 0)``."""
+    coord = normalize_owner_rank(rank)
+    return [dp for dp in get_dedicated_params(model) if dp.owner_rank == coord]
 
 
-def prepare_muon_grads(model: nn.Module) -> None:
-    """``utils.py:178-204``: make every owned dedicated param's reduced grad available."""
+def prepare_muon_grads(model: nn.Module, *, use_reduce_stream: bool = False,
+                       coalesce_wait: bool = False) -> None:
+    """``utils.py:178-204``: make every owned dedicated param's reduced grad available. The
+    reduce-stream and coalesced-wait options of the reference order a side-stream reduce
+    against the current stream; at world_size=1 there is no reduce, so both are accepted and
+    change nothing."""
     for st in iter_dedicated_states(model):
         st.group.wait_for_reduce()
 

@@ -17,13 +17,20 @@
  *     DEVICE arrays of `batch` pointers, because they are separate allocations.
  *
  * Reference interfaces replaced (paths relative to the dmuon source tree):
- *   dmuon_syrk_bf16          dmuon/optim/syrk_dispatch.py:582-651   syrk_or_cublas(A, D, B, C,
- *                                                                   alpha, beta, diag_add)
+ *   dmuon_syrk               dmuon/optim/syrk_dispatch.py:582-651   syrk_or_cublas(A, D, B, C,
+ *                                                                   alpha, beta, diag_add) on the
+ *                                                                   fp16 operands of
+ *                                                                   newton_schulz.py:376-433
  *                            dmuon/kernels/syrk_sm80.py:465-569     syrk_sm80(...) kernel call
- *   dmuon_ns_gemm_bf16       dmuon/optim/newton_schulz.py:268-270   X = a*X + B @ X
- *   dmuon_ns_gemm_final_bf16 dmuon/optim/newton_schulz.py:270-273 + dmuon/optim/muon.py:1728-1740
- *                                                                   last NS step fused with
+ *   dmuon_syrk_workspace_size (the padded path's scratch for shapes syrk_or_cublas hands to
+ *                            cuBLAS, syrk_dispatch.py:644-651)
+ *   dmuon_ns_gemm            dmuon/optim/newton_schulz.py:268-270   X = a*X + B @ X
+ *                            dmuon/optim/newton_schulz.py:405-410   X = Q @ X (restart)
+ *   dmuon_ns_gemm_final      dmuon/optim/newton_schulz.py:270-273,446 + dmuon/optim/muon.py:1728-1740
+ *                                                                   last NS product fused with
  *                                                                   W *= 1-lr*wd; W += -lr*s*U
+ *   dmuon_syrk_bf16, dmuon_ns_gemm_bf16, dmuon_ns_gemm_final_bf16: the three above with bf16
+ *                            operands (kept from ABI 103)
  *   dmuon_muon_pre           dmuon/optim/muon.py:1683-1694 + newton_schulz.py:257-266
  *                                                                   momentum, Nesterov, float(),
  *                                                                   orientation, cast, ||X||^2
@@ -55,6 +62,7 @@ extern "C" {
 
 #define DMUON_DTYPE_F32 0
 #define DMUON_DTYPE_BF16 1
+#define DMUON_DTYPE_F16 2 /* 16-bit product operands only (dmuon_syrk, dmuon_ns_gemm*) */
 
 /* Newton-Schulz device algorithms (the `backend` argument below). */
 #define DMUON_NS_DIRECT 0 /* X <- a X + (b A + c A A^T) X, A = X X^T, every step */
@@ -82,13 +90,36 @@ int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* 
 
 /*
  * D[l] = alpha * s_l * A[l] @ B[l]^T + beta * C[l] + diag_add * I     for l < batch
- * where s_l = alpha_dev[l] if alpha_dev != NULL else 1.
- * A, B: [M][K]; C, D: [M][M]. B == NULL means B = A. The result must be symmetric (always true
- * for B = A; the caller guarantees it when B != A, as syrk_or_cublas requires). Only the upper
- * triangle of tiles is computed; the lower triangle is written as its mirror. C may be NULL
- * (then beta is ignored) and may alias A, but D must not alias A, B or C.
- * tile: 128 or 256 (output tile edge); M % tile == 0, K % 64 == 0.
+ * where s_l = alpha_dev[l] if alpha_dev != NULL else 1, on 16-bit operands of type `dtype`
+ * (DMUON_DTYPE_F16, as gram_newton_schulz calls syrk_or_cublas on X.half(), or
+ * DMUON_DTYPE_BF16); fp32 accumulation, the epilogue in fp32, D rounded to `dtype`.
+ * A, B: [M][K] (row stride lda / ldb); C, D: [M][M]. B == NULL means B = A. The result must be
+ * symmetric (always true for B = A; the caller guarantees it when B != A, as syrk_or_cublas
+ * requires). Only the upper triangle of tiles is computed; the lower triangle is written as its
+ * mirror. C may be NULL (then beta is ignored) and may alias A, but D must not alias A, B or C.
+ * tile: 0 (automatic), 128 or 256 (output tile edge).
+ * Any M >= 0 and K >= 0 are accepted. When M is a multiple of the tile, K of 64, and every base
+ * is 16-byte aligned with leading dimensions and batch strides that are multiples of 8, the
+ * kernel reads the operands in place and `workspace` may be NULL; otherwise the call runs on
+ * zero-padded copies in `workspace` (device memory of dmuon_syrk_workspace_size bytes, at least
+ * 16-byte aligned; contents need no initialisation) and copies the M x M result into D.
  */
+int dmuon_syrk(int dtype, const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
+               int64_t strideB, const void* C, int64_t ldc, int64_t strideC, void* D, int64_t ldd,
+               int64_t strideD, int M, int K, int batch, float alpha, float beta, float diag_add,
+               const float* alpha_dev, int tile, void* workspace, int64_t workspace_bytes,
+               void* stream);
+
+/* Bytes of workspace dmuon_syrk needs for these arguments (0 when it reads the operands in
+ * place). Host-only; the pointers are inspected for alignment, never dereferenced. */
+int dmuon_syrk_workspace_size(int dtype, const void* A, int64_t lda, int64_t strideA,
+                              const void* B, int64_t ldb, int64_t strideB, const void* C,
+                              int64_t ldc, int64_t strideC, const void* D, int64_t ldd,
+                              int64_t strideD, int M, int K, int batch, int tile,
+                              int64_t* workspace_bytes);
+
+/* dmuon_syrk with bf16 operands, tile 128 or 256, M % tile == 0, K % 64 == 0 and aligned
+ * operands (no padded path). */
 int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, int64_t ldb,
                     int64_t strideB, const void* C, int64_t ldc, int64_t strideC, void* D,
                     int64_t ldd, int64_t strideD, int M, int K, int batch, float alpha, float beta,
@@ -98,8 +129,15 @@ int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, 
  * One Newton-Schulz step X' = s_l * (P @ X + beta * X) for l < batch, given P ([M][M], the
  * polynomial b*A + c*A@A of A = X X^T) and XT = X^T ([N][M]); s_l = alpha * alpha_dev[l] (or
  * alpha). Writes X' into Xout ([M][N], may alias X) and X'^T into XTout ([N][M], must not
- * alias XT). M % tile == 0, N % tile == 0.
+ * alias XT). Operands, X, Xout and XTout are 16-bit words of `dtype` (DMUON_DTYPE_F16 or
+ * DMUON_DTYPE_BF16). tile 128 or 256; M % tile == 0, N % tile == 0 (the NS planner pads).
  */
+int dmuon_ns_gemm(int dtype, const void* P, int64_t ldp, int64_t strideP, const void* XT,
+                  int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx, int64_t strideX,
+                  void* Xout, int64_t ldxo, int64_t strideXo, void* XTout, int64_t ldxto,
+                  int64_t strideXTo, int M, int N, int batch, float alpha, float beta,
+                  const float* alpha_dev, int tile, void* stream);
+/* dmuon_ns_gemm with bf16 operands */
 int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT, int64_t ldxt,
                        int64_t strideXT, const void* X, int64_t ldx, int64_t strideX, void* Xout,
                        int64_t ldxo, int64_t strideXo, void* XTout, int64_t ldxto,
@@ -116,7 +154,17 @@ int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* 
  *   pub_ptrs != NULL: pub[l] <- round(new W[l])         (dtype pub_dtype; needs w_ptrs): the
  *     forward copy of an owner's master weight, written in the same pass (the reference copies
  *     _owned_data into the packed forward buffer afterwards, fsdp2/group.py:766-781)
+ * P, XT and X are 16-bit words of `dtype` (DMUON_DTYPE_F16 or DMUON_DTYPE_BF16); U stays fp32
+ * up to the update (W <- round(fma(-lrs, U, round(W*decay))): one rounding, as add_(alpha=)).
  */
+int dmuon_ns_gemm_final(int dtype, const void* P, int64_t ldp, int64_t strideP, const void* XT,
+                        int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx,
+                        int64_t strideX, int M, int N, int batch, float alpha, float beta,
+                        const float* alpha_dev, int m_real, int n_real, int transposed,
+                        void* const* out_ptrs, int out_dtype, void* const* w_ptrs, int w_dtype,
+                        void* const* pub_ptrs, int pub_dtype, float decay, float lrs, int tile,
+                        void* stream);
+/* dmuon_ns_gemm_final with bf16 operands */
 int dmuon_ns_gemm_final_bf16(const void* P, int64_t ldp, int64_t strideP, const void* XT,
                              int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx,
                              int64_t strideX, int M, int N, int batch, float alpha, float beta,

@@ -18,9 +18,10 @@ It restates, in numpy, the reference algorithm of X-Square-Robot/dmuon on this p
                       kernels.
 * ``syrk_emulated_gram_ns`` the same for the build's Gram-form pipeline.
 * ``muon_step``       ``dmuon/optim/muon.py:1683-1740``: sum-form momentum
-                      (``buf.mul_(mu).add_(g)``, first step ``buf = g``), Nesterov
-                      ``g + mu*buf``, NS, ``W *= 1 - lr*wd`` when wd > 0, then
-                      ``W += -lr*0.2*sqrt(max(m, n)) * U.to(W.dtype)``.
+                      (``buf.mul_(mu).add_(g)``, first step ``buf = g``, two roundings),
+                      Nesterov ``g.add(buf, alpha=mu)`` (one rounding: ``fma_f32``), NS,
+                      ``W *= 1 - lr*wd`` when wd > 0, then
+                      ``W.add_(U.to(W.dtype), alpha=-lr*0.2*sqrt(max(m, n)))`` (one FMA).
 
 Pinning (tests/test_oracle.py): ``direct_ns``/``gram_ns`` in fp64 against ``closed_form_ns``;
 ``closed_form_ns`` against scalar special cases (rank-1, scaled partial identity, zero) that
@@ -83,6 +84,34 @@ def rnd(x: np.ndarray, dtype: str) -> np.ndarray:
     raise ValueError(dtype)
 
 
+def fma_f32(a, b, c) -> np.ndarray:
+    """Correctly rounded fp32 fused multiply-add ``a*b + c`` (one rounding), elementwise.
+
+    The reference's ``grad.add(buf, alpha=mu)`` (``muon.py:1694``) and ``owned.add_(U,
+    alpha=-lr*s)`` (``:1737-1740``) are single elementwise kernels computing ``a + alpha*b`` in
+    fp32; compiled for the GPU that expression contracts to one FMA, and torch's CPU kernel uses
+    a vector FMA. The product of two fp32 values is exact in fp64; the fp64 sum is corrected
+    with its exact TwoSum error where it lands on an fp32 rounding tie (the only case in which
+    rounding fp64 -> fp32 twice could differ from rounding once)."""
+    a64 = np.asarray(a, np.float32).astype(np.float64)
+    b64 = np.asarray(b, np.float32).astype(np.float64)
+    c64 = np.asarray(c, np.float32).astype(np.float64)
+    p = a64 * b64
+    s = p + c64
+    bv = s - p
+    e = (p - (s - bv)) + (c64 - bv)            # s + e == p + c exactly
+    with np.errstate(invalid="ignore", over="ignore"):
+        r = np.asarray(s.astype(np.float32))
+        up = np.nextafter(r, np.float32(np.inf))
+        dn = np.nextafter(r, np.float32(-np.inf))
+        r64 = r.astype(np.float64)
+        mid_up = (r64 + up.astype(np.float64)) * 0.5
+        mid_dn = (r64 + dn.astype(np.float64)) * 0.5
+    r = np.where((s == mid_up) & (e > 0), up, r)
+    r = np.where((s == mid_dn) & (e < 0), dn, r)
+    return np.asarray(r, dtype=np.float32)
+
+
 def _mm(a: np.ndarray, b: np.ndarray, dtype: str) -> np.ndarray:
     """Product with fp32 accumulation (fp64 for the fp64 pipeline)."""
     if dtype == "fp64":
@@ -113,13 +142,17 @@ def _orient_normalise(G: np.ndarray, eps: float, dtype: str):
 # ------------------------------------------------------------------------------------------
 def direct_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS, eps: float = 1e-7,
               dtype: str = "fp16") -> np.ndarray:
-    """newton_schulz.py:257-273; returns float32 (float64 for dtype='fp64')."""
+    """newton_schulz.py:257-273; returns float32 (float64 for dtype='fp64').
+
+    Each tensor op of the reference rounds to the compute dtype once. ``B = b * A + c * A @ A``
+    parses as ``(b*A) + ((c*A) @ A)`` (``*`` and ``@`` share one precedence level and associate
+    to the left), so ``c*A`` is rounded before the product."""
     X, t = _orient_normalise(G, eps, dtype)
     X = rnd(X, dtype)
     for a, b, c in coefficients:
         A = rnd(_mm(X, X.T, dtype), dtype)                       # A = X @ X.T
-        AA = rnd(_mm(A, A, dtype), dtype)                        # A @ A
-        B = rnd(rnd(b * A, dtype) + rnd(c * AA, dtype), dtype)   # B = b*A + c*A@A
+        cAA = rnd(_mm(rnd(c * A, dtype), A, dtype), dtype)       # (c * A) @ A
+        B = rnd(rnd(b * A, dtype) + cAA, dtype)                  # B = b*A + (c*A)@A
         X = rnd(rnd(a * X, dtype) + rnd(_mm(B, X, dtype), dtype), dtype)  # X = a*X + B@X
     if t:
         X = X.T
@@ -318,7 +351,8 @@ def syrk_emulated_gram_ns(G: np.ndarray, coefficients: Sequence = POLAR_EXPRESS,
 # Muon per-parameter update
 # ------------------------------------------------------------------------------------------
 def momentum_nesterov(g: np.ndarray, buf: Optional[np.ndarray], mu: float, nesterov: bool = True):
-    """muon.py:1683-1694 in fp32 with the reference's two roundings per line."""
+    """muon.py:1683-1694 in fp32: ``buf.mul_(mu).add_(grad)`` is two ops (two roundings);
+    ``grad.add(buf, alpha=mu)`` is one op, one rounding (``fma_f32``, mu as an fp32 scalar)."""
     g = np.asarray(g, dtype=np.float32)
     mu32 = np.float32(mu)
     if buf is None:
@@ -326,12 +360,13 @@ def momentum_nesterov(g: np.ndarray, buf: Optional[np.ndarray], mu: float, neste
     else:
         nb = (np.asarray(buf, np.float32) * mu32).astype(np.float32) + g
     nb = nb.astype(np.float32)
-    ns_in = (g + (mu32 * nb).astype(np.float32)).astype(np.float32) if nesterov else nb
+    ns_in = fma_f32(mu32, nb, g) if nesterov else nb
     return nb, ns_in
 
 
 def apply_update(W: np.ndarray, U: np.ndarray, lr: float, wd: float, w_dtype: str = "fp32"):
-    """muon.py:1728-1740: W *= 1 - lr*wd (wd > 0); W += -lr*0.2*sqrt(max(m, n)) * U."""
+    """muon.py:1728-1740: W *= 1 - lr*wd (wd > 0); W += -lr*0.2*sqrt(max(m, n)) * U, the
+    second line one ``add_(alpha=)`` op: a single fp32 FMA, then the cast to W's dtype."""
     rows = W.shape[0]
     cols = W.size // rows
     scale = 0.2 * math.sqrt(max(rows, cols))
@@ -339,7 +374,7 @@ def apply_update(W: np.ndarray, U: np.ndarray, lr: float, wd: float, w_dtype: st
     if wd > 0:
         Wf = rnd(Wf * np.float32(1.0 - lr * wd), w_dtype)
     Uw = rnd(U, w_dtype)
-    return rnd(Wf + np.float32(-lr * scale) * Uw, w_dtype)
+    return rnd(fma_f32(np.float32(-lr * scale), Uw, Wf), w_dtype)
 
 
 def muon_step(W, g, buf, lr=0.02, mu=0.95, wd=0.0, nesterov=True, coefficients=KELLER,

@@ -131,3 +131,52 @@ def test_pre_and_final_validation_without_gpu():
         p, 256, 0, p, 256, 0, p, 256, 0, 256, 256, 1, 1.0, 1.0, None, 256, 256, 0, p, 0, None,
         0, p, 1, 1.0, 0.0, 128, None))
     assert lib.dmuon_muon_pre_partials(128, 256) == 8
+
+
+def test_syrk_any_shape_workspace_plan_without_gpu():
+    """dmuon_syrk_workspace_size: 0 for operands the kernel reads in place; otherwise the
+    zero-padded copies (A, a distinct B, C and D) rounded to the tile and the 64-wide slice."""
+    lib = _C.lib()
+    need = ctypes.c_int64()
+
+    def ws(M, K, L=1, lda=None, a=1 << 20, b=None, ldb=0, c=None, tile=0, dtype=_C.DTYPE_F16):
+        lda = K if lda is None else lda
+        rc = lib.dmuon_syrk_workspace_size(dtype, ctypes.c_void_p(a), lda, M * lda,
+                                           None if b is None else ctypes.c_void_p(b), ldb,
+                                           M * ldb, None if c is None else ctypes.c_void_p(c), M,
+                                           M * M, ctypes.c_void_p(1 << 30), M, M * M, M, K, L,
+                                           tile, ctypes.byref(need))
+        assert rc == 0, lib.dmuon_last_error()
+        return need.value
+
+    def al(x):
+        return -(-x // 256) * 256
+
+    assert ws(512, 1024) == 0 and ws(1408, 2048) == 0
+    assert ws(1000, 3000) == al(1024 * 3008 * 2) + al(1024 * 1024 * 2)
+    assert ws(1000, 3000, c=1 << 24) == al(1024 * 3008 * 2) + 2 * al(1024 * 1024 * 2)
+    assert ws(1000, 3000, b=1 << 26, ldb=3000) == 2 * al(1024 * 3008 * 2) + al(1024 * 1024 * 2)
+    assert ws(512, 1024, lda=1025) > 0                   # rows not 16-byte aligned
+    assert ws(512, 1024, a=(1 << 20) + 2) > 0            # base not 16-byte aligned
+    assert ws(384, 640, L=3, tile=256) == 3 * 512 * 640 * 2 + al(3 * 512 * 512 * 2)
+    assert ws(384, 640, L=3, tile=128) == 0
+    # not a 16-bit operand type; a bad tile; D aliasing A
+    p = ctypes.c_void_p(1 << 20)
+    assert "16-bit" in _err(lib.dmuon_syrk_workspace_size(_C.DTYPE_F32, p, 64, 0, None, 0, 0,
+                                                          None, 0, 0, ctypes.c_void_p(1 << 30),
+                                                          64, 0, 64, 64, 1, 0,
+                                                          ctypes.byref(need)))
+    assert "tile" in _err(lib.dmuon_syrk(_C.DTYPE_F16, p, 64, 0, None, 0, 0, None, 0, 0,
+                                         ctypes.c_void_p(1 << 30), 64, 0, 64, 64, 1, 1.0, 0.0,
+                                         0.0, None, 96, None, 0, None))
+    assert "alias" in _err(lib.dmuon_syrk(_C.DTYPE_F16, p, 64, 0, None, 0, 0, None, 0, 0, p, 64,
+                                          0, 64, 64, 1, 1.0, 0.0, 0.0, None, 0, None, 0, None))
+    # the padded path without a workspace is refused before any launch
+    assert "workspace" in _err(lib.dmuon_syrk(_C.DTYPE_F16, p, 100, 0, None, 0, 0, None, 0, 0,
+                                              ctypes.c_void_p(1 << 30), 100, 0, 100, 100, 1, 1.0,
+                                              0.0, 0.0, None, 0, None, 0, None))
+    assert lib.dmuon_syrk(_C.DTYPE_F16, p, 64, 0, None, 0, 0, None, 0, 0, p, 64, 0, 0, 64, 1,
+                          1.0, 0.0, 0.0, None, 0, None, 0, None) == 0      # M = 0: no-op
+    assert "16-bit" in _err(lib.dmuon_ns_gemm(_C.DTYPE_F32, p, 256, 0, p, 256, 0, p, 256, 0, p,
+                                              256, 0, None, 0, 0, 256, 256, 1, 1.0, 1.0, None,
+                                              128, None))

@@ -3,14 +3,17 @@
 Numerics follow the reference's SYRK tests (tests/unit/test_syrk.py:41-172,
 test_syrk_stress.py:28-295): products against a plain torch fp32 reference with a bf16-output
 tolerance, alpha/beta/C/diag epilogue, B != A symmetric products, exact mirror symmetry and
-10-run bit-exact determinism. The bandwidth kernels are bit-exact against torch fp32 ops.
+10-run bit-exact determinism. The bandwidth kernels are bit-exact against the oracle's fp32
+restatement of the reference's ops (one rounding per torch op).
 """
 import ctypes
 
+import numpy as np
 import pytest
 import torch
 
 from dmuon_amd import _C
+from oracle import ns_oracle as o
 
 pytestmark = pytest.mark.gpu
 
@@ -155,7 +158,9 @@ def test_pre_kernel_bit_exact(gpu, rows, cols, gdt, first):
     for i in range(L):
         g = gs[i].float()
         nb = g.clone() if first else (buf0[i] * mu + g)
-        ns = g + nb * mu
+        # grad.add(buf, alpha=mu): one rounding (the oracle's exact fp32 FMA)
+        ns = torch.from_numpy(o.fma_f32(np.float32(mu), nb.cpu().numpy(),
+                                        g.cpu().numpy())).to(gpu)
         assert torch.equal(bufs[i], nb)
         exp = torch.zeros(Rp, Cp, dtype=torch.bfloat16, device=gpu)
         exp[:rows, :cols] = ns.to(torch.bfloat16)
@@ -191,5 +196,7 @@ def test_update_kernel_bit_exact(gpu, wdt):
             up.data_ptr(), _C.DTYPE_F32, 300 * 500, L, decay, lrs, _stream())
     for i in range(L):
         w1 = (W0[i].float() * decay).to(wdt).float()
-        exp = (w1 + (-lrs) * Us[i]).to(wdt)
+        # owned.add_(U, alpha=-lrs): one fp32 rounding, then the cast to W's dtype
+        exp = torch.from_numpy(o.fma_f32(-np.float32(lrs), Us[i].cpu().numpy(),
+                                         w1.cpu().numpy())).to(wdt).to(gpu)
         assert torch.equal(Ws[i], exp)

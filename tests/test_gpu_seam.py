@@ -1,0 +1,186 @@
+"""The reference's symmetric-product seam on the GPU: ``syrk_or_cublas`` (syrk_dispatch.py:582-651)
+on fp16 operands, called exactly as ``gram_newton_schulz`` calls it (newton_schulz.py:376-433):
+``R = X X^T``, ``Z = c R R^T + b R`` (C = R), ``Q = Z + a I`` (diag_add), and the symmetric
+B != A products ``R Z^T + a R`` and ``(R Z + a R) Z^T + a (R Z + a R)``; plus the NS GEMM export
+on fp16. Each result against torch fp32 on the same 16-bit inputs, with the bounds of the SYRK
+kernel tests (max |diff| <= 1% of max |ref|, relative Frobenius < 4e-3; 2e-2 for B != A, as
+the reference's tests/unit/test_syrk.py). Shapes the kernel cannot read in place (M not a
+multiple of the tile, K not a multiple of 64, unaligned rows) take the padded path and must
+equal the in-place path bit for bit where both apply.
+"""
+import ctypes
+import logging
+
+import pytest
+import torch
+
+import dmuon
+from dmuon_amd import _C
+from dmuon.optim.syrk_dispatch import syrk_or_cublas
+
+pytestmark = pytest.mark.gpu
+
+PE = dmuon.POLAR_EXPRESS_COEFFICIENTS
+
+
+def _check_close(out, ref, rel=1e-2, fro_tol=4e-3):
+    out, ref = out.float(), ref.float()
+    diff = (out - ref).abs().max().item()
+    lim = max(rel * ref.abs().max().item(), 1e-6)
+    assert diff <= lim, f"max|diff|={diff:.3e} > {lim:.3e}"
+    fro = ((out - ref).norm() / ref.norm()).item()
+    assert fro < fro_tol, f"rel Frobenius {fro:.3e}"
+
+
+def _x(m, n, seed, gpu, dtype=torch.float16):
+    """The reference's NS operand: X = G / (||G|| + eps), cast with .half(), contiguous."""
+    g = torch.Generator().manual_seed(seed)
+    G = torch.randn(m, n, generator=g)
+    return (G / (G.norm() + 1e-7)).to(dtype).to(gpu).contiguous()
+
+
+def _mm(a, b):
+    return a.float() @ b.float()
+
+
+@pytest.mark.parametrize("m,n", [(256, 1024), (1000, 3000), (1408, 2048), (70, 100)])
+def test_gram_call_sequence_fp16(gpu, m, n):
+    a, b, c = PE[0]
+    X = _x(m, n, m + n, gpu)
+    # Op 1: R = X X^T
+    R = torch.empty(m, m, dtype=torch.float16, device=gpu)
+    syrk_or_cublas(X, R)
+    _check_close(R, _mm(X, X.t()))
+    assert torch.equal(R, R.t())
+    # Op 2: Z = c R R^T + b R   (C = R)
+    Z = torch.empty_like(R)
+    syrk_or_cublas(R, Z, C=R, alpha=c, beta=b)
+    _check_close(Z, c * _mm(R, R.t()) + b * R.float())
+    # Op 3: Q = c R R^T + b R + a I   (diag_add)
+    Q = torch.empty_like(R)
+    syrk_or_cublas(R, Q, C=R, alpha=c, beta=b, diag_add=a)
+    _check_close(Q, c * _mm(R, R.t()) + b * R.float() + a * torch.eye(m, device=gpu))
+    # Ops 5, 6: B != A, symmetric (polynomials of one symmetric matrix)
+    RZ = torch.empty_like(R)
+    syrk_or_cublas(R, RZ, B=Z, C=R, alpha=1.0, beta=a)
+    _check_close(RZ, _mm(R, Z.t()) + a * R.float(), rel=2e-2, fro_tol=2e-2)
+    Rn = torch.empty_like(R)
+    syrk_or_cublas(RZ, Rn, B=Z, C=RZ, alpha=1.0, beta=a)
+    _check_close(Rn, _mm(RZ, Z.t()) + a * RZ.float(), rel=2e-2, fro_tol=2e-2)
+
+
+def test_padded_path_equals_in_place_path(gpu):
+    """The same numbers through the in-place path (aligned) and the padded path (a base 2
+    bytes off, or K not a multiple of 64 completed by zero columns) give the same bits."""
+    m, n = 512, 1024
+    X = _x(m, n, 5, gpu)
+    need = ctypes.c_int64()
+    args = (X.data_ptr(), n, 0, None, 0, 0, None, 0, 0, 1 << 20, m, 0, m, n, 1, 0)
+    _C.call("dmuon_syrk_workspace_size", _C.DTYPE_F16, *args, ctypes.byref(need))
+    assert need.value == 0                      # aligned: read in place
+    R0 = torch.empty(m, m, dtype=torch.float16, device=gpu)
+    syrk_or_cublas(X, R0)
+    big = torch.zeros(m, n + 1, dtype=torch.float16, device=gpu)
+    big[:, 1:] = X
+    Xv = big[:, 1:]                             # rows 2 bytes off 16-byte alignment
+    assert Xv.data_ptr() % 16 != 0 and Xv.stride(-1) == 1
+    R1 = torch.empty_like(R0)
+    syrk_or_cublas(Xv, R1)
+    assert torch.equal(R0, R1)
+    # K = 1000: the zero-padded tail adds exact zeros
+    Xk = X[:, :1000].contiguous()
+    Xz = torch.zeros_like(X)
+    Xz[:, :1000] = Xk
+    R2, R3 = torch.empty_like(R0), torch.empty_like(R0)
+    syrk_or_cublas(Xk, R2)
+    syrk_or_cublas(Xz, R3)
+    assert torch.equal(R2, R3)
+    # repeat calls reuse the workspace and reproduce the bits
+    R4 = torch.empty_like(R0)
+    syrk_or_cublas(Xk, R4)
+    assert torch.equal(R2, R4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_batched_and_tiles(gpu, dtype):
+    L, m, n = 3, 384, 640
+    X = torch.stack([_x(m, n, 40 + i, gpu, dtype) for i in range(L)])
+    ref = torch.bmm(X.float(), X.float().transpose(1, 2).contiguous())
+    outs = []
+    for tile in (0, 128, 256):
+        D = torch.empty(L, m, m, dtype=dtype, device=gpu)
+        syrk_or_cublas(X, D, tile=tile)            # m = 384: the 256-tile runs padded to 512
+        _check_close(D, ref)
+        outs.append(D)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+def test_seam_argument_errors(gpu, caplog):
+    X = _x(128, 256, 9, gpu)
+    R = torch.empty(128, 128, dtype=torch.float16, device=gpu)
+    with pytest.raises(TypeError, match="float16 or bfloat16"):
+        syrk_or_cublas(X.float(), R.float())
+    with pytest.raises(ValueError, match="shape"):
+        syrk_or_cublas(X, torch.empty(128, 129, dtype=torch.float16, device=gpu))
+    with pytest.raises(ValueError, match="contiguous"):
+        syrk_or_cublas(X, torch.empty(128, 256, dtype=torch.float16, device=gpu)[:, :128])
+    with pytest.raises(ValueError, match="dtype"):
+        syrk_or_cublas(X, R.to(torch.bfloat16))
+    # a non-K-contiguous operand is copied with a warning, as the reference does
+    XT = _x(256, 128, 9, gpu).t()
+    with caplog.at_level(logging.WARNING):
+        syrk_or_cublas(XT, R)
+    assert "not K-contiguous" in caplog.text
+    _check_close(R, _mm(XT, XT.t()))
+
+
+@pytest.mark.parametrize("dtype,code", [(torch.float16, _C.DTYPE_F16),
+                                        (torch.bfloat16, _C.DTYPE_BF16)])
+def test_ns_gemm_operand_dtypes(gpu, dtype, code):
+    """dmuon_ns_gemm: X' = s (P X + beta X) and X'^T, fp16 and bf16 operands."""
+    L, M, N = 2, 256, 768
+    g = torch.Generator().manual_seed(3)
+    P = (torch.randn(L, M, M, generator=g) * 0.05).to(dtype).to(gpu)
+    X = (torch.randn(L, M, N, generator=g) * 0.05).to(dtype).to(gpu)
+    XT = X.transpose(1, 2).contiguous()
+    Xo, XTo = torch.empty_like(X), torch.empty_like(XT)
+    stream = torch.cuda.current_stream().cuda_stream
+    _C.call("dmuon_ns_gemm", code, P.data_ptr(), M, M * M, XT.data_ptr(), M, M * N, X.data_ptr(),
+            N, M * N, Xo.data_ptr(), N, M * N, XTo.data_ptr(), M, M * N, M, N, L, 0.5, 3.4445,
+            None, 128, stream)
+    ref = 0.5 * (torch.bmm(P.float(), X.float()) + 3.4445 * X.float())
+    _check_close(Xo, ref)
+    assert torch.equal(XTo, Xo.transpose(1, 2))
+    if dtype == torch.bfloat16:       # the bf16 alias runs the same kernel
+        Xb = torch.empty_like(X)
+        _C.call("dmuon_ns_gemm_bf16", P.data_ptr(), M, M * M, XT.data_ptr(), M, M * N,
+                X.data_ptr(), N, M * N, Xb.data_ptr(), N, M * N, XTo.data_ptr(), M, M * N, M, N,
+                L, 0.5, 3.4445, None, 128, stream)
+        assert torch.equal(Xb, Xo)
+
+
+def test_reference_basic_dp_loop(gpu):
+    """The training loop of the reference's examples/basic_dp.py:63-93 through ``import dmuon``
+    at world_size=1 (``dmuon.replicate`` for the non-dedicated params): loss finite, every
+    dedicated weight updated, momentum state shaped (rows, cols)."""
+    from tests.test_host_api import _TinyModel
+
+    torch.manual_seed(42)
+    model = _TinyModel().to(gpu)
+    dmuon.dedicate_params(model, None, predicate=lambda n, p: "proj" in n and p.ndim == 2)
+    dmuon.replicate(model)
+    optimizer = dmuon.Muon(model, lr=0.02, momentum=0.95, ns_steps=5, adamw_lr=1e-3,
+                           adamw_weight_decay=0.01)
+    owned = dmuon.get_owned_params(model, rank=0)
+    before = [dp.param.detach().clone() for dp in owned]
+    for _ in range(3):
+        optimizer.zero_grad()
+        loss = model(torch.randn(4, 512, device=gpu))
+        loss.backward()
+        optimizer.step()
+        assert torch.isfinite(loss).item()
+    torch.cuda.synchronize()
+    for dp, w0 in zip(owned, before):
+        assert not torch.equal(dp.param.detach(), w0)
+        assert torch.isfinite(dp.param).all()
+        assert optimizer.state[id(dp)]["momentum_buffer"].shape == tuple(dp.full_shape)

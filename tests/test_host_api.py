@@ -105,3 +105,94 @@ def test_backend_strings():
     assert "hip_gfx950" in dmuon.get_ns_backend()
     st = dmuon.get_backend_status()
     assert st["arch"] == "gfx950" and st["quack_available"] is False
+
+
+class _Block(nn.Module):
+    def __init__(self, d=512, ff=2048):
+        super().__init__()
+        self.gate_proj = nn.Linear(d, ff, bias=False)
+        self.up_proj = nn.Linear(d, ff, bias=False)
+        self.down_proj = nn.Linear(ff, d, bias=False)
+        self.ln = nn.LayerNorm(d)
+
+    def forward(self, x):
+        h = self.ln(x)
+        return x + self.down_proj(self.gate_proj(h) * self.up_proj(h))
+
+
+class _TinyModel(nn.Module):
+    """The model of the reference's examples/basic_dp.py:21-44."""
+
+    def __init__(self, num_layers=4, d=512, ff=2048):
+        super().__init__()
+        self.layers = nn.ModuleList([_Block(d, ff) for _ in range(num_layers)])
+        self.head = nn.Linear(d, 1, bias=False)
+
+    def forward(self, x):
+        for layer in self.layers:
+            x = layer(x)
+        return self.head(x).sum()
+
+
+def test_reference_basic_dp_call_sequence():
+    """examples/basic_dp.py:59-87 through ``import dmuon`` at world_size=1, with
+    ``dmuon.replicate`` standing in for ``fully_shard`` (FSDP needs a process group): the
+    constructor, ``get_owned_params(model, rank=rank)``, ``dp.numel``, ``get_ns_backend()``,
+    ``zero_grad`` and the grad-readiness hook run on the CPU; the step itself is GPU-only."""
+    import dmuon
+
+    torch.manual_seed(42)
+    model = _TinyModel()
+    got = dmuon.dedicate_params(model, None, predicate=lambda n, p: "proj" in n and p.ndim == 2)
+    assert len(got) == 12
+    dmuon.replicate(model)
+    optimizer = dmuon.Muon(model, lr=0.02, momentum=0.95, ns_steps=5, adamw_lr=1e-3,
+                           adamw_weight_decay=0.01)
+    owned = dmuon.get_owned_params(model, rank=0)
+    total = sum(dp.numel for dp in owned)
+    assert len(owned) == 12 and total == 12 * 512 * 2048
+    assert all(dp.owner_rank == (0, 0) and dp.owner_shard == 0 for dp in owned)
+    assert "hip_gfx950" in dmuon.get_ns_backend()
+    assert dmuon.get_owned_params(model, rank=(0, 0)) == owned
+    assert dmuon.get_owned_params(model, rank=1) == [] and dmuon.get_owned_params(model, (0, 1)) == []
+    with pytest.raises(TypeError):
+        dmuon.get_owned_params(model, rank=True)
+    with pytest.raises(ValueError):
+        dmuon.get_owned_params(model, rank=-1)
+    optimizer.zero_grad()
+    loss = model(torch.randn(4, 512))
+    loss.backward()
+    dmuon.prepare_muon_grads(model, use_reduce_stream=True, coalesce_wait=True)
+    assert all(dp._reduced_grad is not None for dp in owned)
+    # the same module objects under both names
+    import dmuon_amd
+    from dmuon.optim.newton_schulz import NewtonSchulz
+    from dmuon.optim.syrk_dispatch import syrk_or_cublas
+
+    assert dmuon.Muon is dmuon_amd.Muon and NewtonSchulz is dmuon_amd.NewtonSchulz
+    assert syrk_or_cublas is dmuon_amd.optim.syrk_or_cublas
+    with pytest.raises(RuntimeError, match="GPU"):
+        optimizer.step()
+
+
+def test_restored_state_is_converted_or_rejected():
+    """Optimizer state restored by load_state_dict (keyed by id(dp), which torch leaves uncast)
+    is moved to the kernels' layout before any pointer is taken, or rejected."""
+    from dmuon_amd.optim.muon import _state_tensor
+
+    dev = torch.device("cpu")
+    ref_fmt = torch.randn(4, 6).to(torch.bfloat16)                 # the reference: grad.clone()
+    out = _state_tensor(ref_fmt, (4, 6), dev, torch.float32, "momentum_buffer", "w")
+    assert out.dtype == torch.float32 and out.is_contiguous()
+    assert torch.equal(out, ref_fmt.float())
+    view = torch.randn(6, 4).t()
+    out = _state_tensor(view, (4, 6), dev, torch.float32, "momentum_buffer", "w")
+    assert out.is_contiguous() and torch.equal(out, view)
+    flat = torch.randn(24)
+    assert _state_tensor(flat, (4, 6), dev, torch.float32, "m", "w").shape == (4, 6)
+    same = torch.randn(4, 6)
+    assert _state_tensor(same, (4, 6), dev, torch.float32, "m", "w") is same
+    with pytest.raises(ValueError, match="elements"):
+        _state_tensor(torch.zeros(5), (4, 6), dev, torch.float32, "momentum_buffer", "w")
+    with pytest.raises(TypeError, match="tensor"):
+        _state_tensor([0.0] * 24, (4, 6), dev, torch.float32, "momentum_buffer", "w")

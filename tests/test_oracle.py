@@ -215,7 +215,9 @@ def test_config1_known_answers():
     g = _g((64, 64), seed=1)
     nb, ns_in = o.momentum_nesterov(g, None, mu)
     assert np.array_equal(nb, g)                                   # first step: buf = g
-    assert np.array_equal(ns_in, (g + np.float32(mu) * g).astype(np.float32))
+    torch = pytest.importorskip("torch")
+    tg = torch.from_numpy(g)
+    assert np.array_equal(ns_in, tg.add(tg, alpha=mu).numpy())       # grad.add(buf, alpha=mu)
     np.testing.assert_allclose(ns_in, 1.95 * g, rtol=1e-6)
     # NS is scale invariant up to eps: NS(1.95 g) = NS(g)
     np.testing.assert_allclose(o.closed_form_ns(ns_in, o.KELLER), o.closed_form_ns(g, o.KELLER),
@@ -301,3 +303,102 @@ def test_emulation_with_scale_estimate(shape):
         bad = (u_ * o.poly_compose(s_ * 1.7, coeffs)) @ vt_
         bad = bad.T if shape[0] > shape[1] else bad
         assert o.rel_fro(bad, cf) > 5 * e1, (emu.__name__, o.rel_fro(bad, cf), e1)
+
+
+# --- the reference's op semantics (one rounding per torch op), pinned against torch itself ----
+def test_fma_f32_is_correctly_rounded():
+    """``fma_f32`` against exact rational arithmetic, including constructed cases where the fp64
+    sum lands exactly on an fp32 tie (rounding fp64 -> fp32 a second time would be wrong)."""
+    from fractions import Fraction
+
+    f32 = np.float32
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal(4000).astype(f32)
+    b = rng.standard_normal(4000).astype(f32)
+    c = (rng.standard_normal(4000) * rng.choice([1e-4, 1.0, 1e4], 4000)).astype(f32)
+    # a*b = 64 (1 + 2^-33) and 64 (1 - 2^-40) next to c = 2^30 and the odd 2^30 + 128: the
+    # fp64 sums are the fp32 midpoints 2^30 + 64 and 2^30 + 192, the exact sums are not
+    ta = np.array([1 + 2.0 ** -11, 1 + 2.0 ** -20], f32)
+    tb = np.array([64 * (1 - 2.0 ** -11 + 2.0 ** -22), 64 * (1 - 2.0 ** -20)], f32)
+    tc = np.array([2.0 ** 30, 2.0 ** 30 + 128], f32)
+    a, b, c = np.concatenate([a, ta]), np.concatenate([b, tb]), np.concatenate([c, tc])
+    r = o.fma_f32(a, b, c)
+
+    def nearest(i, x):
+        exact = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        best = None
+        for cand in (np.nextafter(x, f32(-np.inf)), x, np.nextafter(x, f32(np.inf))):
+            d = abs(Fraction(float(cand)) - exact)
+            if best is None or d < best[0]:
+                best = (d, cand)
+        return best[1]
+
+    for i in range(len(a)):
+        assert r[i] == nearest(i, r[i]), i
+    assert r[-2] == f32(2.0 ** 30 + 128) and r[-1] == f32(2.0 ** 30 + 128)
+    naive = (a[-2:].astype(np.float64) * b[-2:] + c[-2:]).astype(f32)
+    assert not np.array_equal(naive, r[-2:])          # the double rounding the emulation avoids
+
+
+def test_momentum_and_nesterov_match_torch_ops():
+    """muon.py:1689-1694 run with torch's own CPU operators: ``buf.mul_(mu).add_(grad)`` and
+    ``grad.add(buf, alpha=mu)`` agree with the oracle bit for bit; the two-rounding form of the
+    Nesterov line does not."""
+    torch = pytest.importorskip("torch")
+    mu = 0.95
+    g, buf = _g((96, 160), seed=31), _g((96, 160), seed=32)
+    nb, ns_in = o.momentum_nesterov(g, buf, mu)
+    tb = torch.from_numpy(buf.copy())
+    tg = torch.from_numpy(g)
+    tb.mul_(mu).add_(tg)
+    assert np.array_equal(nb, tb.numpy())
+    assert np.array_equal(ns_in, tg.add(tb, alpha=mu).numpy())
+    two = (g + (np.float32(mu) * nb).astype(np.float32)).astype(np.float32)
+    assert not np.array_equal(ns_in, two)
+
+
+@pytest.mark.parametrize("w_dtype", ["fp32", "bf16"])
+def test_update_matches_torch_ops(w_dtype):
+    """muon.py:1735-1740 with torch's CPU operators: ``owned.mul_(1 - lr*wd)`` then
+    ``owned.add_(U.to(owned.dtype), alpha=-lr*s)``. torch's CPU bf16 kernel rounds ``alpha``
+    itself to bf16 (its GPU kernel keeps it in fp32), so the bf16 case uses lr = 2^-7 and
+    400 columns, where ``-lr*s = -2^-5`` is exact in both."""
+    torch = pytest.importorskip("torch")
+    rows, cols, lr, wd = (300, 400, 2.0 ** -7, 0.1) if w_dtype == "bf16" else (96, 200, 0.02, 0.1)
+    tdt = torch.bfloat16 if w_dtype == "bf16" else torch.float32
+    W = torch.from_numpy(_g((rows, cols), seed=33)).to(tdt)
+    U = torch.from_numpy(_g((rows, cols), seed=34, std=0.05))
+    s = 0.2 * max(rows, cols) ** 0.5
+    Wt = W.clone()
+    Wt.mul_(1.0 - lr * wd)
+    Wt.add_(U.to(tdt), alpha=-lr * s)
+    Wo = o.apply_update(W.float().numpy(), U.numpy(), lr, wd, w_dtype)
+    assert np.array_equal(Wo, Wt.float().numpy())
+
+
+@pytest.mark.parametrize("coeffs", ["keller", "pe"])
+def test_direct_ns_op_order_matches_torch_fp16(coeffs):
+    """newton_schulz.py:266-270 executed literally with torch's CPU fp16 tensors for one step:
+    ``A = X @ X.T``, ``c * A @ A`` (= ``(c*A) @ A``) and ``B`` agree with the oracle's op order
+    bit for bit; rounding ``A @ A`` before the scale (the other reading of the line) does not."""
+    torch = pytest.importorskip("torch")
+    G = _g((64, 128), seed=35, std=1.0)
+    a, b, c = SETS[coeffs][0]
+    Xf, _ = o._orient_normalise(G, 1e-7, "fp16")
+    X = torch.from_numpy(Xf).half()
+    A = X @ X.T
+    cAA = c * A @ A
+    B = b * A + c * A @ A
+    Xn = a * X + B @ X
+    Af = o.rnd(o._mm(o.rnd(Xf, "fp16"), o.rnd(Xf, "fp16").T, "fp16"), "fp16")
+    assert np.array_equal(Af, A.float().numpy())
+    cAA_o = o.rnd(o._mm(o.rnd(c * Af, "fp16"), Af, "fp16"), "fp16")
+    assert np.array_equal(cAA_o, cAA.float().numpy())
+    Bo = o.rnd(o.rnd(b * Af, "fp16") + cAA_o, "fp16")
+    assert np.array_equal(Bo, B.float().numpy())
+    other = o.rnd(c * o.rnd(o._mm(Af, Af, "fp16"), "fp16"), "fp16")
+    assert np.mean(other == cAA.float().numpy()) < 0.8
+    # the whole first step (B @ X accumulates in another order on the CPU: equal up to
+    # rare fp16 rounding flips)
+    X1 = o.direct_ns(G, [SETS[coeffs][0]], dtype="fp16")
+    assert np.mean(X1 == Xn.float().numpy()) > 0.99
