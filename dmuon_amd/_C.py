@@ -63,6 +63,9 @@ _SIGNATURES = {
     "dmuon_muon_step_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_int, c_int,
                                       c_int, c_int, c_d, c_d, c_d, c_int, c_int, c_fp, c_int,
                                       c_int, c_ip, c_int, c_f, c_vp, c_i64, c_int, c_vp]),
+    "dmuon_muon_step_group_noalloc": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_int,
+                                              c_int, c_int, c_int, c_d, c_d, c_d, c_int, c_int,
+                                              c_fp, c_int, c_int, c_ip, c_int, c_f, c_int, c_vp]),
     "dmuon_muon_stage_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_d, c_int,
                                        c_int, c_int, c_f, c_vp, c_i64, c_int, c_vp]),
     "dmuon_muon_apply_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_d, c_d,

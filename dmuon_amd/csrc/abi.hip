@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -11,6 +12,13 @@
 #include "dmuon_amd_internal.h"
 
 using namespace dmuon;
+
+// Scratch of dmuon_muon_step_group_noalloc: one static device array, of which the loader gives
+// every GPU the library runs on its own copy, held until the process ends. Host code never uses
+// the array's name as an address (on the host it is a stand-in symbol): the device address of
+// the current GPU's copy comes from hipGetSymbolAddress on the first call on that GPU and is
+// kept per device (scratch_of_current_device).
+static __device__ __align__(256) char scratch[DMUON_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -118,10 +126,12 @@ struct Profiler {
   }
 };
 Profiler g_prof;
+// set while an entry point that must not allocate runs: the profiler records no events then
+thread_local bool g_no_events = false;
 
 template <class F>
 int timed(int cls, double flops, double bytes, hipStream_t stream, const char* who, F&& launch) {
-  if (!g_prof.on) return check_launch(launch(), who);
+  if (!g_prof.on || g_no_events) return check_launch(launch(), who);
   hipEvent_t a = g_prof.take(), b = g_prof.take();
   if (!a || !b) return fail("%s: hipEventCreate failed", who);
   if (hipEventRecord(a, stream) != hipSuccess) return fail("%s: hipEventRecord failed", who);
@@ -502,6 +512,35 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   }
   return 0;
 }
+
+// ---- scratch of dmuon_muon_step_group_noalloc (the array itself is at file scope above) --------
+constexpr int64_t kScratchBytes = DMUON_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(const char* who, void** out) {
+  int dev = -1;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail("%s: no current HIP device (%s)", who, hipGetErrorString(ge));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+struct NoEvents {
+  NoEvents() { g_no_events = true; }
+  ~NoEvents() { g_no_events = false; }
+};
 
 }  // namespace
 
@@ -998,6 +1037,37 @@ int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_pt
                    nullptr, 0, rows, cols, batch, (float)mu, nesterov, first_step, decay, lrs,
                    coeffs, T,
                    backend, restarts, n_restarts, eps, workspace, workspace_bytes, tile,
+                   static_cast<hipStream_t>(stream), who);
+}
+
+int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
+                                  float* const* est_ptrs, void* const* w_ptrs, int w_dtype,
+                                  void* const* pub_ptrs, int pub_dtype, int rows, int cols,
+                                  int batch, double lr, double mu, double wd, int nesterov,
+                                  int first_step, const float* coeffs, int T, int backend,
+                                  const int* restarts, int n_restarts, float eps, int tile,
+                                  void* stream) {
+  const char* who = "dmuon_muon_step_group_noalloc";
+  if (batch == 0) return 0;
+  if (!buf_ptrs || !w_ptrs) return fail("%s: buf_ptrs and w_ptrs must be non-NULL", who);
+  if (backend != DMUON_NS_DIRECT && backend != DMUON_NS_GRAM)
+    return fail("%s: unknown NS backend %d", who, backend);
+  int t, mp, np_;
+  int64_t need;
+  if (plan(rows, cols, batch, tile, 0, backend == DMUON_NS_GRAM, &t, &mp, &np_, &need)) return 1;
+  if (need > kScratchBytes)
+    return fail("%s: this group needs %lld bytes of scratch, more than the %lld bytes the "
+                "entry point holds per GPU; split the group or use dmuon_muon_step_group with "
+                "a workspace", who, (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (scratch_of_current_device(who, &ws)) return 1;
+  NoEvents no_events;
+  const double scale = 0.2 * sqrt((double)(rows > cols ? rows : cols));
+  const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
+  const float lrs = (float)(lr * scale);
+  return run_group(g_ptrs, g_dtype, buf_ptrs, est_ptrs, w_ptrs, w_dtype, pub_ptrs, pub_dtype,
+                   nullptr, 0, rows, cols, batch, (float)mu, nesterov, first_step, decay, lrs,
+                   coeffs, T, backend, restarts, n_restarts, eps, ws, kScratchBytes, tile,
                    static_cast<hipStream_t>(stream), who);
 }
 

@@ -261,6 +261,28 @@ int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_pt
                            int n_restarts, void* workspace, int64_t workspace_bytes, int tile,
                            void* stream);
 
+/*
+ * dmuon_muon_step_group for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference (its step allocates through torch). The arguments are dmuon_muon_step_group's minus
+ * the workspace: the scratch is one static device array of DMUON_NOALLOC_SCRATCH_BYTES per GPU
+ * (each GPU the library runs on holds it until the process ends), and a group whose planned
+ * workspace (dmuon_ns_plan) exceeds it is rejected with an error before any launch. The call
+ * allocates nothing: no hipMalloc / hipFree, no library allocation, no profiler events. Every
+ * call on one GPU shares that GPU's array and leaves its contents behind; a step needs none of
+ * them (it writes every scratch byte it reads), but calls that overlap on one GPU (two streams,
+ * two threads) race. `stream` must belong to the current device. Results equal
+ * dmuon_muon_step_group's bit for bit.
+ */
+#define DMUON_NOALLOC_SCRATCH_BYTES (256LL << 20)
+int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
+                                  float* const* est_ptrs, void* const* w_ptrs, int w_dtype,
+                                  void* const* pub_ptrs, int pub_dtype, int rows, int cols,
+                                  int batch, double lr, double mu, double wd, int nesterov,
+                                  int first_step, const float* coeffs, int T, int backend,
+                                  const int* restarts, int n_restarts, float eps, int tile,
+                                  void* stream);
+
 /* direct_newton_schulz / gram_newton_schulz (by `backend`, as above) for `batch` same-shape
  * rows x cols matrices: out[l] <- NS(g[l]). */
 int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,

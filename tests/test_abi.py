@@ -180,3 +180,26 @@ def test_syrk_any_shape_workspace_plan_without_gpu():
     assert "16-bit" in _err(lib.dmuon_ns_gemm(_C.DTYPE_F32, p, 256, 0, p, 256, 0, p, 256, 0, p,
                                               256, 0, None, 0, 0, 256, 256, 1, 1.0, 1.0, None,
                                               128, None))
+
+
+def test_noalloc_step_refuses_groups_beyond_its_scratch_without_gpu():
+    """dmuon_muon_step_group_noalloc checks the planned workspace against its static scratch
+    (DMUON_NOALLOC_SCRATCH_BYTES) before it touches the device."""
+    lib = _C.lib()
+    header = HEADER.read_text()
+    m = re.search(r"#define DMUON_NOALLOC_SCRATCH_BYTES \((\d+)LL << (\d+)\)", header)
+    limit = int(m.group(1)) << int(m.group(2))
+    coeff = (ctypes.c_float * 15)(*([3.4445, -4.7750, 2.0315] * 5))
+    rst = (ctypes.c_int * 1)(2)
+    p = ctypes.c_void_p(4096)
+    assert _C.plan(4096, 14336, 1, backend=_C.NS_GRAM)[3] > limit
+    msg = _err(lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 4096, 14336, 1,
+                                                 0.02, 0.95, 0.1, 1, 1, coeff, 5, 1, rst, 1,
+                                                 1e-7, 0, None))
+    assert "scratch" in msg and str(limit) in msg
+    assert "backend" in _err(lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 64,
+                                                               64, 1, 0.02, 0.95, 0.1, 1, 1,
+                                                               coeff, 5, 7, None, 0, 1e-7, 0,
+                                                               None))
+    assert lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 64, 64, 0, 0.02, 0.95,
+                                             0.1, 1, 1, coeff, 5, 0, None, 0, 1e-7, 0, None) == 0

@@ -1,0 +1,103 @@
+"""dmuon_muon_step_group_noalloc (scratch in a static device array) against
+dmuon_muon_step_group (a torch-allocated workspace), through the C ABI: identical inputs give
+identical weights, momentum buffers, kept scales and forward copies, bit for bit, over calls in a
+row whose second is smaller than the first (the scratch keeps the first call's contents). The
+refusal of a group larger than the scratch is checked on the CPU (tests/test_abi.py)."""
+import ctypes
+
+import pytest
+import torch
+
+import dmuon_amd as dmuon
+from dmuon_amd import _C
+from dmuon_amd.optim.newton_schulz import _coeff_array
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16 = _C.DTYPE_F32, _C.DTYPE_BF16
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptrs(ts, dev):
+    return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
+
+
+class _Group:
+    """One group's user tensors: gradients, fp32 momentum, kept scales, weights and (for an
+    fp32 master) bf16 forward copies."""
+
+    def __init__(self, rows, cols, L, w_dtype, publish, seed, dev):
+        g = torch.Generator().manual_seed(seed)
+        self.g = [(torch.randn(rows, cols, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+                  for _ in range(L)]
+        self.buf = [torch.zeros(rows, cols, device=dev) for _ in range(L)]
+        self.est = [torch.zeros(1, device=dev) for _ in range(L)]
+        self.w = [(torch.randn(rows, cols, generator=g) * 0.02).to(w_dtype).to(dev)
+                  for _ in range(L)]
+        self.pub = [w.to(torch.bfloat16) for w in self.w] if publish else []
+        self.w_code = F32 if w_dtype == torch.float32 else BF16
+        self.tables = (_ptrs(self.g, dev), _ptrs(self.buf, dev), _ptrs(self.est, dev),
+                       _ptrs(self.w, dev), _ptrs(self.pub, dev) if publish else None)
+
+    def clone(self):
+        c = object.__new__(_Group)
+        dev = self.g[0].device
+        c.g = [t.clone() for t in self.g]
+        c.buf = [t.clone() for t in self.buf]
+        c.est = [t.clone() for t in self.est]
+        c.w = [t.clone() for t in self.w]
+        c.pub = [t.clone() for t in self.pub]
+        c.w_code = self.w_code
+        c.tables = (_ptrs(c.g, dev), _ptrs(c.buf, dev), _ptrs(c.est, dev), _ptrs(c.w, dev),
+                    _ptrs(c.pub, dev) if c.pub else None)
+        return c
+
+    def tensors(self):
+        return self.buf + self.est + self.w + self.pub
+
+
+def _args(grp, rows, cols, first, backend, coeffs):
+    c, T = _coeff_array(coeffs)
+    rst = (ctypes.c_int * 1)(2) if backend == _C.NS_GRAM else None
+    gp, bp, ep, wp, pp = grp.tables
+    return [gp.data_ptr(), BF16, bp.data_ptr(), ep.data_ptr(), wp.data_ptr(), grp.w_code,
+            None if pp is None else pp.data_ptr(), BF16 if pp is not None else 0, rows, cols,
+            len(grp.g), 0.02, 0.95, 0.1, 1, first, c, T, backend, rst,
+            1 if backend == _C.NS_GRAM else 0, 1e-7]
+
+
+def _run_both(grp, rows, cols, first, backend, coeffs, dev):
+    other = grp.clone()
+    args = _args(grp, rows, cols, first, backend, coeffs)
+    L = len(grp.g)
+    _, _, _, nbytes = _C.plan(rows, cols, L, 0, 0, backend)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    _C.call("dmuon_muon_step_group", *args, ws.data_ptr(), ws.numel(), 0, _stream())
+    _C.call("dmuon_muon_step_group_noalloc", *_args(other, rows, cols, first, backend, coeffs),
+            0, _stream())
+    torch.cuda.synchronize()
+    for a, b in zip(grp.tensors(), other.tensors()):
+        assert torch.equal(a, b)
+    assert nbytes <= (256 << 20)
+    return other
+
+
+def test_noalloc_matches_workspace_entry_point(gpu):
+    pe = dmuon.POLAR_EXPRESS_COEFFICIENTS
+    keller = dmuon.KELLER_COEFFICIENTS
+    big = _Group(512, 1536, 3, torch.bfloat16, False, 1, gpu)
+    # call 1: a 3 x 512 x 1536 group, Gram NS, first step (exact staging)
+    big = _run_both(big, 512, 1536, 1, _C.NS_GRAM, pe, gpu)
+    # call 2, smaller: 2 x (300 x 200), tall and padded, fp32 master + bf16 forward copy,
+    # direct NS, on the scratch the first call left behind
+    small = _Group(300, 200, 2, torch.float32, True, 2, gpu)
+    _run_both(small, 300, 200, 1, _C.NS_DIRECT, keller, gpu)
+    # call 3: the first group's second step (momentum read, the kept scale stages the operand)
+    gen = torch.Generator().manual_seed(3)
+    for t in big.g:
+        t.copy_((torch.randn(t.shape, generator=gen) * 0.03).to(torch.bfloat16))
+    _run_both(big, 512, 1536, 0, _C.NS_GRAM, pe, gpu)
+
