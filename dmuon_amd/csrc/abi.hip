@@ -579,7 +579,7 @@ int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* 
   return rc;
 }
 
-int dmuon_abi_version(void) { return 104; }
+int dmuon_abi_version(void) { return DMUON_ABI_VERSION; }
 
 }  // extern "C"
 

@@ -71,7 +71,8 @@ extern "C" {
 /* Text of the last error raised on this thread ("" if none). */
 const char* dmuon_last_error(void);
 
-/* ABI version (major*100 + minor). */
+/* ABI version (major*100 + minor): DMUON_ABI_VERSION of the header the library was built with. */
+#define DMUON_ABI_VERSION 104
 int dmuon_abi_version(void);
 
 /*

@@ -24,7 +24,8 @@ def test_library_exports_every_declared_symbol():
     lib = _C.lib()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.dmuon_abi_version() >= 100
+    version = int(re.search(r"#define DMUON_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert lib.dmuon_abi_version() == version
     assert lib.dmuon_last_error() is not None
 
 
