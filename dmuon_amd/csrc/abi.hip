@@ -216,6 +216,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     s.sym_exact = 1;
     s.mode = EPI_SYM; s.alpha = alpha; s.beta = C ? beta : 0.f; s.diag = diag;
     s.C = C; s.ldc = m_pad; s.sC = as;
+    s.c_in = (C && C == A) ? C_IS_A : C_NONE;   // C's tile is the A panel's last slices
     s.D = D; s.ldd = m_pad; s.sD = as;
     s.D2 = D2; s.diag2 = diag2;
     return timed(PC_POLY, tri ? tri_sq_flops : full_sq_flops, 0.0, stream, who,
@@ -479,6 +480,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     q.sym_exact = 1;
     q.mode = EPI_SYM; q.alpha = cc / (rs * rs); q.beta = cb / rs; q.diag = 0.f;
     q.C = w.Am; q.ldc = m_pad; q.sC = as;
+    q.c_in = C_IS_A;
     q.D = w.Pm; q.ldd = m_pad; q.sD = as;
     if (timed(PC_POLY, poly_flops, 0.0, stream, who, [&] { return launch_nt(q, tile, stream); }))
       return 1;
@@ -666,6 +668,7 @@ int syrk_impl(const char* who, int elt, const void* A, int64_t lda, int64_t stri
     s.A = static_cast<const uint16_t*>(A); s.lda = lda; s.sA = strideA;
     s.B = static_cast<const uint16_t*>(B); s.ldb = ldb; s.sB = strideB;
     s.C = static_cast<const uint16_t*>(C); s.ldc = ldc; s.sC = strideC;
+    if (C && C == A && ldc == lda && (batch <= 1 || strideC == strideA) && K == M) s.c_in = C_IS_A;
     s.D = static_cast<uint16_t*>(D); s.ldd = ldd; s.sD = strideD;
     return check_launch(launch_nt(s, pl.tile, stream), who);
   }
@@ -690,12 +693,18 @@ int syrk_impl(const char* who, int elt, const void* A, int64_t lda, int64_t stri
       check_launch(launch_pad_copy(static_cast<const uint16_t*>(B), ldb, strideB, Bp, pl.Kp, sa,
                                    M, K, pl.Mp, pl.Kp, batch, stream), who))
     return 1;
-  if (C && check_launch(launch_pad_copy(static_cast<const uint16_t*>(C), ldc, strideC, Cp, pl.Mp,
-                                        sd, M, M, pl.Mp, pl.Mp, batch, stream), who))
+  // C == A (K == M): the padded C is the padded copy of A itself, and its tile is the A panel's
+  // last slices (NtArgs::c_in)
+  const bool c_from_a = C && C == A && ldc == lda && (batch <= 1 || strideC == strideA) &&
+                        K == M && pl.Kp == pl.Mp;
+  if (C && !c_from_a &&
+      check_launch(launch_pad_copy(static_cast<const uint16_t*>(C), ldc, strideC, Cp, pl.Mp, sd,
+                                   M, M, pl.Mp, pl.Mp, batch, stream), who))
     return 1;
   s.A = Ap; s.lda = pl.Kp; s.sA = sa;
   s.B = Bp; s.ldb = pl.Kp; s.sB = sa;
   s.C = Cp; s.ldc = pl.Mp; s.sC = sd;
+  if (c_from_a) { s.C = Ap; s.ldc = pl.Kp; s.sC = sa; s.c_in = C_IS_A; }
   s.D = Dp; s.ldd = pl.Mp; s.sD = sd;
   if (check_launch(launch_nt(s, pl.tile, stream), who)) return 1;
   return check_launch(launch_pad_copy(Dp, pl.Mp, sd, static_cast<uint16_t*>(D), ldd, strideD, M,

@@ -39,7 +39,14 @@ struct NtArgs {
   int elt;                                // ELT_BF16 / ELT_F16 (A, B, C, D, DT)
   int sym_exact;                          // EPI_SYM + tri: diagonal tiles stored exactly symmetric
   uint16_t* D2; float diag2;              // EPI_SYM + tri + sym_exact: also D2 = D + diag2 * I
+  // K-loop rotation of an M x M product (K == M) whose addend C is one of its own operands
+  // (C_IS_A: C is A, C_IS_B: C is B, the matrix symmetric): the slices of the 256-column block
+  // that holds the tile's C values run last, so the epilogue reads C from lines the block has
+  // just brought into L2. Per-element summation order depends only on the 256-block, so the
+  // 128- and 256-tile kernels still give the same bits.
+  int c_in;
 };
+enum { C_NONE = 0, C_IS_A = 1, C_IS_B = 2 };
 
 // Launches the NT MFMA kernel; picks the tile configuration from args (tile = 256 or 128).
 hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream);

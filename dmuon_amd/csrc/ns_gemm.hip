@@ -9,20 +9,21 @@
 //          writes X' and X'^T (EPI_NS), or on the last iteration applies the Muon
 //          weight update in the original orientation (EPI_FINAL)
 //
-// Tile machine: WM x WN waves; each wave owns a (BM/WM)x(BN/WN) sub-tile made of 32x32 MFMA
-// blocks (v_mfma_f32_32x32x16_bf16 or _f16, fp32 accumulate). 256x256 tiles run 8 waves (two per SIMD,
-// so one wave's MFMAs cover the other's LDS and barrier waits); 128x128 tiles run 4 waves with
-// two blocks per CU. K is staged through LDS in
-// BK-wide slices by direct global->LDS DMA (buffer_load_dwordx4 ... lds: each wave instruction
-// fills 1 KiB of LDS, no staging registers) into an S-deep ring, so S-1 slices are in flight
-// while one is consumed; the wave waits only for the slice it needs (s_waitcnt vmcnt(N)) and
-// then meets the others at a plain s_barrier. 16-byte chunks sit in LDS under an XOR swizzle
-// (chunk ^ f(row)) chosen so that every 16-lane pass of a fragment read covers all 64 banks.
+// Two tile machines on v_mfma_f32_16x16x32 (fp32 accumulate), K staged through LDS in 64-wide
+// slices by direct global->LDS DMA (buffer_load_dwordx4 ... lds: each wave instruction fills
+// 1 KiB of LDS, no staging registers) into a two-slot ring, 16-byte chunks under an XOR swizzle
+// (chunk ^ f(row)) so that every 16-lane pass of a fragment read covers all 64 banks:
+//   256x256 tiles (nt_pp_kernel): 8 waves of 128x64, two per SIMD, in a ping-pong schedule --
+//     one wave of a SIMD issues its MFMAs while the other reads its next fragments and moves
+//     the operands, so barrier and memory waits overlap MFMA work;
+//   128x128 tiles (nt_mfma_kernel): 4 waves of 64x64, two blocks per CU, for batches too small
+//     to fill the machine with 256-tiles; fragments double-buffered per substep, one barrier
+//     per slice.
 #include "dmuon_amd_internal.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -50,13 +51,31 @@ __device__ __forceinline__ float from_elt(uint16_t h) {
   if constexpr (E == ELT_F16) return static_cast<float>(__builtin_bit_cast(_Float16, h));
   else return bf2f(h);
 }
+// v_mfma_f32_16x16x32: a lane holds row (l % 16) of both operands at k-chunk l / 16, and four
+// consecutive output columns of one row. It gives the same bits as the 32x32x16 form (measured:
+// the products accumulate in the same order and round identically), and on MI355X it sustains
+// a higher clock under the board's power limit at equal MFMA work (sustained MFMA-only loops:
+// 1.90 vs 1.65-1.69 PFLOP/s; with 0.5 KB of fragment reads per 32 KFLOP: 1.70 vs 1.53).
 template <int E>
-__device__ __forceinline__ f32x16_t mfma_32x32x16(bf16x8_t b, bf16x8_t a, f32x16_t c) {
+__device__ __forceinline__ f32x4_t mfma_16x16x32(bf16x8_t b, bf16x8_t a, f32x4_t c) {
   if constexpr (E == ELT_F16)
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, b),
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, b),
                                                   __builtin_bit_cast(f16x8_t, a), c, 0, 0, 0);
-  else return __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0);
+  else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a, c, 0, 0, 0);
 }
+
+// A wave's accumulators as the epilogue walks them: per 32-row slab x of the wave tile, NQ groups
+// of four values -- group q of a lane holds slab row row(q), columns col(q) .. col(q) + 3. Indices
+// are compile-time after unrolling, so the registers are addressed statically.
+template <int BI, int BJ>            // BI x BJ blocks of 16x16 (v_mfma_f32_16x16x32)
+struct Acc16 {
+  static constexpr int SLABS = BI / 2, NQ = 2 * BJ;
+  f32x4_t (&acc)[BI][BJ];
+  int lane;
+  __device__ __forceinline__ int row(int q) const { return 16 * (q / BJ) + (lane & 15); }
+  __device__ __forceinline__ int col(int q) const { return 16 * (q % BJ) + 4 * (lane >> 4); }
+  __device__ __forceinline__ float val(int x, int q, int e) const { return acc[2 * x + q / BJ][q % BJ][e]; }
+};
 
 // Maps the hardware block id so that each XCD (blocks are dealt round-robin over 8 XCDs)
 // works on a contiguous range of logical tiles, which then share operands in that XCD's L2.
@@ -119,6 +138,16 @@ __device__ __forceinline__ void bare_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// A barrier that is also a scheduling fence: the compiler treats s_barrier as ordering memory
+// accesses only, and would otherwise move arithmetic (the MFMAs of a ping-pong phase) across it.
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 template <class T>
 __device__ __forceinline__ void wait_slices(int ahead) {
   // wait until at most `ahead` newer slices (T::LPT loads each) are still in flight
@@ -172,6 +201,15 @@ struct Occupancy {
   static constexpr int WPE = (BM / WM) * (BN / WN) >= 128 * 128 ? 1 : 2;
 };
 
+// First K slice of the tile's loop (see NtArgs::c_in): the slices that hold the tile's addend
+// values -- columns j0.. of A (C is A) or rows i0.. of B (C is B), read in the 256-aligned block
+// that contains them -- come last.
+__device__ __forceinline__ int first_slice(const NtArgs& a, int i0, int j0, int BK, int KT) {
+  if (a.c_in == C_NONE) return 0;
+  const int blk = (a.c_in == C_IS_A ? j0 : i0) / 256 + 1;
+  return (blk * 256 / BK) % KT;
+}
+
 // Logical tile of this block: matrix l of the batch, tile row bi, tile column bj.
 struct TilePos {
   int l, bi, bj;
@@ -222,23 +260,22 @@ __device__ __forceinline__ TilePos decode_tile(const NtArgs& a, int hb, int nblo
 // Epilogue of a finished tile: the accumulators of this wave (rows iw.., columns jw.. of
 // matrix l) through the MODE-specific staging and stores. Uses the per-wave LDS area
 // smem + wave * EPI_REGION; the caller guarantees no operand slice is still in use there.
-template <class T, int MODE, int E>
-__device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
-                                            f32x16_t (&acc)[T::TI][T::TJ], int l, int bi,
-                                            int bj, int i0, int j0, int lane, int wave,
+template <class T, int MODE, int E, class Acc>
+__device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const Acc& acc, int l,
+                                            int bi, int bj, int i0, int j0, int lane, int wave,
                                             int wi, int wj) {
-  const int li = lane & 31, lh = lane >> 5;
+  constexpr int NQ = Acc::NQ;
+  static_assert(Acc::SLABS * 32 == T::WTM && NQ * 4 * 64 == 32 * T::WTN, "accumulator layout");
   const int iw = i0 + wi * T::WTM, jw = j0 + wj * T::WTN;
   const uint16_t* Cb = a.C ? a.C + (long long)l * a.sC : nullptr;
   // addend C (X for the NS step, A for the polynomial), one 32-row slab at a time, the next
-  // slab's loads in flight while the current one is processed: element (y, g) of slab x is
-  // 4 bf16 at row iw + 32x + li, columns jw + 32y + 8g + 4lh .. +3
-  const unsigned clo = (unsigned)(li * a.ldc + 4 * lh);
+  // slab's loads in flight while the current one is processed: group q of slab x is 4 values at
+  // row iw + 32x + row(q), columns jw + col(q) .. +3
   auto load_c = [&](int x, u32x2_t* dst) {
-    const uint16_t* crow = Cb + (long long)(iw + 32 * x) * a.ldc + jw + clo;
+    const uint16_t* crow = Cb + (long long)(iw + 32 * x) * a.ldc + jw;
 #pragma unroll
-    for (int q = 0; q < T::TJ * 4; ++q)
-      dst[q] = *reinterpret_cast<const u32x2_t*>(crow + 32 * (q >> 2) + 8 * (q & 3));
+    for (int q = 0; q < NQ; ++q)
+      dst[q] = *reinterpret_cast<const u32x2_t*>(crow + (long long)acc.row(q) * a.ldc + acc.col(q));
   };
   float s = a.alpha;
   if (a.alpha_dev) s *= a.alpha_dev[l];
@@ -270,40 +307,38 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
     if constexpr (MODE == EPI_SYM) {
       if (a.D2) D2b = a.D2 + (long long)l * a.sD;
     }
-    u32x2_t cbuf[2][T::TJ * 4];
+    u32x2_t cbuf[2][NQ];
     if (Cb) load_c(0, cbuf[0]);
 #pragma unroll
-    for (int x = 0; x < T::TI; ++x) {
-      if (Cb && x + 1 < T::TI) load_c(x + 1, cbuf[(x + 1) & 1]);
-      u32x2_t o2[T::TJ * 4];
+    for (int x = 0; x < Acc::SLABS; ++x) {
+      if (Cb && x + 1 < Acc::SLABS) load_c(x + 1, cbuf[(x + 1) & 1]);
+      u32x2_t o2[NQ];
 #pragma unroll
-      for (int y = 0; y < T::TJ; ++y)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int jo = 32 * y + 8 * g;
-          float cv[4] = {0.f, 0.f, 0.f, 0.f};
-          if (Cb) {
-            const u32x2_t c2 = cbuf[x & 1][y * 4 + g];
-            cv[0] = from_elt<E>(c2.x & 0xffff); cv[1] = from_elt<E>(c2.x >> 16);
-            cv[2] = from_elt<E>(c2.y & 0xffff); cv[3] = from_elt<E>(c2.y >> 16);
-          }
-          uint16_t o[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float v = acc[x][y][4 * g + e];
-            float r;
-            if constexpr (MODE == EPI_SYM) {
-              r = s * v + a.beta * cv[e];
-              if (iw + 32 * x + li == jw + jo + 4 * lh + e) r += a.diag;
-            } else {
-              r = s * (v + a.beta * cv[e]);
-            }
-            o[e] = to_elt<E>(r);
-          }
-          o2[y * 4 + g].x = (unsigned)o[0] | ((unsigned)o[1] << 16);
-          o2[y * 4 + g].y = (unsigned)o[2] | ((unsigned)o[3] << 16);
-          *reinterpret_cast<u32x2_t*>(reg + li * T::EPN + (jo + 4 * lh) * 2) = o2[y * 4 + g];
+      for (int q = 0; q < NQ; ++q) {
+        const int ro = acc.row(q), co = acc.col(q);
+        float cv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (Cb) {
+          const u32x2_t c2 = cbuf[x & 1][q];
+          cv[0] = from_elt<E>(c2.x & 0xffff); cv[1] = from_elt<E>(c2.x >> 16);
+          cv[2] = from_elt<E>(c2.y & 0xffff); cv[3] = from_elt<E>(c2.y >> 16);
         }
+        uint16_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = acc.val(x, q, e);
+          float r;
+          if constexpr (MODE == EPI_SYM) {
+            r = s * v + a.beta * cv[e];
+            if (iw + 32 * x + ro == jw + co + e) r += a.diag;
+          } else {
+            r = s * (v + a.beta * cv[e]);
+          }
+          o[e] = to_elt<E>(r);
+        }
+        o2[q].x = (unsigned)o[0] | ((unsigned)o[1] << 16);
+        o2[q].y = (unsigned)o[2] | ((unsigned)o[3] << 16);
+        *reinterpret_cast<u32x2_t*>(reg + ro * T::EPN + co * 2) = o2[q];
+      }
       {
         constexpr int CPRW = T::WTN / 4;          // 8-byte chunks per slab row
         constexpr int RPIT = 64 / CPRW;           // slab rows per wave instruction
@@ -335,17 +370,14 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
       if (DTb) {
         // transposed slab [WTN][32] at pitch EPT; each lane scatters its 4 consecutive j
 #pragma unroll
-        for (int y = 0; y < T::TJ; ++y)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int j = 32 * y + 8 * g + 4 * lh;
-            uint16_t* col = reinterpret_cast<uint16_t*>(reg + j * T::EPT) + li;
-            const u32x2_t p = o2[y * 4 + g];
-            col[0] = (uint16_t)(p.x & 0xffff);
-            col[T::EPT / 2] = (uint16_t)(p.x >> 16);
-            col[T::EPT] = (uint16_t)(p.y & 0xffff);
-            col[3 * T::EPT / 2] = (uint16_t)(p.y >> 16);
-          }
+        for (int q = 0; q < NQ; ++q) {
+          uint16_t* col = reinterpret_cast<uint16_t*>(reg + acc.col(q) * T::EPT) + acc.row(q);
+          const u32x2_t p = o2[q];
+          col[0] = (uint16_t)(p.x & 0xffff);
+          col[T::EPT / 2] = (uint16_t)(p.x >> 16);
+          col[T::EPT] = (uint16_t)(p.y & 0xffff);
+          col[3 * T::EPT / 2] = (uint16_t)(p.y >> 16);
+        }
         const int cr = lane >> 2, cc = lane & 3;  // 4 lanes x 16 B per 32-value row
         const long long toff = (long long)(jw + cr) * ldt + iw + 32 * x + 8 * cc;
         uint16_t* dst = DTb + toff;
@@ -388,27 +420,23 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem,
     const bool valign = ((reinterpret_cast<uintptr_t>(wp) | reinterpret_cast<uintptr_t>(outp) |
                           reinterpret_cast<uintptr_t>(pp)) & 15) == 0;
 #pragma unroll
-    for (int x = 0; x < T::TI; ++x) {
-      u32x2_t cfin[T::TJ * 4];
+    for (int x = 0; x < Acc::SLABS; ++x) {
+      u32x2_t cfin[NQ];
       if (Cb) load_c(x, cfin);
 #pragma unroll
-      for (int y = 0; y < T::TJ; ++y) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int jo = 32 * y + 8 * g;
-          float cv[4] = {0.f, 0.f, 0.f, 0.f};
-          if (Cb) {
-            const u32x2_t c2 = cfin[y * 4 + g];
-            cv[0] = from_elt<E>(c2.x & 0xffff); cv[1] = from_elt<E>(c2.x >> 16);
-            cv[2] = from_elt<E>(c2.y & 0xffff); cv[3] = from_elt<E>(c2.y >> 16);
-          }
-          float4 u4;
-          u4.x = s * (acc[x][y][4 * g + 0] + a.beta * cv[0]);
-          u4.y = s * (acc[x][y][4 * g + 1] + a.beta * cv[1]);
-          u4.z = s * (acc[x][y][4 * g + 2] + a.beta * cv[2]);
-          u4.w = s * (acc[x][y][4 * g + 3] + a.beta * cv[3]);
-          *reinterpret_cast<float4*>(slab + li * kLd + jo + 4 * lh) = u4;
+      for (int q = 0; q < NQ; ++q) {
+        float cv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (Cb) {
+          const u32x2_t c2 = cfin[q];
+          cv[0] = from_elt<E>(c2.x & 0xffff); cv[1] = from_elt<E>(c2.x >> 16);
+          cv[2] = from_elt<E>(c2.y & 0xffff); cv[3] = from_elt<E>(c2.y >> 16);
         }
+        float4 u4;
+        u4.x = s * (acc.val(x, q, 0) + a.beta * cv[0]);
+        u4.y = s * (acc.val(x, q, 1) + a.beta * cv[1]);
+        u4.z = s * (acc.val(x, q, 2) + a.beta * cv[2]);
+        u4.w = s * (acc.val(x, q, 3) + a.beta * cv[3]);
+        *reinterpret_cast<float4*>(slab + acc.row(q) * kLd + acc.col(q)) = u4;
       }
       const int ibase = iw + 32 * x;
       // Read-modify-write of the slab in 8-element vectors (16 B of bf16 / 32 B of fp32):
@@ -628,69 +656,39 @@ void nt_mfma_kernel(const NtArgs a) {
             rsB, (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * T::NW), 16, offb[q], so_, 0, 0);    \
   } while (0)
 
-  // 8-wave tiles alternate the DMA between the two halves of the block (waves w and w + 4 share
-  // a SIMD when waves are dealt round-robin): the waves of half kt & 1 issue the whole of slice
-  // kt + 2 while their SIMD partners keep issuing MFMAs (measured 1.1% on the c5 step, 2-3% on
-  // the full products). A wave then has at most one slice of loads in flight, so the vmcnt(0)
-  // at each slice barrier still waits for exactly the next slice.
-  constexpr bool PP = T::NW == 8;
-  constexpr int HW = T::NW / 2;
-  const int vw = wave % HW, half = wave / HW;
-  unsigned offa2[16], offb2[16];
-  if constexpr (PP) {
+  // the wave sub-tile as BI x BJ blocks of 16x16 (v_mfma_f32_16x16x32)
+  constexpr int BI = T::WTM / 16, BJ = T::WTN / 16;
+  f32x4_t acc[BI][BJ];
 #pragma unroll
-    for (int q = 0; q < 2 * T::A_INST; ++q) {
-      const int r = (HW * q + vw) * T::RPI + lrow;
-      offa2[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8) * 2u;
-    }
+  for (int x = 0; x < BI; ++x)
 #pragma unroll
-    for (int q = 0; q < 2 * T::B_INST; ++q) {
-      const int r = (HW * q + vw) * T::RPI + lrow;
-      offb2[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
-    }
-  }
-#define DMUON_ISSUE2(slice_, slot_)                                                            \
-  do {                                                                                         \
-    char* st_ = smem + (slot_) * T::STAGE + vw * 1024;                                         \
-    const unsigned so_ = (unsigned)((slice_) * BK * 2);                                        \
-    _Pragma("unroll") for (int q = 0; q < 2 * T::A_INST; ++q)                                  \
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsA, (lds_ptr_t)(st_ + q * 1024 * HW), 16,    \
-                                                 offa2[q], so_, 0, 0);                         \
-    _Pragma("unroll") for (int q = 0; q < 2 * T::B_INST; ++q)                                  \
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                              \
-            rsB, (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * HW), 16, offb2[q], so_, 0, 0);      \
-  } while (0)
-
-  f32x16_t acc[T::TI][T::TJ];
-#pragma unroll
-  for (int x = 0; x < T::TI; ++x)
-#pragma unroll
-    for (int y = 0; y < T::TJ; ++y)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[x][y][v] = 0.f;
+    for (int y = 0; y < BJ; ++y) acc[x][y] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int KT = a.K / BK;
-  constexpr int KS = BK / 16;                     // MFMA substeps per slice
+  const int kt0 = first_slice(a, i0, j0, BK, KT);
+  auto rot = [&](int t) { return t + kt0 >= KT ? t + kt0 - KT : t + kt0; };
+  constexpr int KS = BK / 32;                     // MFMA substeps per slice
   static_assert(KS % 2 == 0, "fragment double buffer alternates per substep");
-  const int arow0 = wi * T::WTM + (lane & 31);
-  const int brow0 = wj * T::WTN + (lane & 31);
-  const int khalf = lane >> 5;
+  const int arow0 = wi * T::WTM + (lane & 15);
+  const int brow0 = wj * T::WTN + (lane & 15);
+  const int kq = lane >> 4;
 
+  // lane l reads row (l % 16) of each 16-row block at the 16-byte chunk 4 ks + l / 16
   auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8_t* af, bf16x8_t* bfr) {
-    const int kc = ks * 2 + khalf;
+    const int kc = ks * 4 + kq;
 #pragma unroll
-    for (int x = 0; x < T::TI; ++x) {
-      const int row = arow0 + x * 32;
+    for (int x = 0; x < BI; ++x) {
+      const int row = arow0 + x * 16;
       af[x] = *reinterpret_cast<const bf16x8_t*>(sa + row * T::ROWB + (T::slot(kc, row) << 4));
     }
 #pragma unroll
-    for (int y = 0; y < T::TJ; ++y) {
-      const int row = brow0 + y * 32;
+    for (int y = 0; y < BJ; ++y) {
+      const int row = brow0 + y * 16;
       bfr[y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
     }
   };
-  constexpr int NF = T::TI + T::TJ, NM = T::TI * T::TJ;
-  bf16x8_t af[2][T::TI], bfr[2][T::TJ];
+  constexpr int NF = BI + BJ, NM = BI * BJ;
+  bf16x8_t af[2][BI], bfr[2][BJ];
 
   // Ring schedule: slot s % S holds slice s; the prologue fills all S slots. Iteration kt
   // consumes slice kt. Substeps 0 .. KS-2 each read the next substep's fragments under their
@@ -699,17 +697,10 @@ void nt_mfma_kernel(const NtArgs a) {
   // and slot kt % S is free, so the DMA of slice kt+S and the reads of slice kt+1's first
   // fragments both run under the last substep's MFMAs and no wave starts a slice with an empty
   // pipeline. Past the end the DMA re-fetches the last slice into the free slot (never read),
-  // which keeps the number of loads per iteration, and so the vmcnt targets, uniform. With the
-  // alternating halves, half 0 issues slice 0 and waits for it, half 1 only issues slice 1.
-  if constexpr (PP) {
-    static_assert(S == 2, "alternating DMA halves need the two-slot ring");
-    if (half == 0) { DMUON_ISSUE2(0, 0); wait_vmcnt<0>(); }
-    else DMUON_ISSUE2(min(1, KT - 1), 1);
-  } else {
+  // which keeps the number of loads per iteration, and so the vmcnt targets, uniform.
 #pragma unroll
-    for (int s0 = 0; s0 < S; ++s0) DMUON_ISSUE(min(s0, KT - 1), s0);
-    wait_slices<T>(S - 1);
-  }
+  for (int s0 = 0; s0 < S; ++s0) DMUON_ISSUE(rot(min(s0, KT - 1)), s0);
+  wait_slices<T>(S - 1);
   bare_barrier();
   load_frags(smem, smem + T::A_BYTES, 0, af[0], bfr[0]);
 
@@ -724,12 +715,12 @@ void nt_mfma_kernel(const NtArgs a) {
       __builtin_amdgcn_s_setprio(1);
       load_frags(sa, sb, ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
 #pragma unroll
-      for (int x = 0; x < T::TI; ++x)
+      for (int x = 0; x < BI; ++x)
 #pragma unroll
-        for (int y = 0; y < T::TJ; ++y)
+        for (int y = 0; y < BJ; ++y)
           // MFMA rows <- j (B operand), MFMA cols <- i (A operand): each lane then holds
           // four consecutive j of one i, i.e. 8-byte row-major stores of D.
-          acc[x][y] = mfma_32x32x16<E>(bfr[ks & 1][y], af[ks & 1][x], acc[x][y]);
+          acc[x][y] = mfma_16x16x32<E>(bfr[ks & 1][y], af[ks & 1][x], acc[x][y]);
     }
     sched_substeps<KS - 1, NM, NF>();
     __builtin_amdgcn_s_setprio(0);
@@ -740,24 +731,156 @@ void nt_mfma_kernel(const NtArgs a) {
       const char* na = smem + ((kt + 1) % S) * T::STAGE;
       load_frags(na, na + T::A_BYTES, 0, af[0], bfr[0]);
     }
-    if constexpr (PP) {
-      if (half == (kt & 1)) DMUON_ISSUE2(min(kt + S, KT - 1), kt % S);
-    } else {
-      DMUON_ISSUE(min(kt + S, KT - 1), kt % S);
-    }
+    DMUON_ISSUE(rot(min(kt + S, KT - 1)), kt % S);
 #pragma unroll
-    for (int x = 0; x < T::TI; ++x)
+    for (int x = 0; x < BI; ++x)
 #pragma unroll
-      for (int y = 0; y < T::TJ; ++y)
-        acc[x][y] = mfma_32x32x16<E>(bfr[1][y], af[1][x], acc[x][y]);
+      for (int y = 0; y < BJ; ++y)
+        acc[x][y] = mfma_16x16x32<E>(bfr[1][y], af[1][x], acc[x][y]);
     sched_front<0, NM, NF, T::LPT>();
   }
 #undef DMUON_ISSUE
-#undef DMUON_ISSUE2
   wait_vmcnt<0>();
   bare_barrier();
 
-  nt_epilogue<T, MODE, E>(a, smem, acc, l, bi, bj, i0, j0, lane, wave, wi, wj);
+  nt_epilogue<T, MODE, E>(a, smem, Acc16<BI, BJ>{acc, lane}, l, bi, bj, i0, j0, lane, wave, wi,
+                          wj);
+}
+
+// Ping-pong schedule of the 256x256 tile with 8 waves of 128x64 (wave w and w + 4 share a SIMD).
+// Group 0 (waves 0-3) owns tile rows 0-127, group 1 (waves 4-7) rows 128-255; the groups run one
+// phase apart, every phase ending at a workgroup barrier:
+//   group 0:  |0 M0 |1 C0 |2 M1 |3 C1 |4 ... M(KT-1) |2KT-1 C(KT-1) |2KT        |2KT+1
+//   group 1:  |0    |1 M0 |2 C0 |3 M1 |4 ...         |2KT-1 M(KT-1) |2KT C(KT-1) |2KT+1
+// M(k) reads all of the wave's fragments of K slice k from LDS into registers; C(k) issues its
+// 16x16x32 MFMAs on them. While one wave of a SIMD runs its MFMAs back to back, its partner does the LDS
+// reads, so the MFMA pipe never waits on a fragment read or a barrier. Group 1 also moves the
+// operands: in M(k), once its own reads of slot k % S are back, it issues the DMA of slice k + S
+// into that slot (group 0 finished reading it a phase earlier) and waits until slice k + 1 has
+// landed -- under group 0's MFMAs -- before the barrier that opens group 0's M(k + 1). A slice
+// is in flight for 2S - 1 phases.
+template <int BK, int S, int MODE, int E>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void nt_pp_kernel(const NtArgs a) {
+  using T = Tile<256, 256, BK, S, 2, 4>;
+  __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
+  static_assert(T::LDS_BYTES <= 160 * 1024, "LDS budget");
+  constexpr int KS = BK / 32;                        // 16x16x32 MFMA substeps per slice
+  constexpr int NI = 256 / T::RPI / 4;               // DMA instructions per group-1 wave, per operand
+  constexpr int LPT1 = 2 * NI;                       // per group-1 wave per slice
+  static_assert(NI <= 8 && (S - 1) * LPT1 <= 63, "DMA instruction counts");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wj = wave & 3, wi = grp;
+
+  const TilePos tp = decode_tile(a, blockIdx.x, gridDim.x);
+  const int l = tp.l, bi = tp.bi, bj = tp.bj;
+  const int i0 = bi * 256, j0 = bj * 256;
+  const uint16_t* __restrict__ Ab = a.A + (long long)l * a.sA + (long long)i0 * a.lda;
+  const uint16_t* __restrict__ Bb = a.B + (long long)l * a.sB + (long long)j0 * a.ldb;
+
+  // group-1 DMA: instruction q of wave v = wave - 4 fills tile rows (4q + v) * RPI .. + RPI - 1
+  // of each operand (lane l writes LDS slot l % CPR of row l / CPR: it fetches the global chunk
+  // the swizzle places there)
+  const int v = wave & 3;
+  const int lrow = lane / T::CPR, lsl = lane % T::CPR;
+  unsigned offa[8], offb[8];
+#pragma unroll
+  for (int q = 0; q < NI; ++q) {
+    const int r = (4 * q + v) * T::RPI + lrow;
+    offa[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8) * 2u;
+    offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
+  }
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(Ab), (short)0, (int)((long long)256 * a.lda * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(Bb), (short)0, (int)((long long)256 * a.ldb * 2), 0x00020000);
+#define DMUON_PP_ISSUE(slice_, slot_)                                                          \
+  do {                                                                                         \
+    char* st_ = smem + (slot_) * T::STAGE + v * 1024;                                          \
+    const unsigned so_ = (unsigned)((slice_) * BK * 2);                                        \
+    _Pragma("unroll") for (int q = 0; q < NI; ++q)                                             \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsA, (lds_ptr_t)(st_ + q * 4096), 16,         \
+                                                 offa[q], so_, 0, 0);                          \
+    _Pragma("unroll") for (int q = 0; q < NI; ++q)                                             \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsB, (lds_ptr_t)(st_ + T::A_BYTES + q * 4096), \
+                                                 16, offb[q], so_, 0, 0);                      \
+  } while (0)
+
+  // the wave's 128x64 sub-tile as 8 x 4 blocks of 16x16
+  f32x4_t acc[8][4];
+#pragma unroll
+  for (int x = 0; x < 8; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y) acc[x][y] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // fragment of a 16-row block at substep ks: lane l reads row (l % 16) at 16-byte chunk
+  // 4 ks + l / 16 (every 16-lane pass of a ds_read_b128: 16 rows at one chunk, all 64 banks)
+  const int arow0 = wi * 128 + (lane & 15);
+  const int brow0 = wj * 64 + (lane & 15);
+  const int kq = lane >> 4;
+  bf16x8_t af[KS][8], bfr[KS][4];
+  auto mem_phase = [&](int slot) {
+    const char* sa = smem + slot * T::STAGE;
+    const char* sb = sa + T::A_BYTES;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int kc = ks * 4 + kq;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        const int row = arow0 + x * 16;
+        af[ks][x] = *reinterpret_cast<const bf16x8_t*>(sa + row * T::ROWB + (T::slot(kc, row) << 4));
+      }
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        const int row = brow0 + y * 16;
+        bfr[ks][y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
+      }
+    }
+  };
+
+  const int KT = a.K / BK;
+  const int kt0 = first_slice(a, i0, j0, BK, KT);
+  auto rot = [&](int t) { return t + kt0 >= KT ? t + kt0 - KT : t + kt0; };
+  if (grp == 1) {
+    // slices 0 .. S-1 (past the end: the last slice again, into a slot never read)
+#pragma unroll
+    for (int s0 = 0; s0 < S; ++s0) DMUON_PP_ISSUE(rot(min(s0, KT - 1)), s0);
+    wait_vmcnt<(S - 1) * LPT1>();                     // slice 0 has landed
+  }
+  phase_barrier();                                    // |0
+  if (grp == 1) phase_barrier();                      // |1: group 1 starts one phase behind
+  for (int kt = 0; kt < KT; ++kt) {
+    mem_phase(kt % S);
+    // this wave's fragments are in registers (and, for group 1, slot kt % S may be refilled)
+    __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0), vmcnt / expcnt untouched
+    if (grp == 1) {
+      if (kt + S < KT) {
+        DMUON_PP_ISSUE(rot(kt + S), kt % S);
+        wait_vmcnt<(S - 1) * LPT1>();                 // slice kt + 1 has landed
+      } else {
+        wait_vmcnt<0>();
+      }
+    }
+    phase_barrier();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int x = 0; x < 8; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y)
+          acc[x][y] = mfma_16x16x32<E>(bfr[ks][y], af[ks][x], acc[x][y]);
+    phase_barrier();
+  }
+#undef DMUON_PP_ISSUE
+  if (grp == 0) phase_barrier();                      // |2KT+1
+  wait_vmcnt<0>();
+
+  nt_epilogue<T, MODE, E>(a, smem, Acc16<8, 4>{acc, lane}, l, bi, bj, i0, j0, lane, wave, wi,
+                          wj);
 }
 
 }  // namespace
@@ -781,17 +904,30 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
       hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_FINAL, E>), grid,      \
                          block, 0, stream, a);                                                 \
   } while (0)
-  // 64-wide K slices double-buffered; 256-tiles with 8 waves, 128-tiles with 4 (two blocks per
-  // CU). Measured and not kept: 32-wide slices in 3-, 4- and 5-deep rings (the barriers they add
-  // cost what the deeper prefetch saves) and 256-tiles of 4 waves with 128x128 per wave.
+#define DMUON_PP(E)                                                                            \
+  do {                                                                                         \
+    dim3 block(512);                                                                           \
+    if (a.mode == EPI_SYM)                                                                     \
+      hipLaunchKernelGGL((nt_pp_kernel<64, 2, EPI_SYM, E>), grid, block, 0, stream, a);        \
+    else if (a.mode == EPI_NS)                                                                 \
+      hipLaunchKernelGGL((nt_pp_kernel<64, 2, EPI_NS, E>), grid, block, 0, stream, a);         \
+    else                                                                                       \
+      hipLaunchKernelGGL((nt_pp_kernel<64, 2, EPI_FINAL, E>), grid, block, 0, stream, a);      \
+  } while (0)
+  // 256-tiles: the ping-pong kernel, 8 waves, 64-wide K slices in a two-slot ring; 128-tiles:
+  // 4 waves, two blocks per CU. Measured and not kept: 32-wide slices in a four-slot ring for the
+  // ping-pong kernel (7-12% slower: twice the phases and barriers), the in-phase 8-wave schedule
+  // it replaced (3-11% slower on the c5 product shapes), 256-tiles of 4 waves with 128x128 per
+  // wave, and 32x32x16 MFMAs (identical results; 5-15% slower under the board power limit).
   if (a.elt == ELT_F16) {
-    if (tile == 256) DMUON_NT(256, 64, 2, 2, 4, ELT_F16);
+    if (tile == 256) DMUON_PP(ELT_F16);
     else DMUON_NT(128, 64, 2, 2, 2, ELT_F16);
   } else {
-    if (tile == 256) DMUON_NT(256, 64, 2, 2, 4, ELT_BF16);
+    if (tile == 256) DMUON_PP(ELT_BF16);
     else DMUON_NT(128, 64, 2, 2, 2, ELT_BF16);
   }
 #undef DMUON_NT
+#undef DMUON_PP
   return hipGetLastError();
 }
 

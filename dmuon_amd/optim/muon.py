@@ -72,7 +72,9 @@ class Muon(torch.optim.Optimizer):
     (``replicate_async``, ``group_prepare_ahead``, ``tp_distributed_gram*``,
     ``post_step_prefetch_*``, ``forward_prefetch_depth``, ...) are accepted and have no effect
     at world_size=1. ``workspace_limit_bytes`` bounds the NS scratch of one chunk (a bucket of
-    same-shape matrices is processed in chunks that fit); ``overlap_staging=True`` stages the
+    same-shape matrices is processed in chunks that fit, sized to waste little of the last wave
+    of tiles; the 24 GiB default holds a whole 4096 x 4096 Llama bucket of 64, or 32 of the
+    4096 x 14336 ones, in one chunk -- a small part of MI355X's 288 GB); ``overlap_staging=True`` stages the
     next chunk on a side stream while the current chunk's NS runs, with two such workspaces
     (bit-identical results; off by default: on MI355X the concurrent staging traffic slows the
     MFMA kernels by about as much as it hides). ``single_pass_staging=True`` (the default) keeps
@@ -99,7 +101,7 @@ class Muon(torch.optim.Optimizer):
         ns_backend: Union[str, NewtonSchulz] = "gram",
         nesterov: bool = True,
         record_step_profile: bool = False,
-        workspace_limit_bytes: int = 8 << 30,
+        workspace_limit_bytes: int = 24 << 30,
         ns_eps: float = 1e-7,
         overlap_staging: bool = False,
         single_pass_staging: bool = True,
@@ -309,9 +311,10 @@ class Muon(torch.optim.Optimizer):
         for (rows, cols, gdt, wdt, pdt, dev, first), items in self._buckets(group).items():
             _require_cuda(dev)
             num_cus = torch.cuda.get_device_properties(dev).multi_processor_count
-            chunk = self._chunk_size(rows, cols, len(items), num_cus, backend)
-            for s0 in range(0, len(items), chunk):
-                part = items[s0:s0 + chunk]
+            s0 = 0
+            for size in self._chunk_sizes(rows, cols, len(items), num_cus, backend):
+                part = items[s0:s0 + size]
+                s0 += size
                 for dp, _ in part:
                     st = self.state[id(dp)]
                     if "momentum_buffer" not in st:
@@ -394,13 +397,34 @@ class Muon(torch.optim.Optimizer):
                 dp._reduced_grad = None
         return count, numel
 
-    def _chunk_size(self, rows: int, cols: int, L: int, num_cus: int, backend: int) -> int:
+    def _chunk_sizes(self, rows: int, cols: int, L: int, num_cus: int, backend: int) -> list:
+        """Split a bucket of L same-shape matrices into chunks whose NS workspace fits
+        ``workspace_limit_bytes``: the fewest chunks, or a few more when that wastes less of the
+        last wave of tiles. Cost of a split = sum over chunks of the waves its triangle products
+        take (tiles / tiles resident at once, rounded up; a 128-tile wave counts half a
+        256-tile wave), the launches that dominate both NS forms."""
         per = _C.plan(rows, cols, 1, 0, num_cus, backend)[3]
-        chunk = max(1, min(L, self._workspace_limit // max(per, 1)))
-        while chunk > 1 and _C.plan(rows, cols, chunk, 0, num_cus, backend)[3] > \
+        most = max(1, min(L, self._workspace_limit // max(per, 1)))
+        while most > 1 and _C.plan(rows, cols, most, 0, num_cus, backend)[3] > \
                 self._workspace_limit:
-            chunk -= 1
-        return chunk
+            most -= 1
+
+        def waves(size: int) -> float:
+            tile, m_pad, _, _ = _C.plan(rows, cols, size, 0, num_cus, backend)
+            mt = m_pad // tile
+            tiles = size * mt * (mt + 1) // 2
+            if tile == 256:
+                return float(-(-tiles // num_cus))
+            return 0.5 * (-(-tiles // (2 * num_cus)))
+
+        best = None
+        n_min = -(-L // most)
+        for n in range(n_min, min(L, n_min + 3) + 1):
+            sizes = [L // n + (1 if i < L % n else 0) for i in range(n)]
+            cost = sum(waves(sz) for sz in sizes)
+            if best is None or cost < best[0] - 1e-9:
+                best = (cost, sizes)
+        return best[1]
 
     def _get_workspace(self, device, nbytes: int, slot: int = 0) -> Tensor:
         ws = self._workspaces[slot]
