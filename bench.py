@@ -1,27 +1,29 @@
 #!/usr/bin/env python3
-"""Benchmark: one full Muon optimizer step over the Llama-3-8B-shaped matrix set on one MI355X.
+"""Benchmark: one full Muon optimizer step over the Llama-3-8B-shaped parameter set on one MI355X.
 
 Workload (BASELINE config c5): 32 layers x {q, o 4096x4096; k, v 1024x4096; gate, up
-14336x4096; down 4096x14336} = 224 matrices, bf16 weights and gradients ~N(0, 0.02^2), fp32
-momentum, all owned by the single rank; dmuon_amd.Muon(lr=0.02, momentum=0.95 Nesterov,
-weight_decay=0.1) with the reference Muon's default Newton-Schulz: gram_newton_schulz, 5
-Polar-Express steps, restart at step 2, fp16 operands (--ns direct: 5 direct steps of Keller's
-(3.4445, -4.7750, 2.0315) instead, also fp16). A "step" is one optimizer.step() over the set
-(momentum, normalisation, 5 NS steps, update). Synthetic data is generated on the GPU (values
-do not affect timing).
+14336x4096; down 4096x14336} = 224 dedicated matrices, bf16 weights and gradients ~N(0, 0.02^2),
+fp32 momentum, all owned by the single rank, plus the AdamW-routed rest of Llama-3-8B
+(embeddings and lm_head 128256x4096, 65 RMSNorm weights of 4096, bf16); dmuon_amd.Muon(lr=0.02,
+momentum=0.95 Nesterov, weight_decay=0.1) with the reference Muon's default Newton-Schulz:
+gram_newton_schulz, 5 Polar-Express steps, restart at step 2, fp16 operands (--ns direct: 5
+direct steps of Keller's (3.4445, -4.7750, 2.0315) instead, also fp16). A "step" is one
+optimizer.step(): momentum, normalisation, 5 NS steps and the update of every matrix, and the
+AdamW update of the rest. Synthetic data is generated on the GPU (values do not affect timing).
 
-Prints ONE JSON line. Extra fields: per-kernel-class breakdown from the library's hipEvent
-profiler (a second, separately timed pass), the roofline of the dominant kernel family (the
-MFMA NT kernels: Gram / SYRK products, polynomial and Q products, NS GEMM) and of the fused
-momentum kernel, the gradient clip and the AdamW step for the embeddings/norms (reported
-separately), and a CPU baseline: the numpy restatement of the reference math on the host cores,
-over a bounded sample of the same workload.
+Prints ONE JSON line. Besides the contract fields: the per-kernel-class breakdown from the
+library's hipEvent profiler (a second, separately timed pass), the roofline of the dominant
+kernel family (the MFMA NT kernels) and of the fused momentum kernel next to a plain device copy
+measured in the same run, the AdamW share of the step, the gradient clip, the other BASELINE
+configs (c2 single 4096^2 matrix x 100 steps, c3 aspect ratios one matrix each, c4 the MoE
+expert batch) each with ms / TFLOP/s / fraction of peak, and a CPU baseline: the numpy
+restatement of the reference math (fp16 cast points emulated) on the host cores, over a bounded
+sample of the same workload.
 """
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -34,15 +36,20 @@ LLAMA3_8B_LAYER = {  # name: (rows, cols)
     "gate": (14336, 4096), "up": (14336, 4096), "down": (4096, 14336),
 }
 N_LAYERS = 32
+LLAMA3_8B_VOCAB, LLAMA3_8B_DIM, LLAMA3_8B_NORMS = 128256, 4096, 65
 KELLER = [(3.4445, -4.7750, 2.0315)] * 5
-MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 / fp16
 HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+C3_SHAPES = [(1024, 16384), (16384, 1024), (4096, 14336), (14336, 4096), (2048, 8192)]
+C4_SHAPES = [(1408, 2048)] * 64 + [(2048, 1408)] * 64
 
 
-def build_matrix_set(torch, device, dtype, n_layers):
+def build_model(torch, device, dtype, n_layers, with_rest):
+    """The c5 parameter set: `mats` (dedicated to Muon) and, with_rest, the AdamW-routed
+    embeddings, lm_head and norms; gradients attached."""
     from torch import nn
 
-    class MatrixSet(nn.Module):
+    class Llama8BParams(nn.Module):
         def __init__(self):
             super().__init__()
             gen = torch.Generator(device=device).manual_seed(0)
@@ -52,8 +59,17 @@ def build_matrix_set(torch, device, dtype, n_layers):
                     w = torch.empty(shape, device=device, dtype=dtype)
                     w.normal_(0.0, 0.02, generator=gen)
                     self.mats.append(nn.Parameter(w))
+            if with_rest:
+                shape = (LLAMA3_8B_VOCAB, LLAMA3_8B_DIM)
+                self.embed = nn.Parameter(torch.empty(shape, device=device, dtype=dtype))
+                self.lm_head = nn.Parameter(torch.empty(shape, device=device, dtype=dtype))
+                self.embed.data.normal_(0.0, 0.02, generator=gen)
+                self.lm_head.data.normal_(0.0, 0.02, generator=gen)
+                self.norms = nn.ParameterList(
+                    [nn.Parameter(torch.ones(LLAMA3_8B_DIM, device=device, dtype=dtype))
+                     for _ in range(LLAMA3_8B_NORMS)])
 
-    m = MatrixSet()
+    m = Llama8BParams()
     gen = torch.Generator(device=device).manual_seed(1)
     for p in m.parameters():
         g = torch.empty_like(p)
@@ -62,24 +78,62 @@ def build_matrix_set(torch, device, dtype, n_layers):
     return m
 
 
+def build_set(torch, device, shapes, seed):
+    """bf16 matrices of the given shapes with N(0, 0.02^2) weights and gradients."""
+    from torch import nn
+
+    class MatrixSet(nn.Module):
+        def __init__(self):
+            super().__init__()
+            gen = torch.Generator(device=device).manual_seed(seed)
+            self.mats = nn.ParameterList()
+            for shape in shapes:
+                w = torch.empty(shape, device=device, dtype=torch.bfloat16)
+                w.normal_(0.0, 0.02, generator=gen)
+                self.mats.append(nn.Parameter(w))
+
+    m = MatrixSet()
+    gen = torch.Generator(device=device).manual_seed(seed + 1)
+    for p in m.parameters():
+        g = torch.empty_like(p)
+        g.normal_(0.0, 0.02, generator=gen)
+        p.grad = g
+    return m
+
+
+def cpu_info() -> dict:
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_count": os.cpu_count(), "cpu_model": model}
+
+
 def cpu_baseline(budget_s: float = 60.0, ns: str = "gram") -> dict:
-    """Times the oracle (numpy restatement of the reference math, fp32 compute) on the host:
-    momentum + Nesterov + 5 NS steps (the same NS form as the GPU leg: gram_newton_schulz with
-    Polar-Express and a restart at 2, or direct Keller) + update for every matrix of layer 0
-    (q, k, v, o, gate, up, down); the 32-layer step is that time x 32 (all layers have the same
-    shapes)."""
+    """Times the oracle (numpy restatement of the reference math with the reference's fp16 cast
+    points: every tensor op rounded to fp16, products accumulated in fp32) on the host:
+    momentum + Nesterov + 5 NS steps (the same NS form as the GPU leg) + update for every
+    matrix of layer 0 (q, k, v, o, gate, up, down); the 32-layer step is that time x 32 (all
+    layers have the same shapes). The AdamW part of the step is not included."""
     import numpy as np
 
     from oracle import ns_oracle as o
 
+    threads = None
     try:
         from threadpoolctl import threadpool_info
         threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     except Exception:
-        threads = os.cpu_count() or 1
+        pass
     rng = np.random.default_rng(0)
     per = {}
     spent = 0.0
+    info = cpu_info()
     for name, (rows, cols) in LLAMA3_8B_LAYER.items():
         W = rng.standard_normal((rows, cols), dtype=np.float32) * 0.02
         g = rng.standard_normal((rows, cols), dtype=np.float32) * 0.02
@@ -87,21 +141,25 @@ def cpu_baseline(budget_s: float = 60.0, ns: str = "gram") -> dict:
         t0 = time.perf_counter()
         o.muon_step(W, g, buf, lr=0.02, mu=0.95, wd=0.1,
                     coefficients=o.POLAR_EXPRESS if ns == "gram" else o.KELLER, ns=ns,
-                    dtype="fp32")
+                    dtype="fp16")
         dt = time.perf_counter() - t0
         spent += dt
         per[name] = round(dt, 3)
         if spent > budget_s and len(per) < len(LLAMA3_8B_LAYER):
-            return {"value": None, "unit": "ms", "cores": threads, "kind": "port",
+            return {"value": None, "unit": "ms", "cores": threads or info["cpu_count"],
+                    "kind": "port", **info,
                     "sample": f"incomplete: {spent:.1f} s budget exhausted after {list(per)}"}
     return {
         "value": round(spent * N_LAYERS * 1e3, 1),
         "unit": "ms",
-        "cores": threads,
+        "cores": threads or info["cpu_count"],
         "kind": "port",
-        "sample": (f"oracle/ns_oracle.muon_step(ns={ns!r}) (numpy, fp32 compute; the "
-                   "reference's fp16 casts are not emulated) on the 7 matrices of layer 0 = "
-                   f"{spent:.1f} s of CPU work; the 32-layer step is extrapolated as 32 x layer 0"),
+        **info,
+        "sample": (f"oracle/ns_oracle.muon_step(ns={ns!r}, dtype='fp16') (numpy: each op "
+                   "rounded to fp16 as the reference's tensors are, products accumulated in "
+                   "fp32) on the 7 matrices of layer 0 = "
+                   f"{spent:.1f} s of CPU work on {threads} BLAS threads; the 32-layer step is "
+                   "extrapolated as 32 x layer 0 (Muon matrices only, no AdamW)"),
         "per_matrix_s": per,
     }
 
@@ -143,6 +201,74 @@ def library_compare(torch, dev, _C, reps: int = 5) -> dict:
     return out
 
 
+def time_steps(torch, opt, warmup: int, steps: int) -> list:
+    """Per-step milliseconds of `steps` optimizer steps after `warmup` untimed ones."""
+    for _ in range(warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record()
+    for k in range(steps):
+        opt.step()
+        evs[k + 1].record()
+    torch.cuda.synchronize()
+    return [evs[k].elapsed_time(evs[k + 1]) for k in range(steps)]
+
+
+def config_leg(torch, dmuon, dev, shapes, ns, steps, warmup, seed, momentum_init=False):
+    """One BASELINE config on its own matrices (bf16 weights updated in place, fp32 momentum):
+    ms per optimizer step and useful NS TFLOP/s."""
+    from dmuon_amd.optim.newton_schulz import ns_useful_flops
+
+    model = build_set(torch, dev, shapes, seed)
+    dmuon.dedicate_params(model, None, lambda n, p: p.dim() == 2,
+                          param_policy={"defaults": {"master_dtype": torch.bfloat16}})
+    dmuon.replicate(model)
+    opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=ns)
+    if momentum_init:
+        gen = torch.Generator(device=dev).manual_seed(seed + 2)
+        for dp in dmuon.get_owned_params(model):
+            buf = torch.empty(dp.full_shape, device=dev, dtype=torch.float32)
+            buf.normal_(0.0, 0.02, generator=gen)
+            opt.state[id(dp)]["momentum_buffer"] = buf
+    per = sorted(time_steps(torch, opt, warmup, steps))
+    ms = per[len(per) // 2]
+    flops = sum(ns_useful_flops(*s, 5, ns.backend, ns.restart_iterations) for s in shapes)
+    tf = flops / (ms * 1e-3) / 1e12
+    from dmuon_amd import _C
+    tile, m_pad, n_pad, _ = _C.plan(*shapes[0], 1, 0, 0, _C.NS_GRAM if ns.backend == "gram"
+                                    else _C.NS_DIRECT)
+    out = {"ms_per_step_median": round(ms, 3), "steps": steps,
+           "useful_ns_tflop": round(flops / 1e12, 4), "tflops": round(tf, 1),
+           "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+           "ns_shape": [min(shapes[0]), max(shapes[0])]}
+    del opt, model
+    torch.cuda.empty_cache()
+    return out
+
+
+def copy_leg(torch, dev, gib: int = 4, reps: int = 5) -> dict:
+    """A plain device-to-device copy of `gib` GiB: the streaming rate of this HBM, read + write
+    bytes over the time (the practical ceiling the bandwidth-bound kernels run against)."""
+    n = (gib << 30) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    gbs = 2.0 * n * 4 / (ms * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bytes_moved": 2 * n * 4, "ms": round(ms, 3), "gbs": round(gbs, 1),
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), "impl": "torch Tensor.copy_"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -150,8 +276,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=N_LAYERS, help="layers of the matrix set")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-adamw", action="store_true")
+    ap.add_argument("--no-adamw", action="store_true",
+                    help="leave the AdamW-routed embeddings / lm_head / norms out of the step")
     ap.add_argument("--no-clip", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the c2 / c3 / c4 legs")
     ap.add_argument("--ns", choices=("gram", "direct"), default="gram",
                     help="gram: the reference Muon's default NS (gram_newton_schulz, "
                          "Polar-Express coefficients, restart at step 2; fp16 operands); "
@@ -182,6 +310,7 @@ def main():
 
     import dmuon_amd as dmuon
     from dmuon_amd import _C
+    from dmuon_amd.optim.newton_schulz import ns_useful_flops
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -194,32 +323,33 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    model = build_matrix_set(torch, dev, torch.bfloat16, args.layers)
+    with_rest = not args.no_adamw
+    model = build_model(torch, dev, torch.bfloat16, args.layers, with_rest)
     # c5 keeps the bf16 weights as the owner's master (updated in place); --master fp32 runs the
     # reference's default policy instead: fp32 masters, bf16 forward copies published by the
     # update epilogue
     policy = ({"defaults": {"master_dtype": torch.bfloat16}} if args.master == "bf16" else None)
-    dmuon.dedicate_params(model, None, lambda n, p: p.dim() == 2, param_policy=policy)
-    dmuon.replicate(model)
-    from dmuon_amd.optim.newton_schulz import ns_useful_flops
+    dmuon.dedicate_params(model, None, lambda n, p: n.startswith("mats.") and p.dim() == 2,
+                          param_policy=policy)
+    dmuon.replicate(model)                    # embeddings, lm_head, norms -> AdamW
 
     if args.ns == "gram":
         ns = dmuon.NewtonSchulz("gram")                   # Polar-Express, restarts [2]
     else:
         ns = dmuon.NewtonSchulz("direct", coefficients=KELLER)
-    opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=ns,
-                     overlap_staging=args.overlap_staging,
+    opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, adamw_lr=1e-3,
+                     ns_backend=ns, overlap_staging=args.overlap_staging,
                      single_pass_staging=not args.two_pass_staging)
-    n_mats = sum(1 for _ in model.parameters())
-    n_elems = sum(p.numel() for p in model.parameters())
-    flops = sum(ns_useful_flops(*p.shape, 5, ns.backend, ns.restart_iterations)
-                for p in model.parameters())
+    mats = list(model.mats)
+    n_mats = len(mats)
+    n_elems = sum(p.numel() for p in mats)
+    rest_elems = sum(p.numel() for n, p in model.named_parameters() if not n.startswith("mats."))
+    flops = sum(ns_useful_flops(*p.shape, 5, ns.backend, ns.restart_iterations) for p in mats)
 
+    # ---- timed region: exactly K optimizer steps (Muon matrices + AdamW rest) -----------------
     for _ in range(args.warmup):
         opt.step()
     torch.cuda.synchronize()
-
-    # ---- timed region: exactly K optimizer steps ---------------------------------------------
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -270,6 +400,17 @@ def main():
     actual_per_elem = 14.0 if single_pass else 20.0
     pre_actual = n_elems * actual_per_elem * prof_steps
     pre_actual_gbs = pre_actual / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
+    adam = prof["adamw"]
+    adamw = None
+    if with_rest and adam["launches"]:
+        a_ms = adam["ms"] / prof_steps
+        a_gbs = adam["bytes"] / (adam["ms"] * 1e-3) / 1e9
+        adamw = {"ms_per_step": round(a_ms, 3), "params": rest_elems,
+                 "impl": "fused HIP multi-tensor AdamW inside the timed opt.step() "
+                         "(dmuon_adamw_multi; reference muon.py:1857-1916 semantics)",
+                 "roofline": {"bound": "hbm", "achieved": round(a_gbs, 1), "peak": HBM_PEAK_GBS,
+                              "unit": "GB/s", "frac": round(a_gbs / HBM_PEAK_GBS, 4),
+                              "algorithmic_bytes_per_elem": 14}}
 
     # ---- gradient clipping of the same Muon gradients (segmented HIP kernels), reported apart --
     clip = None
@@ -291,52 +432,23 @@ def main():
                 "roofline": {"bound": "hbm", "achieved": round(c_gbs, 1), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(c_gbs / HBM_PEAK_GBS, 4),
                              "algorithmic_bytes_per_elem": 6}}
+    del opt, model, mats
+    torch.cuda.empty_cache()
 
-    # ---- AdamW-routed params of the c5 config (embeddings, lm_head, norms), reported apart ----
-    adamw = None
-    if not args.no_adamw:
-        from torch import nn
+    copy = copy_leg(torch, dev)
 
-        class Rest(nn.Module):
-            def __init__(self):
-                super().__init__()
-                self.embed = nn.Parameter(torch.zeros(128256, 4096, device=dev, dtype=torch.bfloat16))
-                self.lm_head = nn.Parameter(torch.zeros(128256, 4096, device=dev, dtype=torch.bfloat16))
-                self.norms = nn.ParameterList(
-                    [nn.Parameter(torch.ones(4096, device=dev, dtype=torch.bfloat16)) for _ in range(65)])
-                self.proj = nn.Parameter(torch.zeros(256, 256, device=dev, dtype=torch.bfloat16))
-
-        del opt
-        rest = Rest()
-        for p in rest.parameters():
-            p.grad = torch.randn_like(p) * 0.02
-        dmuon.dedicate_params(rest, None, lambda n, p: n == "proj")
-        dmuon.replicate(rest)
-        opt2 = dmuon.Muon(rest, adamw_lr=1e-3)
-        adam_groups = [g for g in opt2.param_groups if not g["use_muon"]]
-
-        def adamw_step():
-            for g in adam_groups:
-                opt2._step_adamw_group(g)
-
-        adamw_step()
-        torch.cuda.synchronize()
-        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a0.record()
-        for _ in range(3):
-            adamw_step()
-        a1.record()
-        torch.cuda.synchronize()
-        a_ms = a0.elapsed_time(a1) / 3
-        a_elems = int(sum(p.numel() for n, p in rest.named_parameters() if n != "proj"))
-        a_bytes = a_elems * 14          # bf16 p, g, exp_avg, exp_avg_sq read; p, m, v written
-        a_gbs = a_bytes / (a_ms * 1e-3) / 1e9
-        adamw = {"ms_per_step": round(a_ms, 3), "params": a_elems,
-                 "impl": "fused HIP multi-tensor AdamW (dmuon_adamw_multi; reference "
-                         "muon.py:1857-1916 semantics)",
-                 "roofline": {"bound": "hbm", "achieved": round(a_gbs, 1), "peak": HBM_PEAK_GBS,
-                              "unit": "GB/s", "frac": round(a_gbs / HBM_PEAK_GBS, 4),
-                              "algorithmic_bytes_per_elem": 14}}
+    configs = None
+    if not args.no_configs:
+        configs = {"c2": dict(config_leg(torch, dmuon, dev, [(4096, 4096)], ns, 100, 3, 20,
+                                         momentum_init=True),
+                              workload="one bf16 4096x4096 matrix, momentum ~N(0, 0.02^2), "
+                                       "100 timed steps")}
+        configs["c3"] = {}
+        for i, shape in enumerate(C3_SHAPES):
+            configs["c3"][f"{shape[0]}x{shape[1]}"] = config_leg(torch, dmuon, dev, [shape], ns,
+                                                                 20, 3, 30 + i)
+        configs["c4"] = dict(config_leg(torch, dmuon, dev, C4_SHAPES, ns, 20, 3, 40),
+                             workload="64 x (1408x2048) + 64 x (2048x1408) bf16 expert matrices")
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget, args.ns)
 
@@ -364,12 +476,15 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic",
-        "config": {"workload": f"Llama-3-8B matrix set: {args.layers} layers x 7 matrices "
-                               f"({n_mats} bf16 matrices, {n_elems / 1e9:.2f} G elements), "
-                               "fp32 momentum, " + (
+        "config": {"workload": f"Llama-3-8B parameter set: {args.layers} layers x 7 matrices "
+                               f"({n_mats} bf16 matrices, {n_elems / 1e9:.2f} G elements) on "
+                               "Muon, fp32 momentum, " + (
                                    "Gram NS (5 Polar-Express steps, restart at 2, fp16 MFMA)"
                                    if args.ns == "gram" else
-                                   "5 direct NS steps (Keller, fp16 MFMA)"),
+                                   "5 direct NS steps (Keller, fp16 MFMA)") + (
+                                   f"; embeddings, lm_head and {LLAMA3_8B_NORMS} norms "
+                                   f"({rest_elems / 1e9:.2f} G bf16 elements) on AdamW in the "
+                                   "same step" if with_rest else "; AdamW params left out"),
                    "ns_backend": args.ns,
                    "matrices": n_mats, "useful_ns_tflop_per_step": round(flops / 1e12, 2),
                    "master": ("bf16 weights updated in place" if args.master == "bf16" else
@@ -378,10 +493,10 @@ def main():
         "ns_tflops": round(flops / (ms_per_step * 1e-3) / 1e12, 1),
         "ns_frac_mfma_peak_step": round(flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "roofline": {
-            "kernel": ("nt_mfma_kernel<..., fp16> (Gram X X^T, R/Z/W triangle products, "
-                       "Q update, restart Q X, final Q X + update)" if args.ns == "gram" else
-                       "nt_mfma_kernel<..., fp16> (SYRK X X^T, SYRK-poly, NS GEMM, final "
-                       "GEMM+update)"),
+            "kernel": ("nt_pp_kernel / nt_mfma_kernel<..., fp16> (Gram X X^T, R/Z/W triangle "
+                       "products, Q update, restart Q X, final Q X + update)" if args.ns == "gram"
+                       else "nt_pp_kernel / nt_mfma_kernel<..., fp16> (SYRK X X^T, SYRK-poly, "
+                            "NS GEMM, final GEMM+update)"),
             "bound": "mfma", "achieved": round(achieved_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved_tf / MFMA_BF16_PEAK_TFLOPS, 4),
             "traffic": traffic,
@@ -400,10 +515,14 @@ def main():
             "algorithmic_bytes_per_elem": 12,
             "actual_bytes_per_elem": actual_per_elem,
             "actual_gbs": None if pre_actual_gbs is None else round(pre_actual_gbs, 1),
+            "copy_gbs": copy["gbs"],
+            "frac_of_copy": None if pre_actual_gbs is None else round(pre_actual_gbs / copy["gbs"], 4),
         },
+        "hbm_copy": copy,
         "kernel_classes": classes,
-        "grad_clip": clip,
         "adamw_rest": adamw,
+        "grad_clip": clip,
+        "configs": configs,
         "cpu_baseline": cpu,
         "wall_s_timed": round(wall, 3),
         "device": torch.cuda.get_device_name(dev),

@@ -103,13 +103,14 @@ struct Tile {
   static constexpr int RPL = 256 / ROWB;          // rows per 256-byte LDS bank line (64 banks)
   static constexpr int A_BYTES = BM * ROWB;
   static constexpr int STAGE = (BM + BN) * ROWB;
-  // epilogue staging per wave, one 32-row slab: row-major pitch EPN (WTN bf16 + 8 B, so the
-  // 32 rows of a lane column fall on distinct banks), transposed pitch EPT (32 bf16 + 16 B), and
+  // epilogue staging per wave: one 32-row slab row-major at pitch EPN (WTN bf16 + 8 B, so the
+  // 32 rows of a lane column fall on distinct banks), two slabs transposed at pitch EPT (64 bf16
+  // + 16 B: the four lane groups of a scatter hit different banks), and
   // the fp32 slab of the final step (32 rows of WTN + 4 floats)
   static constexpr int EPN = WTN * 2 + 8;
-  static constexpr int EPT = 32 * 2 + 16;
+  static constexpr int EPT = 64 * 2 + 16;
   static constexpr int EPF = 32 * (WTN + 4) * 4;
-  static constexpr int EPI_MAX2 = (32 * EPN > WTN * EPT ? 32 * EPN : WTN * EPT);
+  static constexpr int EPI_MAX2 = 32 * EPN + WTN * EPT;
   static constexpr int EPI_REGION_RAW = (EPI_MAX2 > EPF ? EPI_MAX2 : EPF);
   static constexpr int EPI_REGION = (EPI_REGION_RAW + 15) / 16 * 16;
   static constexpr int LDS_BYTES = (S * STAGE > NW * EPI_REGION ? S * STAGE : NW * EPI_REGION);
@@ -281,10 +282,11 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
   if (a.alpha_dev) s *= a.alpha_dev[l];
 
   if constexpr (MODE == EPI_SYM || MODE == EPI_NS) {
-    // Each 32-row slab of the wave tile goes through a small per-wave LDS staging area twice --
-    // row-major for D, then transposed for D^T (NS step) or the mirrored block (SYRK) -- so that
-    // the global stores are row segments (8 B x 16 lanes = 128 B for D, 16 B x 4 lanes = 64 B
-    // for D^T) instead of scattered 2-byte stores.
+    // Each 32-row slab of the wave tile goes through a small per-wave LDS staging area row-major
+    // for D, and pairs of slabs transposed for D^T (NS step) or the mirrored block (SYRK), so
+    // that the global stores are whole 128-byte row segments (8 B x 16 lanes for a D row,
+    // 16 B x 8 lanes for a 64-value D^T row) instead of scattered 2-byte stores.
+    static_assert(Acc::SLABS % 2 == 0, "transposed rows pair the slabs");
     uint16_t* Db = a.D + (long long)l * a.sD;
     uint16_t* DTb = nullptr;
     long long ldt = 0;
@@ -301,6 +303,7 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
       if (a.DT) { DTb = a.DT + (long long)l * a.sDT; ldt = a.lddt; }
     }
     char* reg = smem + wave * T::EPI_REGION;
+    char* regt = reg + 32 * T::EPN;               // [WTN][64] transposed pair of slabs
     // optional second output of a triangle product: D2 = D + diag2 * I (same layout as D; the
     // diagonal only lives in the straddling chunks of diagonal tiles' row path)
     uint16_t* D2b = nullptr;
@@ -368,24 +371,30 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
         }
       }
       if (DTb) {
-        // transposed slab [WTN][32] at pitch EPT; each lane scatters its 4 consecutive j
+        // slab x into columns 32 (x & 1) .. + 31 of the transposed pair; each lane scatters its
+        // 4 consecutive j
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-          uint16_t* col = reinterpret_cast<uint16_t*>(reg + acc.col(q) * T::EPT) + acc.row(q);
+          uint16_t* col = reinterpret_cast<uint16_t*>(regt + acc.col(q) * T::EPT) +
+                          32 * (x & 1) + acc.row(q);
           const u32x2_t p = o2[q];
           col[0] = (uint16_t)(p.x & 0xffff);
           col[T::EPT / 2] = (uint16_t)(p.x >> 16);
           col[T::EPT] = (uint16_t)(p.y & 0xffff);
           col[3 * T::EPT / 2] = (uint16_t)(p.y >> 16);
         }
-        const int cr = lane >> 2, cc = lane & 3;  // 4 lanes x 16 B per 32-value row
-        const long long toff = (long long)(jw + cr) * ldt + iw + 32 * x + 8 * cc;
+      }
+      if (DTb && (x & 1)) {
+        // the pair (slabs x - 1, x): D^T rows j of 64 values i = iw + 32 (x - 1) .. + 63
+        const int cr = lane >> 3, cc = lane & 7;  // 8 lanes x 16 B per 64-value row
+        const int ip = iw + 32 * (x - 1);
+        const long long toff = (long long)(jw + cr) * ldt + ip + 8 * cc;
         uint16_t* dst = DTb + toff;
 #pragma unroll
-        for (int r0 = 0; r0 < T::WTN; r0 += 16) {
-          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(reg + (r0 + cr) * T::EPT + 16 * cc);
+        for (int r0 = 0; r0 < T::WTN; r0 += 8) {
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(regt + (r0 + cr) * T::EPT + 16 * cc);
           // diagonal tile: output row j keeps columns i < j (chunk i0 .. i0+7)
-          const int dj = jw + r0 + cr, di = iw + 32 * x + 8 * cc;
+          const int dj = jw + r0 + cr, di = ip + 8 * cc;
           if (!diag || di + 7 < dj) {
             __builtin_nontemporal_store(v,
                                         reinterpret_cast<u32x4_t*>(dst + (long long)r0 * ldt));

@@ -93,23 +93,35 @@ def fma_f32(a, b, c) -> np.ndarray:
     a vector FMA. The product of two fp32 values is exact in fp64; the fp64 sum is corrected
     with its exact TwoSum error where it lands on an fp32 rounding tie (the only case in which
     rounding fp64 -> fp32 twice could differ from rounding once)."""
-    a64 = np.asarray(a, np.float32).astype(np.float64)
-    b64 = np.asarray(b, np.float32).astype(np.float64)
-    c64 = np.asarray(c, np.float32).astype(np.float64)
+    a64, b64, c64 = np.broadcast_arrays(np.asarray(a, np.float32).astype(np.float64),
+                                        np.asarray(b, np.float32).astype(np.float64),
+                                        np.asarray(c, np.float32).astype(np.float64))
+    shape = a64.shape
+    a64, b64, c64 = (np.atleast_1d(x) for x in (a64, b64, c64))
     p = a64 * b64
     s = p + c64
-    bv = s - p
-    e = (p - (s - bv)) + (c64 - bv)            # s + e == p + c exactly
     with np.errstate(invalid="ignore", over="ignore"):
-        r = np.asarray(s.astype(np.float32))
-        up = np.nextafter(r, np.float32(np.inf))
-        dn = np.nextafter(r, np.float32(-np.inf))
-        r64 = r.astype(np.float64)
-        mid_up = (r64 + up.astype(np.float64)) * 0.5
-        mid_dn = (r64 + dn.astype(np.float64)) * 0.5
-    r = np.where((s == mid_up) & (e > 0), up, r)
-    r = np.where((s == mid_dn) & (e < 0), dn, r)
-    return np.asarray(r, dtype=np.float32)
+        r = np.array(s.astype(np.float32))
+    # candidates: s exactly halfway between two fp32 values (the 29 fp64 mantissa bits below
+    # an fp32 of normal range read 1000...0), or s in fp32's subnormal range; elsewhere the
+    # single rounding of s is the rounding of p + c
+    cand = ((s.view(np.uint64) & np.uint64(0x1FFFFFFF)) == np.uint64(0x10000000)) | \
+        (np.abs(s) < 2.0 ** -126)
+    idx = np.nonzero(cand)
+    if idx[0].size:
+        ps, cs, ss, rs = p[idx], c64[idx], s[idx], r[idx]
+        bv = ss - ps
+        e = (ps - (ss - bv)) + (cs - bv)        # ss + e == ps + cs exactly
+        with np.errstate(invalid="ignore", over="ignore"):
+            up = np.nextafter(rs, np.float32(np.inf))
+            dn = np.nextafter(rs, np.float32(-np.inf))
+            r64 = rs.astype(np.float64)
+            mid_up = (r64 + up.astype(np.float64)) * 0.5
+            mid_dn = (r64 + dn.astype(np.float64)) * 0.5
+        rs = np.where((ss == mid_up) & (e > 0), up, rs)
+        rs = np.where((ss == mid_dn) & (e < 0), dn, rs)
+        r[idx] = rs
+    return np.asarray(r, dtype=np.float32).reshape(shape)
 
 
 def _mm(a: np.ndarray, b: np.ndarray, dtype: str) -> np.ndarray:
