@@ -61,18 +61,20 @@ _SIGNATURES = {
     "dmuon_ns_plan": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(c_int),
                               ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_i64)]),
     "dmuon_muon_step_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_int, c_int,
-                                      c_int, c_int, c_d, c_d, c_d, c_int, c_int, c_fp, c_int,
-                                      c_int, c_ip, c_int, c_f, c_vp, c_i64, c_int, c_vp]),
+                                      c_int, c_int, c_int, c_d, c_d, c_d, c_int, c_int, c_fp,
+                                      c_int, c_int, c_ip, c_int, c_f, c_vp, c_i64, c_int, c_vp]),
     "dmuon_muon_step_group_noalloc": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_int,
-                                              c_int, c_int, c_int, c_d, c_d, c_d, c_int, c_int,
-                                              c_fp, c_int, c_int, c_ip, c_int, c_f, c_int, c_vp]),
-    "dmuon_muon_stage_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_d, c_int,
-                                       c_int, c_int, c_f, c_vp, c_i64, c_int, c_vp]),
-    "dmuon_muon_apply_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_d, c_d,
-                                       c_fp, c_int, c_int, c_ip, c_int, c_vp, c_i64, c_int, c_vp]),
-    "dmuon_newton_schulz_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_fp,
-                                          c_int, c_int, c_ip, c_int, c_f, c_vp, c_i64, c_int,
-                                          c_vp]),
+                                              c_int, c_int, c_int, c_int, c_d, c_d, c_d, c_int,
+                                              c_int, c_fp, c_int, c_int, c_ip, c_int, c_f, c_int,
+                                              c_vp]),
+    "dmuon_muon_stage_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int, c_d,
+                                       c_int, c_int, c_int, c_f, c_vp, c_i64, c_int, c_vp]),
+    "dmuon_muon_apply_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int, c_d,
+                                       c_d, c_fp, c_int, c_int, c_ip, c_int, c_vp, c_i64, c_int,
+                                       c_vp]),
+    "dmuon_newton_schulz_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int,
+                                          c_fp, c_int, c_int, c_ip, c_int, c_f, c_vp, c_i64,
+                                          c_int, c_vp]),
     "dmuon_adamw_multi": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_i64, c_int, c_int,
                                   c_int, c_int, c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_f, c_vp]),
     "dmuon_segmented_l2_norm_sq": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp,

@@ -190,6 +190,7 @@ int plan(int rows, int cols, int batch, int tile_req, int num_cus, int gram, int
 // X carries KX = 2^12 throughout, the first R (eigenvalues ~1/m) carries kr = 2^floor(log2 m)
 // (at most 2^12) until its first update; all scale changes are folded into alpha / beta.
 int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, int batch, bool tall,
+             int n_flip,
              const float* coeffs, int T, const int* restarts, int n_restarts,
              void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype,
              void* const* out_ptrs, int out_dtype, float decay, float lrs, double syrk_flops,
@@ -268,7 +269,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;
     g.w_ptrs = w_ptrs; g.w_dtype = w_dtype; g.decay = decay; g.lrs = lrs;
     g.pub_ptrs = pub_ptrs; g.pub_dtype = pub_dtype;
-    g.m_real = m; g.n_real = n; g.transposed = tall ? 1 : 0;
+    g.m_real = m; g.n_real = n; g.transposed = tall ? 1 : 0; g.n_flip = n_flip;
     return timed(PC_FINAL, gemm_flops, final_bytes, stream, who,
                  [&] { return launch_nt(g, tile, stream); });
   };
@@ -344,7 +345,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
 enum { PH_STAGE = 1, PH_APPLY = 2 };
 int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* const* est_ptrs,
               void* const* w_ptrs, int w_dtype, void* const* pub_ptrs, int pub_dtype, void* const* out_ptrs,
-              int out_dtype, int rows, int cols, int batch,
+              int out_dtype, int rows, int cols, int batch, int n_t,
               float mu, int nesterov, int first_step, float decay, float lrs, const float* coeffs,
               int T, int backend, const int* restarts, int n_restarts, float eps, void* workspace,
               int64_t workspace_bytes, int tile_req, hipStream_t stream, const char* who,
@@ -370,6 +371,8 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   }
   if (backend != DMUON_NS_DIRECT && backend != DMUON_NS_GRAM)
     return fail("%s: unknown NS backend %d", who, backend);
+  if (n_t < 0 || n_t > batch)
+    return fail("%s: n_transposed=%d outside [0, batch=%d]", who, n_t, batch);
   const int gram = backend == DMUON_NS_GRAM;
   if (!workspace || !aligned16(workspace)) return fail("%s: workspace NULL or misaligned", who);
   int tile, m_pad, n_pad;
@@ -384,26 +387,41 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   Workspace w = carve(static_cast<char*>(workspace), m_pad, n_pad, Rp, Cp, batch, gram);
   const long long xs = (long long)m_pad * n_pad, as = (long long)m_pad * m_pad;
 
-  PreArgs p{};
-  p.g_ptrs = g_ptrs;
-  p.g_dtype = g_dtype;
-  p.buf_ptrs = buf_ptrs;
-  p.Y = tall ? w.XT0 : w.X;
-  p.ldy = tall ? m_pad : n_pad;
-  p.sY = xs;
-  p.YT = tall ? w.X : w.XT0;
-  p.ldyt = tall ? n_pad : m_pad;
-  p.sYT = xs;
-  p.partials = w.partials;
-  p.rows = rows;
-  p.cols = cols;
-  p.Rp = Rp;
-  p.Cp = Cp;
-  p.L = batch;
-  p.mu = mu;
-  p.first_step = first_step;
-  p.nesterov = nesterov;
-  p.stage = PRE_NORM;
+  (void)Rp; (void)Cp;
+  // The group's matrices share the m x n NS shape: [0, batch - n_t) are rows x cols and the last
+  // n_t are cols x rows (their transposes). Each orientation is staged by its own launch into
+  // its slice of the workspace; everything after the staging sees one m x n batch, and the final
+  // epilogue writes each matrix back in its own orientation. (Square shapes have one
+  // orientation: the n_t part is staged and written like the rest.)
+  const int n_flip = rows == cols ? 0 : n_t;
+  auto pre_args = [&](int part) {
+    const int l0 = part == 0 ? 0 : batch - n_t;
+    const int r_ = part == 0 ? rows : cols, c_ = part == 0 ? cols : rows;
+    const bool tall_ = r_ > c_;
+    PreArgs q{};
+    q.g_ptrs = g_ptrs ? g_ptrs + l0 : nullptr;
+    q.g_dtype = g_dtype;
+    q.buf_ptrs = buf_ptrs ? buf_ptrs + l0 : nullptr;
+    q.est_ptrs = est_ptrs ? est_ptrs + l0 : nullptr;
+    q.Y = (tall_ ? w.XT0 : w.X) + l0 * xs;
+    q.ldy = tall_ ? m_pad : n_pad;
+    q.sY = xs;
+    q.YT = (tall_ ? w.X : w.XT0) + l0 * xs;
+    q.ldyt = tall_ ? n_pad : m_pad;
+    q.sYT = xs;
+    q.partials = w.partials + (long long)l0 * w.nparts;
+    q.rows = r_;
+    q.cols = c_;
+    q.Rp = tall_ ? n_pad : m_pad;
+    q.Cp = tall_ ? m_pad : n_pad;
+    q.L = part == 0 ? batch - n_t : n_t;
+    q.mu = mu;
+    q.first_step = first_step;
+    q.nesterov = nesterov;
+    q.kx = kNsKx;
+    q.scale = w.scale + l0;
+    return q;
+  };
   const double Ld = batch, md = m, nd = n, elems = (double)rows * cols * batch;
   const double gbytes = g_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0;
   if (do_stage) {
@@ -418,21 +436,25 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   // which then stages exactly as without an estimate.
   const bool est = est_ptrs != nullptr;
   const double mom_bytes = buf_ptrs ? (first_step ? 4.0 : 8.0) : 0.0;
-  const double pre_bytes = elems * (gbytes + mom_bytes + (est ? 2.0 : 0.0));
-  p.stage = est ? PRE_EST : PRE_NORM;
-  p.est_ptrs = est_ptrs;
-  p.kx = kNsKx;
-  if (timed(PC_PRE, 0.0, pre_bytes, stream, who, [&] { return launch_pre(p, stream); })) return 1;
+  for (int part = 0; part < 2; ++part) {
+    PreArgs p = pre_args(part);
+    if (p.L == 0) continue;
+    p.stage = est ? PRE_EST : PRE_NORM;
+    const double pre_bytes = elems * p.L / batch * (gbytes + mom_bytes + (est ? 2.0 : 0.0));
+    if (timed(PC_PRE, 0.0, pre_bytes, stream, who, [&] { return launch_pre(p, stream); }))
+      return 1;
+  }
   if (timed(PC_NORM, 0.0, (double)batch * w.nparts * 4, stream, who, [&] {
         return launch_norm_finalize_est(w.partials, w.nparts, batch, eps, w.scale, w.scale_sq,
                                         est_ptrs, w.ratio, w.ratio_sq, w.restage, stream);
       }))
     return 1;
-  {
+  for (int part = 0; part < 2; ++part) {
+    PreArgs p = pre_args(part);
+    if (p.L == 0) continue;
     p.stage = PRE_F16;
-    p.scale = w.scale;
-    p.restage = est ? w.restage : nullptr;
-    const double st_bytes = est ? 0.0 : elems * 2.0;
+    p.restage = est ? w.restage + (part == 0 ? 0 : batch - n_t) : nullptr;
+    const double st_bytes = est ? 0.0 : elems * p.L / batch * 2.0;
     if (timed(PC_PRE, 0.0, st_bytes, stream, who, [&] { return launch_pre(p, stream); }))
       return 1;
   }
@@ -447,7 +469,8 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   uint16_t* xt_cur = w.XT0;
   uint16_t* xt_nxt = w.XT1;
   if (gram)
-    return run_gram(w, m, n, m_pad, n_pad, tile, batch, tall, coeffs, T, restarts, n_restarts,
+    return run_gram(w, m, n, m_pad, n_pad, tile, batch, tall, n_flip, coeffs, T, restarts,
+                    n_restarts,
                     w_ptrs, w_dtype, pub_ptrs, pub_dtype, out_ptrs, out_dtype, decay, lrs,
                     syrk_flops, poly_flops, gemm_flops, wbytes + obytes + pbytes, stream, who);
   // Direct NS on the same fp16 operands as the Gram form: X carries the power-of-two scale
@@ -506,7 +529,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
       g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;
       g.w_ptrs = w_ptrs; g.w_dtype = w_dtype; g.decay = decay; g.lrs = lrs;
       g.pub_ptrs = pub_ptrs; g.pub_dtype = pub_dtype;
-      g.m_real = m; g.n_real = n; g.transposed = tall ? 1 : 0;
+      g.m_real = m; g.n_real = n; g.transposed = tall ? 1 : 0; g.n_flip = n_flip;
       if (timed(PC_FINAL, gemm_flops, wbytes + obytes + pbytes, stream, who,
                 [&] { return launch_nt(g, tile, stream); }))
         return 1;
@@ -1031,7 +1054,8 @@ int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int 
 int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
                           float* const* est_ptrs, void* const* w_ptrs, int w_dtype,
                           void* const* pub_ptrs, int pub_dtype, int rows, int cols, int batch,
-                          double lr, double mu, double wd, int nesterov, int first_step,
+                          int n_transposed, double lr, double mu, double wd, int nesterov,
+                          int first_step,
                           const float* coeffs, int T, int backend, const int* restarts,
                           int n_restarts, float eps, void* workspace, int64_t workspace_bytes,
                           int tile, void* stream) {
@@ -1043,16 +1067,16 @@ int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_pt
   const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
   const float lrs = (float)(lr * scale);
   return run_group(g_ptrs, g_dtype, buf_ptrs, est_ptrs, w_ptrs, w_dtype, pub_ptrs, pub_dtype,
-                   nullptr, 0, rows, cols, batch, (float)mu, nesterov, first_step, decay, lrs,
-                   coeffs, T,
-                   backend, restarts, n_restarts, eps, workspace, workspace_bytes, tile,
+                   nullptr, 0, rows, cols, batch, n_transposed, (float)mu, nesterov, first_step,
+                   decay, lrs, coeffs, T, backend, restarts, n_restarts, eps, workspace, workspace_bytes, tile,
                    static_cast<hipStream_t>(stream), who);
 }
 
 int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
                                   float* const* est_ptrs, void* const* w_ptrs, int w_dtype,
                                   void* const* pub_ptrs, int pub_dtype, int rows, int cols,
-                                  int batch, double lr, double mu, double wd, int nesterov,
+                                  int batch, int n_transposed, double lr, double mu, double wd,
+                                  int nesterov,
                                   int first_step, const float* coeffs, int T, int backend,
                                   const int* restarts, int n_restarts, float eps, int tile,
                                   void* stream) {
@@ -1075,40 +1099,43 @@ int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const
   const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
   const float lrs = (float)(lr * scale);
   return run_group(g_ptrs, g_dtype, buf_ptrs, est_ptrs, w_ptrs, w_dtype, pub_ptrs, pub_dtype,
-                   nullptr, 0, rows, cols, batch, (float)mu, nesterov, first_step, decay, lrs,
-                   coeffs, T, backend, restarts, n_restarts, eps, ws, kScratchBytes, tile,
+                   nullptr, 0, rows, cols, batch, n_transposed, (float)mu, nesterov, first_step,
+                   decay, lrs, coeffs, T, backend, restarts, n_restarts, eps, ws, kScratchBytes, tile,
                    static_cast<hipStream_t>(stream), who);
 }
 
 int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,
-                              int out_dtype, int rows, int cols, int batch, const float* coeffs,
+                              int out_dtype, int rows, int cols, int batch, int n_transposed,
+                              const float* coeffs,
                               int T, int backend, const int* restarts, int n_restarts, float eps,
                               void* workspace, int64_t workspace_bytes, int tile, void* stream) {
   const char* who = "dmuon_newton_schulz_group";
   if (batch == 0) return 0;
   if (!out_ptrs) return fail("%s: out_ptrs must be non-NULL", who);
   return run_group(g_ptrs, g_dtype, nullptr, nullptr, nullptr, 0, nullptr, 0, out_ptrs, out_dtype,
-                   rows,
-                   cols, batch, 0.f, 0, 1, 1.f, 0.f, coeffs, T, backend, restarts, n_restarts,
-                   eps, workspace, workspace_bytes, tile,
+                   rows, cols, batch, n_transposed, 0.f, 0, 1, 1.f, 0.f, coeffs, T, backend,
+                   restarts, n_restarts, eps, workspace, workspace_bytes, tile,
                    static_cast<hipStream_t>(stream), who);
 }
 
 int dmuon_muon_stage_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
-                           float* const* est_ptrs, int rows, int cols, int batch, double mu, int nesterov, int first_step,
+                           float* const* est_ptrs, int rows, int cols, int batch,
+                           int n_transposed, double mu, int nesterov, int first_step,
                            int backend, float eps, void* workspace, int64_t workspace_bytes,
                            int tile, void* stream) {
   const char* who = "dmuon_muon_stage_group";
   if (batch == 0) return 0;
   if (!buf_ptrs) return fail("%s: buf_ptrs must be non-NULL", who);
   return run_group(g_ptrs, g_dtype, buf_ptrs, est_ptrs, nullptr, 0, nullptr, 0, nullptr, 0, rows,
-                   cols, batch, (float)mu, nesterov, first_step, 1.f, 0.f, nullptr, 0, backend,
+                   cols, batch, n_transposed, (float)mu, nesterov, first_step, 1.f, 0.f, nullptr,
+                   0, backend,
                    nullptr, 0, eps, workspace, workspace_bytes, tile,
                    static_cast<hipStream_t>(stream), who, PH_STAGE);
 }
 
 int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_ptrs,
-                           int pub_dtype, int rows, int cols, int batch, double lr, double wd,
+                           int pub_dtype, int rows, int cols, int batch, int n_transposed,
+                           double lr, double wd,
                            const float* coeffs, int T, int backend, const int* restarts,
                            int n_restarts, void* workspace, int64_t workspace_bytes, int tile,
                            void* stream) {
@@ -1119,9 +1146,8 @@ int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_pt
   const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
   const float lrs = (float)(lr * scale);
   return run_group(nullptr, 0, nullptr, nullptr, w_ptrs, w_dtype, pub_ptrs, pub_dtype, nullptr, 0,
-                   rows,
-                   cols, batch, 0.f, 0, 0, decay, lrs, coeffs, T, backend, restarts, n_restarts,
-                   0.f, workspace, workspace_bytes, tile, static_cast<hipStream_t>(stream), who,
+                   rows, cols, batch, n_transposed, 0.f, 0, 0, decay, lrs, coeffs, T, backend,
+                   restarts, n_restarts, 0.f, workspace, workspace_bytes, tile, static_cast<hipStream_t>(stream), who,
                    PH_APPLY);
 }
 

@@ -36,6 +36,7 @@ struct NtArgs {
   void* const* pub_ptrs; int pub_dtype;   // EPI_FINAL: optional forward copies of the new W
   float decay, lrs;                       // W <- round(W*decay) - lrs*U   (decay==1: no decay rounding)
   int m_real, n_real, transposed;         // true NS dims; transposed: original = X^T (n_real x m_real)
+  int n_flip;                             // the last n_flip matrices take the other orientation
   int elt;                                // ELT_BF16 / ELT_F16 (A, B, C, D, DT)
   int sym_exact;                          // EPI_SYM + tri: diagonal tiles stored exactly symmetric
   uint16_t* D2; float diag2;              // EPI_SYM + tri + sym_exact: also D2 = D + diag2 * I

@@ -424,7 +424,9 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
     void* outp = a.out_ptrs ? a.out_ptrs[l] : nullptr;
     void* wp = a.w_ptrs ? a.w_ptrs[l] : nullptr;
     void* pp = (wp && a.pub_ptrs) ? a.pub_ptrs[l] : nullptr;   // forward copy of the new W
-    const long long pitch = a.transposed ? a.m_real : a.n_real;
+    // the last n_flip matrices of the batch are stored in the other orientation
+    const bool tr = (a.transposed != 0) != (l >= a.L - a.n_flip);
+    const long long pitch = tr ? a.m_real : a.n_real;
     // 16-byte vectors need 16-byte aligned bases (torch allocations are; views may not be)
     const bool valign = ((reinterpret_cast<uintptr_t>(wp) | reinterpret_cast<uintptr_t>(outp) |
                           reinterpret_cast<uintptr_t>(pp)) & 15) == 0;
@@ -462,7 +464,7 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
         const int idx = v * 64 + lane;
-        if (!a.transposed) {
+        if (!tr) {
           vr[v] = idx / (T::WTN / 8);
           vc[v] = (idx % (T::WTN / 8)) * 8;
           const int i = ibase + vr[v], j = jw + vc[v];
@@ -490,7 +492,7 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
         float u[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t)
-          u[t] = a.transposed ? slab[(vr[v] + t) * kLd + vc[v]] : slab[vr[v] * kLd + vc[v] + t];
+          u[t] = tr ? slab[(vr[v] + t) * kLd + vc[v]] : slab[vr[v] * kLd + vc[v] + t];
         if (vfull[v]) {
           if (outp) {
             if (a.out_dtype == DT_F32) {
@@ -564,11 +566,11 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
           // from the slab, so the unrolled slab loop around it stays small)
 #pragma unroll 1
           for (int t = 0; t < 8; ++t) {
-            const int i = ibase + vr[v] + (a.transposed ? t : 0);
-            const int j = jw + vc[v] + (a.transposed ? 0 : t);
+            const int i = ibase + vr[v] + (tr ? t : 0);
+            const int j = jw + vc[v] + (tr ? 0 : t);
             if (i >= a.m_real || j >= a.n_real) continue;
-            const long long off = a.transposed ? (long long)j * pitch + i : (long long)i * pitch + j;
-            const float ut = a.transposed ? slab[(vr[v] + t) * kLd + vc[v]]
+            const long long off = tr ? (long long)j * pitch + i : (long long)i * pitch + j;
+            const float ut = tr ? slab[(vr[v] + t) * kLd + vc[v]]
                                           : slab[vr[v] * kLd + vc[v] + t];
             if (outp) {
               if (a.out_dtype == DT_F32) static_cast<float*>(outp)[off] = ut;

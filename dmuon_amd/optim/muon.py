@@ -275,6 +275,11 @@ class Muon(torch.optim.Optimizer):
         return prof
 
     def _buckets(self, group) -> "OrderedDict[tuple, list]":
+        """Owned params with a gradient, grouped by their oriented NS shape (m, n) =
+        (min, max) of (rows, cols) and the dtypes the kernels specialise on: a matrix and its
+        transpose share every NS product. Each bucket lists (dp, grad, (rows, cols)), the
+        params stored m x n first and the transposed (n x m) ones after them, which is the
+        order the group entry points take (their last ``n_transposed`` members)."""
         buckets: OrderedDict[tuple, list] = OrderedDict()
         for p in group["params"]:
             dp = self._dp_by_param.get(id(p))
@@ -288,9 +293,11 @@ class Muon(torch.optim.Optimizer):
             rows = p.shape[0]
             cols = p.numel() // rows
             pub = dp.publish_target()
-            key = (rows, cols, g.dtype, dp._owned_data.dtype,
+            key = (min(rows, cols), max(rows, cols), g.dtype, dp._owned_data.dtype,
                    None if pub is None else pub.dtype, g.device, first)
-            buckets.setdefault(key, []).append((dp, g))
+            buckets.setdefault(key, []).append((dp, g, (rows, cols)))
+        for items in buckets.values():
+            items.sort(key=lambda it: it[2][0] > it[2][1])   # stable: m x n first
         return buckets
 
     def _step_muon_group(self, group) -> tuple[int, int]:
@@ -315,14 +322,15 @@ class Muon(torch.optim.Optimizer):
             for size in self._chunk_sizes(rows, cols, len(items), num_cus, backend):
                 part = items[s0:s0 + size]
                 s0 += size
-                for dp, _ in part:
+                n_t = sum(1 for _, _, shape in part if shape[0] != rows)
+                for dp, _, shape in part:
                     st = self.state[id(dp)]
                     if "momentum_buffer" not in st:
-                        st["momentum_buffer"] = torch.zeros((rows, cols), dtype=torch.float32,
+                        st["momentum_buffer"] = torch.zeros(shape, dtype=torch.float32,
                                                             device=dev)
                     else:
                         st["momentum_buffer"] = _state_tensor(
-                            st["momentum_buffer"], (rows, cols), dev, torch.float32,
+                            st["momentum_buffer"], shape, dev, torch.float32,
                             "momentum_buffer", dp.param_name)
                     if self._single_pass:
                         sc = st.get("ns_scale")
@@ -335,19 +343,19 @@ class Muon(torch.optim.Optimizer):
                     if not dp._owned_data.is_contiguous():
                         raise RuntimeError(f"{dp.param_name}: Muon needs a contiguous weight")
                 tile, _, _, nbytes = _C.plan(rows, cols, len(part), 0, num_cus, backend)
-                chunks.append((rows, cols, dev, first, pdt is not None, part, tile, nbytes))
+                chunks.append((rows, cols, n_t, dev, first, pdt is not None, part, tile, nbytes))
                 count += len(part)
                 numel += len(part) * rows * cols
         if not chunks:
             return 0, 0
-        dev = chunks[0][2]
+        dev = chunks[0][3]
         main = torch.cuda.current_stream(dev)
         overlap = self._overlap_staging and len(chunks) > 1
         side = self._side_stream(dev) if overlap else main
         # both workspaces exist before the hand-over event, so no block the side stream writes
         # can still be in use by later work on `main`
         nslots = 2 if overlap else 1
-        wss = [self._get_workspace(dev, max(c[7] for k, c in enumerate(chunks)
+        wss = [self._get_workspace(dev, max(c[8] for k, c in enumerate(chunks)
                                             if k % nslots == sl), sl)
                for sl in range(min(nslots, len(chunks)))]
         if overlap:
@@ -355,7 +363,7 @@ class Muon(torch.optim.Optimizer):
             start.record(main)           # gradients, buffers and weights are ready on `main`
             side.wait_event(start)
         free = [None, None]
-        for k, (rows, cols, dev, first, has_pub, part, tile, nbytes) in enumerate(chunks):
+        for k, (rows, cols, n_t, dev, first, has_pub, part, tile, nbytes) in enumerate(chunks):
             slot = k % nslots
             ws = wss[slot]
             L = len(part)
@@ -363,37 +371,37 @@ class Muon(torch.optim.Optimizer):
                 if free[slot] is not None:
                     side.wait_event(free[slot])
                 # contiguous copies (if any) on the staging stream, ordered before the staging
-                gs = [g if g.is_contiguous() else g.contiguous() for _, g in part]
-                ests = ([self.state[id(dp)]["ns_scale"].data_ptr() for dp, _ in part]
+                gs = [g if g.is_contiguous() else g.contiguous() for _, g, _ in part]
+                ests = ([self.state[id(dp)]["ns_scale"].data_ptr() for dp, _, _ in part]
                         if self._single_pass else [])
                 ptrs = _pinned_ptrs([t.data_ptr() for t in gs]
                                     + [self.state[id(dp)]["momentum_buffer"].data_ptr()
-                                       for dp, _ in part] + ests, dev)
+                                       for dp, _, _ in part] + ests, dev)
                 _C.call("dmuon_muon_stage_group", ptrs.data_ptr(), _float_dtype_code(gs[0]),
                         ptrs.data_ptr() + 8 * L,
-                        ptrs.data_ptr() + 16 * L if ests else None, rows, cols, L, mu,
-                        int(self._nesterov),
-                        int(first), backend, self._ns_eps, ws.data_ptr(), ws.numel(), tile,
+                        ptrs.data_ptr() + 16 * L if ests else None, rows, cols, L, n_t, mu,
+                        int(self._nesterov), int(first), backend, self._ns_eps, ws.data_ptr(), ws.numel(), tile,
                         side.cuda_stream)
                 if overlap:
                     staged = torch.cuda.Event()
                     staged.record(side)
             if overlap:
                 main.wait_event(staged)
-            W = [dp._owned_data for dp, _ in part]
-            pubs = [dp.publish_target() for dp, _ in part] if has_pub else []
+            W = [dp._owned_data for dp, _, _ in part]
+            pubs = [dp.publish_target() for dp, _, _ in part] if has_pub else []
             wptrs = _pinned_ptrs([t.data_ptr() for t in W] + [t.data_ptr() for t in pubs], dev)
             # the forward copies (master != parameter) are written by the same epilogue
             _C.call("dmuon_muon_apply_group", wptrs.data_ptr(), _float_dtype_code(W[0]),
                     wptrs.data_ptr() + 8 * L if pubs else None,
-                    _float_dtype_code(pubs[0]) if pubs else 0, rows, cols, L, lr, wd, coeffs, T,
+                    _float_dtype_code(pubs[0]) if pubs else 0, rows, cols, L, n_t, lr, wd,
+                    coeffs, T,
                     backend, rst, n_rst, ws.data_ptr(), ws.numel(), tile, main.cuda_stream)
             if overlap:
                 done = torch.cuda.Event()
                 done.record(main)
                 free[slot] = done
-        for _, _, _, _, _, part, _, _ in chunks:
-            for dp, _ in part:
+        for c in chunks:
+            for dp, _, _ in c[6]:
                 dp._reduced_grad = None
         return count, numel
 

@@ -194,7 +194,7 @@ def newton_schulz_batched(
     op = _ptr_array(outs, G0.device)
     stream = torch.cuda.current_stream(G0.device).cuda_stream
     _C.call("dmuon_newton_schulz_group", gp.data_ptr(), _float_dtype_code(ins[0]), op.data_ptr(),
-            _float_dtype_code(outs[0]), rows, cols, L, coeff, T, code, rst, n_rst, float(eps),
+            _float_dtype_code(outs[0]), rows, cols, L, 0, coeff, T, code, rst, n_rst, float(eps),
             ws.data_ptr(), ws.numel(), t, stream)
     if out is None and G0.dtype != work_dtype:
         return [o.to(G0.dtype) for o in outs]

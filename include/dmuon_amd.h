@@ -72,7 +72,7 @@ extern "C" {
 const char* dmuon_last_error(void);
 
 /* ABI version (major*100 + minor): DMUON_ABI_VERSION of the header the library was built with. */
-#define DMUON_ABI_VERSION 104
+#define DMUON_ABI_VERSION 105
 int dmuon_abi_version(void);
 
 /*
@@ -209,7 +209,11 @@ int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int 
                   int* tile, int* m_pad, int* n_pad, int64_t* workspace_bytes);
 
 /*
- * Full Muon update for `batch` same-shape rows x cols params (one owner's group):
+ * Full Muon update for `batch` params of one oriented NS shape (one owner's group): the first
+ * batch - n_transposed are rows x cols, the last n_transposed are cols x rows (their momentum
+ * buffers, weights and forward copies too). Both orientations share the m x n NS products
+ * (m = min(rows, cols)); each param's update is written in its own orientation. Square shapes
+ * ignore the split. Steps:
  *   momentum (+Nesterov), normalise, T Newton-Schulz steps with per-step coefficients
  *   coeffs[3*t .. 3*t+2] = (a, b, c) (HOST array), then
  *   W <- round(W*(1 - lr*wd)) - lr*0.2*sqrt(max(rows, cols)) * U    (decay skipped if wd <= 0)
@@ -234,10 +238,10 @@ int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int 
 int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
                           float* const* est_ptrs, void* const* w_ptrs, int w_dtype,
                           void* const* pub_ptrs, int pub_dtype, int rows, int cols, int batch,
-                          double lr, double mu, double wd, int nesterov, int first_step,
-                          const float* coeffs, int T, int backend, const int* restarts,
-                          int n_restarts, float eps, void* workspace, int64_t workspace_bytes,
-                          int tile, void* stream);
+                          int n_transposed, double lr, double mu, double wd, int nesterov,
+                          int first_step, const float* coeffs, int T, int backend,
+                          const int* restarts, int n_restarts, float eps, void* workspace,
+                          int64_t workspace_bytes, int tile, void* stream);
 
 /*
  * dmuon_muon_step_group in two halves, for callers that overlap the bandwidth-bound half of one
@@ -247,18 +251,19 @@ int dmuon_muon_step_group(void* const* g_ptrs, int g_dtype, float* const* buf_pt
  *          written into `workspace`;
  *   apply: the NS products from that staged workspace and the fused weight update (+ optional
  *          forward copy), as dmuon_muon_step_group's second half.
- * Both calls of one group must pass the same rows, cols, batch, backend, tile and workspace; the
- * workspace must not be staged again before its apply has run. Results equal
+ * Both calls of one group must pass the same rows, cols, batch, n_transposed, backend, tile and
+ * workspace; the workspace must not be staged again before its apply has run. Results equal
  * dmuon_muon_step_group's bit for bit. No reference counterpart (the reference runs the step
  * per parameter on one stream); it serves the same seam, muon.py:1683-1740.
  */
 int dmuon_muon_stage_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
-                           float* const* est_ptrs, int rows, int cols, int batch, double mu,
-                           int nesterov, int first_step, int backend, float eps, void* workspace,
-                           int64_t workspace_bytes, int tile, void* stream);
+                           float* const* est_ptrs, int rows, int cols, int batch,
+                           int n_transposed, double mu, int nesterov, int first_step,
+                           int backend, float eps, void* workspace, int64_t workspace_bytes,
+                           int tile, void* stream);
 int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_ptrs,
-                           int pub_dtype, int rows, int cols, int batch, double lr, double wd,
-                           const float* coeffs, int T, int backend, const int* restarts,
+                           int pub_dtype, int rows, int cols, int batch, int n_transposed,
+                           double lr, double wd, const float* coeffs, int T, int backend, const int* restarts,
                            int n_restarts, void* workspace, int64_t workspace_bytes, int tile,
                            void* stream);
 
@@ -279,15 +284,16 @@ int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_pt
 int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
                                   float* const* est_ptrs, void* const* w_ptrs, int w_dtype,
                                   void* const* pub_ptrs, int pub_dtype, int rows, int cols,
-                                  int batch, double lr, double mu, double wd, int nesterov,
-                                  int first_step, const float* coeffs, int T, int backend,
+                                  int batch, int n_transposed, double lr, double mu, double wd,
+                                  int nesterov, int first_step, const float* coeffs, int T, int backend,
                                   const int* restarts, int n_restarts, float eps, int tile,
                                   void* stream);
 
-/* direct_newton_schulz / gram_newton_schulz (by `backend`, as above) for `batch` same-shape
- * rows x cols matrices: out[l] <- NS(g[l]). */
+/* direct_newton_schulz / gram_newton_schulz (by `backend`, as above) for `batch` matrices of one
+ * oriented shape (the last n_transposed are cols x rows, as above): out[l] <- NS(g[l]). */
 int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,
-                              int out_dtype, int rows, int cols, int batch, const float* coeffs,
+                              int out_dtype, int rows, int cols, int batch, int n_transposed,
+                              const float* coeffs,
                               int T, int backend, const int* restarts, int n_restarts, float eps,
                               void* workspace, int64_t workspace_bytes, int tile, void* stream);
 

@@ -87,37 +87,27 @@ def test_group_validation_without_gpu():
     lib = _C.lib()
     coeff = (ctypes.c_float * 15)(*([3.4445, -4.7750, 2.0315] * 5))
     p = ctypes.c_void_p(4096)
-    # workspace too small
-    msg = _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1, 0.02, 0.95, 0.0,
-                                         1, 1, coeff, 5, 0, None, 0, 1e-7, p, 16, 0, None))
-    assert "workspace" in msg
-    # unsupported dtype code
-    assert "dtype" in _err(lib.dmuon_muon_step_group(p, 7, p, None, p, 1, None, 0, 512, 1024, 1, 0.02,
-                                                     0.95, 0.0, 1, 1, coeff, 5, 0, None, 0, 1e-7, p,
-                                                     1 << 40, 0, None))
-    # unsupported publish dtype
-    assert "publish" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 0, p, 9, 512, 1024, 1, 0.02,
-                                                       0.95, 0.0, 1, 1, coeff, 5, 0, None, 0, 1e-7,
-                                                       p, 1 << 40, 0, None))
-    # no coefficients
-    assert "coefficient" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1,
-                                                           0.02, 0.95, 0.0, 1, 1, coeff, 0, 0, None,
-                                                           0, 1e-7, p, 1 << 40, 0, None))
-    # NS group needs outputs
-    assert "out_ptrs" in _err(lib.dmuon_newton_schulz_group(p, 1, None, 1, 64, 64, 1, coeff, 5,
-                                                            0, None, 0, 1e-7, p, 1 << 30, 0, None))
-    # unknown backend, restart list missing
-    assert "backend" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1, 0.02,
-                                                       0.95, 0.0, 1, 1, coeff, 5, 5, None, 0,
-                                                       1e-7, p, 1 << 40, 0, None))
-    assert "restart" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1, 0.02,
-                                                       0.95, 0.0, 1, 1, coeff, 5, 1, None, 2,
-                                                       1e-7, p, 1 << 40, 0, None))
+
+    def step(g_dtype=1, w_dtype=1, pub=None, pub_dtype=0, batch=1, n_t=0, T=5, backend=0,
+             restarts=None, n_restarts=0, ws_bytes=1 << 40):
+        return _err(lib.dmuon_muon_step_group(p, g_dtype, p, None, p, w_dtype, pub, pub_dtype,
+                                              512, 1024, batch, n_t, 0.02, 0.95, 0.0, 1, 1,
+                                              coeff, T, backend, restarts, n_restarts, 1e-7, p,
+                                              ws_bytes, 0, None))
+
+    assert "workspace" in step(ws_bytes=16)            # workspace too small
+    assert "dtype" in step(g_dtype=7)                  # unsupported gradient dtype code
+    assert "publish" in step(w_dtype=0, pub=p, pub_dtype=9)
+    assert "coefficient" in step(T=0)
+    assert "backend" in step(backend=5)
+    assert "restart" in step(backend=1, n_restarts=2)
+    assert "n_transposed" in step(n_t=2)               # more transposed members than the batch
+    assert "n_transposed" in step(n_t=-1)
     # gram workspace is larger than direct's
-    ws_direct = _C.plan(512, 1024, 1)[3]
-    assert "workspace" in _err(lib.dmuon_muon_step_group(p, 1, p, None, p, 1, None, 0, 512, 1024, 1,
-                                                         0.02, 0.95, 0.0, 1, 1, coeff, 5, 1, None,
-                                                         0, 1e-7, p, ws_direct, 0, None))
+    assert "workspace" in step(backend=1, ws_bytes=_C.plan(512, 1024, 1)[3])
+    # NS group needs outputs
+    assert "out_ptrs" in _err(lib.dmuon_newton_schulz_group(p, 1, None, 1, 64, 64, 1, 0, coeff, 5,
+                                                            0, None, 0, 1e-7, p, 1 << 30, 0, None))
 
 
 def test_pre_and_final_validation_without_gpu():
@@ -194,13 +184,13 @@ def test_noalloc_step_refuses_groups_beyond_its_scratch_without_gpu():
     rst = (ctypes.c_int * 1)(2)
     p = ctypes.c_void_p(4096)
     assert _C.plan(4096, 14336, 1, backend=_C.NS_GRAM)[3] > limit
-    msg = _err(lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 4096, 14336, 1,
+    msg = _err(lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 4096, 14336, 1, 0,
                                                  0.02, 0.95, 0.1, 1, 1, coeff, 5, 1, rst, 1,
                                                  1e-7, 0, None))
     assert "scratch" in msg and str(limit) in msg
     assert "backend" in _err(lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 64,
-                                                               64, 1, 0.02, 0.95, 0.1, 1, 1,
+                                                               64, 1, 0, 0.02, 0.95, 0.1, 1, 1,
                                                                coeff, 5, 7, None, 0, 1e-7, 0,
                                                                None))
-    assert lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 64, 64, 0, 0.02, 0.95,
+    assert lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 64, 64, 0, 0, 0.02, 0.95,
                                              0.1, 1, 1, coeff, 5, 0, None, 0, 1e-7, 0, None) == 0

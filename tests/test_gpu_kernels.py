@@ -200,3 +200,46 @@ def test_update_kernel_bit_exact(gpu, wdt):
         exp = torch.from_numpy(o.fma_f32(-np.float32(lrs), Us[i].cpu().numpy(),
                                          w1.cpu().numpy())).to(wdt).to(gpu)
         assert torch.equal(Ws[i], exp)
+
+
+@pytest.mark.parametrize("backend", [_C.NS_DIRECT, _C.NS_GRAM])
+@pytest.mark.parametrize("rows,cols,outdt", [(192, 448, torch.float32), (130, 250, torch.bfloat16),
+                                             (640, 256, torch.float32)])
+def test_ns_group_mixed_orientation_equals_separate_calls(gpu, backend, rows, cols, outdt):
+    """dmuon_newton_schulz_group with n_transposed: the batch's last members are cols x rows.
+    Each output must equal (bit for bit) that of a call holding only its own orientation, and
+    the transposed members' outputs must be the transposes of NS of their transposes."""
+    n_a, n_b = 3, 2
+    A = [_rand((rows, cols), 80 + i, dtype=torch.float32).to(gpu) for i in range(n_a)]
+    B = [_rand((cols, rows), 90 + i, dtype=torch.float32).to(gpu) for i in range(n_b)]
+    coeff = (ctypes.c_float * 15)(*([3.4445, -4.7750, 2.0315] * 5))
+    rst, n_rst = _C.restart_array((2,) if backend == _C.NS_GRAM else ())
+    code = _C.DTYPE_F32 if outdt == torch.float32 else _C.DTYPE_BF16
+
+    def run(ins, r, c, n_t):
+        outs = [torch.empty(t.shape, dtype=outdt, device=gpu) for t in ins]
+        _, _, _, nbytes = _C.plan(r, c, len(ins), 0, 0, backend)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+        gp, op = _ptrs(ins, gpu), _ptrs(outs, gpu)
+        _C.call("dmuon_newton_schulz_group", gp.data_ptr(), _C.DTYPE_F32, op.data_ptr(), code,
+                r, c, len(ins), n_t, coeff, 5, backend, rst, n_rst, 1e-7, ws.data_ptr(),
+                ws.numel(), 0, _stream())
+        torch.cuda.synchronize()
+        return outs
+
+    mixed = run(A + B, rows, cols, n_b)
+    only_a = run(A, rows, cols, 0)
+    only_b = run(B, cols, rows, 0)
+    for x, y in zip(mixed, only_a + only_b):
+        assert torch.equal(x, y)
+    # the whole batch given as cols x rows with the A members transposed: same outputs
+    flipped = run(B + A, cols, rows, n_a)
+    for x, y in zip(flipped, only_b + only_a):
+        assert torch.equal(x, y)
+    # NS(B^T) = NS(B)^T, evaluated as one mixed group holding both (equal up to the norm's
+    # summation order, which follows each matrix's own layout)
+    bt = [b.t().contiguous() for b in B]
+    pair = run(bt + B, rows, cols, n_b)
+    for i in range(n_b):
+        x, y = pair[i].float(), pair[n_b + i].t().float()
+        assert ((x - y).norm() / x.norm()).item() < 1e-2

@@ -442,3 +442,58 @@ def test_restored_state_cpu_mapped_and_reference_dtype(gpu):
         buf = opt2.state[id(dp)]["momentum_buffer"]
         assert buf.dtype == torch.float32 and buf.device == gpu and torch.isfinite(buf).all()
         assert torch.isfinite(dp._owned_data).all()
+
+
+# ------------------------------------------- oriented grouping: a shape and its transpose share
+def _run_muon(shapes, inits, grads_per_step, backend, gpu, profile=False):
+    m = Mats(shapes, torch.bfloat16, gpu)
+    with torch.no_grad():
+        for p, w in zip(m.parameters(), inits):
+            p.copy_(w)
+    dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2)        # fp32 masters + publish
+    dmuon.replicate(m)
+    opt = dmuon.Muon(m, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=backend,
+                     workspace_limit_bytes=64 << 20)
+    from dmuon_amd import _C
+    launches = 0
+    for gs in grads_per_step:
+        for p, g in zip(m.parameters(), gs):
+            p.grad = g.to(gpu)
+        if profile:
+            _C.profile_enable(True)
+        opt.step()
+        if profile:
+            torch.cuda.synchronize()
+            launches += sum(v["launches"] for v in _C.profile_collect().values())
+            _C.profile_enable(False)
+    torch.cuda.synchronize()
+    dps = dmuon.get_owned_params(m)
+    return ([p.detach().clone() for p in m.parameters()],
+            [dp._owned_data.clone() for dp in dps],
+            [opt.state[id(dp)]["momentum_buffer"].clone() for dp in dps], launches)
+
+
+@pytest.mark.parametrize("backend", ["gram", "direct"])
+def test_mixed_orientation_group_matches_per_orientation_runs(gpu, backend):
+    """Params of shape r x c and c x r land in one group (one set of NS launches over the
+    shared m x n products); every param's weight, forward copy and momentum must equal a run
+    that holds only params of its own orientation, bit for bit, over three steps. Ragged
+    shapes (padded NS tiles) and a square shape ride along."""
+    shapes = ([(256, 640)] * 3 + [(640, 256)] * 2 + [(130, 250), (250, 130), (250, 130)]
+              + [(512, 512)] * 2)
+    gen = torch.Generator().manual_seed(11)
+    inits = [(torch.randn(s, generator=gen) * 0.02).to(torch.bfloat16) for s in shapes]
+    steps = [[(torch.randn(s, generator=gen) * 0.02).to(torch.bfloat16) for s in shapes]
+             for _ in range(3)]
+    mixed = _run_muon(shapes, inits, steps, backend, gpu, profile=True)
+    wide = [i for i, s in enumerate(shapes) if s[0] <= s[1]]
+    tall = [i for i, s in enumerate(shapes) if s[0] > s[1]]
+    launches = 0
+    for idx in (wide, tall):
+        sub = _run_muon([shapes[i] for i in idx], [inits[i] for i in idx],
+                        [[gs[i] for i in idx] for gs in steps], backend, gpu, profile=True)
+        launches += sub[3]
+        for field in range(3):
+            for k, i in enumerate(idx):
+                assert torch.equal(mixed[field][i], sub[field][k]), (field, shapes[i])
+    assert mixed[3] < launches            # fewer launches than one group per orientation

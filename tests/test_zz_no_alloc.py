@@ -65,7 +65,7 @@ def _args(grp, rows, cols, first, backend, coeffs):
     gp, bp, ep, wp, pp = grp.tables
     return [gp.data_ptr(), BF16, bp.data_ptr(), ep.data_ptr(), wp.data_ptr(), grp.w_code,
             None if pp is None else pp.data_ptr(), BF16 if pp is not None else 0, rows, cols,
-            len(grp.g), 0.02, 0.95, 0.1, 1, first, c, T, backend, rst,
+            len(grp.g), 0, 0.02, 0.95, 0.1, 1, first, c, T, backend, rst,
             1 if backend == _C.NS_GRAM else 0, 1e-7]
 
 
