@@ -46,6 +46,10 @@ struct NtArgs {
   // just brought into L2. Per-element summation order depends only on the 256-block, so the
   // 128- and 256-tile kernels still give the same bits.
   int c_in;
+  // B stored k-major, [L][K][N] with row stride ldb (X itself rather than a transposed copy):
+  // the kernels stage its slices as BK rows of the tile's N values and assemble the MFMA
+  // operand with transposing LDS reads. C_IS_B then means C is B as stored.
+  int b_kmajor;
 };
 enum { C_NONE = 0, C_IS_A = 1, C_IS_B = 2 };
 

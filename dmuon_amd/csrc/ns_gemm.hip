@@ -64,6 +64,40 @@ __device__ __forceinline__ f32x4_t mfma_16x16x32(bf16x8_t b, bf16x8_t a, f32x4_t
   else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a, c, 0, 0, 0);
 }
 
+// k-major operand (stored [K][N], N contiguous): a slice of BK k-rows sits in LDS row by row,
+// 16-byte chunk c of row r at slot c ^ kswz(r). ds_read_b64_tr_b16 gives lane i of each 16-lane
+// group element i % 4 of the 8 bytes addressed by lane 4j + i / 4 of that group (j = 0..3), so
+// when the 16 lanes of group g address rows 8g + s / 4 (s = lane % 16) at values 4 (s % 4) ..
+// of a 16-value block, lane i receives the 4 consecutive k of value i -- half of the 16x16x32
+// operand; a second read 4 rows further gives the other half. The swizzle spreads the 16 rows
+// of one read over all 64 banks (two passes for its 512 bytes).
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int kswz(int r) { return 2 * ((r & 3) | (((r >> 3) & 1) << 2)); }
+__device__ __forceinline__ bf16x8_t read_kmajor(const char* p, int row_bytes) {
+  typedef __attribute__((address_space(3))) s16x4_t* lds_s4_t;
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t)(p));
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t)(p + 4 * row_bytes));
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+// The ping-pong kernel keeps a k-major B tile as four column blocks of 64 values, BK rows of
+// 128 bytes each; rows r and r + 1 share a 256-byte bank line, so the swizzle of a read's 16
+// rows (two passes) comes from row bits 1 and 3.
+__device__ __forceinline__ int kswz64(int r) { return 2 * (((r >> 1) & 1) | (((r >> 3) & 1) << 1)); }
+__device__ __forceinline__ int kmajor64_lane_off(int lane, int n0) {
+  const int s16 = lane & 15, g = lane >> 4;
+  const int h = 2 * (((s16 >> 3) & 1) | ((g & 1) << 1));   // kswz64 of every row this lane reads
+  const int chunk = ((n0 / 8) ^ h) | ((s16 & 3) >> 1);
+  return (8 * g + (s16 >> 2)) * 128 + chunk * 16 + (s16 & 1) * 8;
+}
+// byte offset, within a k-major slice of `row_bytes`-wide rows, of what lane (s = lane % 16,
+// g = lane / 16) addresses for the 16-value block starting at value n0 (a multiple of 16)
+__device__ __forceinline__ int kmajor_lane_off(int lane, int n0, int row_bytes) {
+  const int s16 = lane & 15, g = lane >> 4;
+  const int h = 2 * ((s16 >> 2) | ((g & 1) << 2));          // kswz of every row this lane reads
+  const int chunk = ((n0 / 8) ^ h) | ((s16 & 3) >> 1);
+  return (8 * g + (s16 >> 2)) * row_bytes + chunk * 16 + (s16 & 1) * 8;
+}
+
 // A wave's accumulators as the epilogue walks them: per 32-row slab x of the wave tile, NQ groups
 // of four values -- group q of a lane holds slab row row(q), columns col(q) .. col(q) + 3. Indices
 // are compile-time after unrolling, so the registers are addressed statically.
@@ -602,7 +636,7 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
   }
 }
 
-template <int BM, int BN, int BK, int S, int WM, int WN, int MODE, int E>
+template <int BM, int BN, int BK, int S, int WM, int WN, int MODE, int E, bool BKM>
 __global__ __launch_bounds__(64 * WM * WN)
 __attribute__((amdgpu_waves_per_eu(Occupancy<BM, BN, WM, WN>::WPE, Occupancy<BM, BN, WM, WN>::WPE)))
 void nt_mfma_kernel(const NtArgs a) {
@@ -623,7 +657,10 @@ void nt_mfma_kernel(const NtArgs a) {
   const int i0 = bi * BM, j0 = bj * BN;
 
   const uint16_t* __restrict__ Ab = a.A + (long long)l * a.sA + (long long)i0 * a.lda;
-  const uint16_t* __restrict__ Bb = a.B + (long long)l * a.sB + (long long)j0 * a.ldb;
+  const uint16_t* __restrict__ Bb =
+      a.B + (long long)l * a.sB + (BKM ? (long long)j0 : (long long)j0 * a.ldb);
+  constexpr int KROWB = BN * 2;                   // k-major B: bytes of one k-row of the tile
+  constexpr int KCPR = BN / 8, KRPK = 1024 / KROWB;
 
   // ---- global -> LDS DMA ring --------------------------------------------------------
   // DMA instruction q of wave w fills rows R0 = (NW q + w) * RPI .. R0 + RPI - 1 of a tile: lane l
@@ -641,8 +678,15 @@ void nt_mfma_kernel(const NtArgs a) {
   }
 #pragma unroll
   for (int q = 0; q < T::B_INST; ++q) {
-    const int r = (T::NW * q + wave) * T::RPI + lrow;
-    offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
+    if constexpr (BKM) {
+      // k-major: instruction q fills k-rows (NW q + w) KRPK.. of the slice; lane l writes slot
+      // l % KCPR of its row, i.e. fetches the chunk kswz places there
+      const int kr = (T::NW * q + wave) * KRPK + lane / KCPR, sl = lane % KCPR;
+      offb[q] = (unsigned)(kr * a.ldb + 8 * (sl ^ kswz(kr))) * 2u;
+    } else {
+      const int r = (T::NW * q + wave) * T::RPI + lrow;
+      offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
+    }
   }
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
   // The loads are MUBUF buffer loads into LDS (buffer_load_dwordx4 ... lds): one resource per
@@ -653,18 +697,21 @@ void nt_mfma_kernel(const NtArgs a) {
   const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(Ab), (short)0, (int)((long long)BM * a.lda * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(Bb), (short)0, (int)((long long)BN * a.ldb * 2), 0x00020000);
+      const_cast<uint16_t*>(Bb), (short)0,
+      (int)((long long)(BKM ? a.K : BN) * a.ldb * 2), 0x00020000);
+  const unsigned kstepB = BKM ? (unsigned)a.ldb : 1u;   // B slice offset: k-rows or k values
   // slice sl_ of A and B into ring slot slot_ (this wave's share)
 #define DMUON_ISSUE(slice_, slot_)                                                             \
   do {                                                                                         \
     char* st_ = smem + (slot_) * T::STAGE + wave * 1024;                                       \
     const unsigned so_ = (unsigned)((slice_) * BK * 2);                                        \
+    const unsigned sob_ = so_ * kstepB;                                                        \
     _Pragma("unroll") for (int q = 0; q < T::A_INST; ++q)                                      \
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsA, (lds_ptr_t)(st_ + q * 1024 * T::NW), 16, \
                                                  offa[q], so_, 0, 0);                          \
     _Pragma("unroll") for (int q = 0; q < T::B_INST; ++q)                                      \
         __builtin_amdgcn_raw_ptr_buffer_load_lds(                                              \
-            rsB, (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * T::NW), 16, offb[q], so_, 0, 0);    \
+            rsB, (lds_ptr_t)(st_ + T::A_BYTES + q * 1024 * T::NW), 16, offb[q], sob_, 0, 0);   \
   } while (0)
 
   // the wave sub-tile as BI x BJ blocks of 16x16 (v_mfma_f32_16x16x32)
@@ -683,6 +730,9 @@ void nt_mfma_kernel(const NtArgs a) {
   const int arow0 = wi * T::WTM + (lane & 15);
   const int brow0 = wj * T::WTN + (lane & 15);
   const int kq = lane >> 4;
+  int kboff[BJ];                                  // k-major B: this lane's read offsets
+#pragma unroll
+  for (int y = 0; y < BJ; ++y) kboff[y] = BKM ? kmajor_lane_off(lane, wj * T::WTN + 16 * y, KROWB) : 0;
 
   // lane l reads row (l % 16) of each 16-row block at the 16-byte chunk 4 ks + l / 16
   auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8_t* af, bf16x8_t* bfr) {
@@ -694,11 +744,15 @@ void nt_mfma_kernel(const NtArgs a) {
     }
 #pragma unroll
     for (int y = 0; y < BJ; ++y) {
-      const int row = brow0 + y * 16;
-      bfr[y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
+      if constexpr (BKM) {
+        bfr[y] = read_kmajor(sb + kboff[y] + ks * 32 * KROWB, KROWB);
+      } else {
+        const int row = brow0 + y * 16;
+        bfr[y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
+      }
     }
   };
-  constexpr int NF = BI + BJ, NM = BI * BJ;
+  constexpr int NF = BI + (BKM ? 2 : 1) * BJ, NM = BI * BJ;
   bf16x8_t af[2][BI], bfr[2][BJ];
 
   // Ring schedule: slot s % S holds slice s; the prologue fills all S slots. Iteration kt
@@ -766,20 +820,23 @@ void nt_mfma_kernel(const NtArgs a) {
 // M(k) reads all of the wave's fragments of K slice k from LDS into registers; C(k) issues its
 // 16x16x32 MFMAs on them. While one wave of a SIMD runs its MFMAs back to back, its partner does the LDS
 // reads, so the MFMA pipe never waits on a fragment read or a barrier. Group 1 also moves the
-// operands: in M(k), once its own reads of slot k % S are back, it issues the DMA of slice k + S
-// into that slot (group 0 finished reading it a phase earlier) and waits until slice k + 1 has
-// landed -- under group 0's MFMAs -- before the barrier that opens group 0's M(k + 1). A slice
-// is in flight for 2S - 1 phases.
-template <int BK, int S, int MODE, int E>
+// operands: at the end of M(k) it waits until slice k + 1 has landed -- under group 0's MFMAs --
+// before the barrier that opens group 0's M(k + 1), and right after that barrier (every wave's
+// reads of slot k % S are done) it issues the DMA of slice k + S into that slot. A slice is in
+// flight for about 2S - 2 phases.
+template <int BK, int S, int MODE, int E, bool BKM>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void nt_pp_kernel(const NtArgs a) {
   using T = Tile<256, 256, BK, S, 2, 4>;
   __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
   static_assert(T::LDS_BYTES <= 160 * 1024, "LDS budget");
   constexpr int KS = BK / 32;                        // 16x16x32 MFMA substeps per slice
-  constexpr int NI = 256 / T::RPI / 4;               // DMA instructions per group-1 wave, per operand
-  constexpr int LPT1 = 2 * NI;                       // per group-1 wave per slice
-  static_assert(NI <= 8 && (S - 1) * LPT1 <= 63, "DMA instruction counts");
+  // Group-1 wave v refills, per slice, three parts of the ring slot (RPI rows per instruction):
+  // A rows v*32 .. +31 (read by group 0 only), its own B block (rows / values v*64 .. +63: read
+  // by wave v and by itself) and A rows 128 + v*32 .. +31 (read by every group-1 wave).
+  constexpr int NAL = 32 / T::RPI, NB = 64 / T::RPI;
+  constexpr int LPT1 = 2 * NAL + NB;                 // per group-1 wave per slice
+  static_assert(NB <= 8 && (S - 1) * LPT1 <= 63, "DMA instruction counts");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -790,36 +847,57 @@ void nt_pp_kernel(const NtArgs a) {
   const int l = tp.l, bi = tp.bi, bj = tp.bj;
   const int i0 = bi * 256, j0 = bj * 256;
   const uint16_t* __restrict__ Ab = a.A + (long long)l * a.sA + (long long)i0 * a.lda;
-  const uint16_t* __restrict__ Bb = a.B + (long long)l * a.sB + (long long)j0 * a.ldb;
+  const uint16_t* __restrict__ Bb =
+      a.B + (long long)l * a.sB + (BKM ? (long long)j0 : (long long)j0 * a.ldb);
+  // k-major B: four column blocks of 64 values (one per wave column), each BK k-rows of 128
+  // bytes; chunk c of row r at slot c ^ kswz64(r)
+  constexpr int KBLK = BK * 128;
 
-  // group-1 DMA: instruction q of wave v = wave - 4 fills tile rows (4q + v) * RPI .. + RPI - 1
-  // of each operand (lane l writes LDS slot l % CPR of row l / CPR: it fetches the global chunk
-  // the swizzle places there)
+  // lane l of a DMA instruction writes LDS slot l % CPR of row l / CPR of its RPI-row group: it
+  // fetches the global chunk the swizzle places there
   const int v = wave & 3;
   const int lrow = lane / T::CPR, lsl = lane % T::CPR;
-  unsigned offa[8], offb[8];
+  unsigned offal[4], offah[4], offb[8];
 #pragma unroll
-  for (int q = 0; q < NI; ++q) {
-    const int r = (4 * q + v) * T::RPI + lrow;
-    offa[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8) * 2u;
-    offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
+  for (int q = 0; q < NAL; ++q) {
+    const int r = v * 32 + q * T::RPI + lrow, r2 = r + 128;
+    offal[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8) * 2u;
+    offah[q] = (unsigned)(r2 * a.lda + T::slot(lsl, r2) * 8) * 2u;
+  }
+#pragma unroll
+  for (int q = 0; q < NB; ++q) {
+    if constexpr (BKM) {
+      const int kr = q * 8 + (lane >> 3), sl = lane & 7;
+      offb[q] = (unsigned)(kr * a.ldb + v * 64 + 8 * (sl ^ kswz64(kr))) * 2u;
+    } else {
+      const int r = v * 64 + q * T::RPI + lrow;
+      offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
+    }
   }
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
   const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(Ab), (short)0, (int)((long long)256 * a.lda * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(Bb), (short)0, (int)((long long)256 * a.ldb * 2), 0x00020000);
-#define DMUON_PP_ISSUE(slice_, slot_)                                                          \
+      const_cast<uint16_t*>(Bb), (short)0,
+      (int)((long long)(BKM ? a.K : 256) * a.ldb * 2), 0x00020000);
+  const unsigned kstepB = BKM ? (unsigned)a.ldb : 1u;   // B slice offset: k-rows or k values
+  char* const a_lo = smem + v * 32 * T::ROWB;
+  char* const a_hi = smem + (128 + v * 32) * T::ROWB;
+  char* const b_own = smem + T::A_BYTES + v * 64 * T::ROWB;
+  static_assert(64 * T::ROWB == KBLK, "B block of a wave column");
+#define DMUON_PP_PART(rs_, base_, off_, n_, soff_, slot_)                                      \
   do {                                                                                         \
-    char* st_ = smem + (slot_) * T::STAGE + v * 1024;                                          \
-    const unsigned so_ = (unsigned)((slice_) * BK * 2);                                        \
-    _Pragma("unroll") for (int q = 0; q < NI; ++q)                                             \
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsA, (lds_ptr_t)(st_ + q * 4096), 16,         \
-                                                 offa[q], so_, 0, 0);                          \
-    _Pragma("unroll") for (int q = 0; q < NI; ++q)                                             \
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsB, (lds_ptr_t)(st_ + T::A_BYTES + q * 4096), \
-                                                 16, offb[q], so_, 0, 0);                      \
+    _Pragma("unroll") for (int q = 0; q < (n_); ++q)                                           \
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(                                              \
+            rs_, (lds_ptr_t)((base_) + (slot_) * T::STAGE + q * 1024), 16, off_[q], soff_, 0,  \
+            0);                                                                                \
   } while (0)
+#define DMUON_PP_ALO(slice_, slot_) \
+  DMUON_PP_PART(rsA, a_lo, offal, NAL, (unsigned)((slice_) * BK * 2), slot_)
+#define DMUON_PP_AHI(slice_, slot_) \
+  DMUON_PP_PART(rsA, a_hi, offah, NAL, (unsigned)((slice_) * BK * 2), slot_)
+#define DMUON_PP_B(slice_, slot_) \
+  DMUON_PP_PART(rsB, b_own, offb, NB, (unsigned)((slice_) * BK * 2) * kstepB, slot_)
 
   // the wave's 128x64 sub-tile as 8 x 4 blocks of 16x16
   f32x4_t acc[8][4];
@@ -833,6 +911,9 @@ void nt_pp_kernel(const NtArgs a) {
   const int arow0 = wi * 128 + (lane & 15);
   const int brow0 = wj * 64 + (lane & 15);
   const int kq = lane >> 4;
+  int kboff[4];                                      // k-major B: this lane's read offsets
+#pragma unroll
+  for (int y = 0; y < 4; ++y) kboff[y] = BKM ? wj * KBLK + kmajor64_lane_off(lane, 16 * y) : 0;
   bf16x8_t af[KS][8], bfr[KS][4];
   auto mem_phase = [&](int slot) {
     const char* sa = smem + slot * T::STAGE;
@@ -847,8 +928,12 @@ void nt_pp_kernel(const NtArgs a) {
       }
 #pragma unroll
       for (int y = 0; y < 4; ++y) {
-        const int row = brow0 + y * 16;
-        bfr[ks][y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
+        if constexpr (BKM) {
+          bfr[ks][y] = read_kmajor(sb + kboff[y] + ks * 32 * 128, 128);
+        } else {
+          const int row = brow0 + y * 16;
+          bfr[ks][y] = *reinterpret_cast<const bf16x8_t*>(sb + row * T::ROWB + (T::slot(kc, row) << 4));
+        }
       }
     }
   };
@@ -859,24 +944,36 @@ void nt_pp_kernel(const NtArgs a) {
   if (grp == 1) {
     // slices 0 .. S-1 (past the end: the last slice again, into a slot never read)
 #pragma unroll
-    for (int s0 = 0; s0 < S; ++s0) DMUON_PP_ISSUE(rot(min(s0, KT - 1)), s0);
+    for (int s0 = 0; s0 < S; ++s0) {
+      DMUON_PP_ALO(rot(min(s0, KT - 1)), s0);
+      DMUON_PP_B(rot(min(s0, KT - 1)), s0);
+      DMUON_PP_AHI(rot(min(s0, KT - 1)), s0);
+    }
     wait_vmcnt<(S - 1) * LPT1>();                     // slice 0 has landed
   }
   phase_barrier();                                    // |0
   if (grp == 1) phase_barrier();                      // |1: group 1 starts one phase behind
   for (int kt = 0; kt < KT; ++kt) {
+    // Group 1 refills slot kt % S with slice kt + S part by part, each part as soon as no wave
+    // can still read it: group 0 read the slot a phase earlier; the A rows 0-127 are read by
+    // group 0 only, the wave's B block by this wave only (in group 1), and A rows 128-255 by all
+    // of group 1, so that part waits for the barrier that ends this phase. No refill past the
+    // last slice: every DMA has landed when the loop ends, before the epilogue reuses the LDS.
+    const bool refill = grp == 1 && kt + S < KT;
     mem_phase(kt % S);
-    // this wave's fragments are in registers (and, for group 1, slot kt % S may be refilled)
+    if (refill) DMUON_PP_ALO(rot(kt + S), kt % S);   // after the reads in program order
+    // this wave's fragments are in registers
     __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0), vmcnt / expcnt untouched
     if (grp == 1) {
-      if (kt + S < KT) {
-        DMUON_PP_ISSUE(rot(kt + S), kt % S);
-        wait_vmcnt<(S - 1) * LPT1>();                 // slice kt + 1 has landed
-      } else {
-        wait_vmcnt<0>();
-      }
+      if (refill) DMUON_PP_B(rot(kt + S), kt % S);
+      // slice kt + 1 has landed (group 0 reads it right after the barrier); what was issued
+      // after its last part -- slices kt + 2 .. kt + S - 1 and the two parts of slice kt + S
+      // above -- may still be in flight
+      if (kt + S < KT) wait_vmcnt<(S - 2) * LPT1 + NAL + NB>();
+      else wait_vmcnt<0>();
     }
     phase_barrier();
+    if (refill) DMUON_PP_AHI(rot(kt + S), kt % S);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -886,7 +983,10 @@ void nt_pp_kernel(const NtArgs a) {
           acc[x][y] = mfma_16x16x32<E>(bfr[ks][y], af[ks][x], acc[x][y]);
     phase_barrier();
   }
-#undef DMUON_PP_ISSUE
+#undef DMUON_PP_PART
+#undef DMUON_PP_ALO
+#undef DMUON_PP_AHI
+#undef DMUON_PP_B
   if (grp == 0) phase_barrier();                      // |2KT+1
   wait_vmcnt<0>();
 
@@ -901,29 +1001,42 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   if (nb <= 0) return hipSuccess;
   // the second output relies on the exactly symmetric diagonal-tile path for its diagonal
   if (a.D2 && !(a.mode == EPI_SYM && a.tri && a.sym_exact)) return hipErrorInvalidValue;
+  // k-major B: whole-panel buffer range and slice offsets in 32 bits, rows of whole tiles
+  if (a.b_kmajor && ((long long)a.K * a.ldb * 2 >= (1LL << 31) || a.ldb < a.N))
+    return hipErrorInvalidValue;
   dim3 grid((unsigned)nb);
-#define DMUON_NT(TILE, BK, S, WM, WN, E)                                                       \
+#define DMUON_NT3(TILE, BK, S, WM, WN, E, KM)                                                  \
   do {                                                                                         \
     dim3 block(64 * WM * WN);                                                                  \
     if (a.mode == EPI_SYM)                                                                     \
-      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_SYM, E>), grid, block, \
-                         0, stream, a);                                                        \
+      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_SYM, E, KM>), grid,    \
+                         block, 0, stream, a);                                                 \
     else if (a.mode == EPI_NS)                                                                 \
-      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_NS, E>), grid, block,  \
-                         0, stream, a);                                                        \
+      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_NS, E, KM>), grid,     \
+                         block, 0, stream, a);                                                 \
     else                                                                                       \
-      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_FINAL, E>), grid,      \
+      hipLaunchKernelGGL((nt_mfma_kernel<TILE, TILE, BK, S, WM, WN, EPI_FINAL, E, KM>), grid,  \
                          block, 0, stream, a);                                                 \
   } while (0)
-#define DMUON_PP(E)                                                                            \
+#define DMUON_NT(TILE, BK, S, WM, WN, E)                                                       \
+  do {                                                                                         \
+    if (a.b_kmajor) DMUON_NT3(TILE, BK, S, WM, WN, E, true);                                   \
+    else DMUON_NT3(TILE, BK, S, WM, WN, E, false);                                             \
+  } while (0)
+#define DMUON_PP3(E, KM)                                                                       \
   do {                                                                                         \
     dim3 block(512);                                                                           \
     if (a.mode == EPI_SYM)                                                                     \
-      hipLaunchKernelGGL((nt_pp_kernel<64, 2, EPI_SYM, E>), grid, block, 0, stream, a);        \
+      hipLaunchKernelGGL((nt_pp_kernel<64, 2, EPI_SYM, E, KM>), grid, block, 0, stream, a);    \
     else if (a.mode == EPI_NS)                                                                 \
-      hipLaunchKernelGGL((nt_pp_kernel<64, 2, EPI_NS, E>), grid, block, 0, stream, a);         \
+      hipLaunchKernelGGL((nt_pp_kernel<64, 2, EPI_NS, E, KM>), grid, block, 0, stream, a);     \
     else                                                                                       \
-      hipLaunchKernelGGL((nt_pp_kernel<64, 2, EPI_FINAL, E>), grid, block, 0, stream, a);      \
+      hipLaunchKernelGGL((nt_pp_kernel<64, 2, EPI_FINAL, E, KM>), grid, block, 0, stream, a);  \
+  } while (0)
+#define DMUON_PP(E)                                                                            \
+  do {                                                                                         \
+    if (a.b_kmajor) DMUON_PP3(E, true);                                                        \
+    else DMUON_PP3(E, false);                                                                  \
   } while (0)
   // 256-tiles: the ping-pong kernel, 8 waves, 64-wide K slices in a two-slot ring; 128-tiles:
   // 4 waves, two blocks per CU. Measured and not kept: 32-wide slices in a four-slot ring for the
@@ -938,7 +1051,9 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
     else DMUON_NT(128, 64, 2, 2, 2, ELT_BF16);
   }
 #undef DMUON_NT
+#undef DMUON_NT3
 #undef DMUON_PP
+#undef DMUON_PP3
   return hipGetLastError();
 }
 
