@@ -793,14 +793,29 @@ static int gemm_common_checks(const char* who, const void* P, int64_t ldp, int64
   if (tile != 128 && tile != 256) return fail("%s: tile must be 128 or 256, got %d", who, tile);
   if (M <= 0 || N <= 0 || batch < 0) return fail("%s: bad sizes M=%d N=%d batch=%d", who, M, N, batch);
   if (M % tile || N % tile) return fail("%s: M=%d and N=%d must be multiples of the tile %d", who, M, N, tile);
-  if (!P || !XT) return fail("%s: P and XT must be non-NULL", who);
-  if (!aligned16(P) || !aligned16(XT) || (X && !aligned16(X)))
+  if (!P || (!XT && !X)) return fail("%s: P and one of XT / X must be non-NULL", who);
+  if (!aligned16(P) || (XT && !aligned16(XT)) || (X && !aligned16(X)))
     return fail("%s: operands must be 16-byte aligned", who);
-  if (!ld_ok(ldp) || !ld_ok(ldxt) || (X && !ld_ok(ldx)) || ldp < M || ldxt < M || (X && ldx < N))
+  if (!ld_ok(ldp) || ldp < M || (XT && (!ld_ok(ldxt) || ldxt < M)) || (X && (!ld_ok(ldx) || ldx < N)))
     return fail("%s: bad leading dimensions", who);
-  if (!stride_ok(strideP, batch) || !stride_ok(strideXT, batch) || (X && !stride_ok(strideX, batch)))
+  if (!stride_ok(strideP, batch) || (XT && !stride_ok(strideXT, batch)) ||
+      (X && !stride_ok(strideX, batch)))
     return fail("%s: batch strides must be non-negative multiples of 8", who);
+  // XT == NULL: the product reads X itself as its k-major B operand (one 32-bit buffer range
+  // per matrix)
+  if (!XT && (int64_t)M * ldx * 2 >= (1LL << 31))
+    return fail("%s: X read in place needs M * ldx * 2 < 2^31 bytes (pass XT instead)", who);
   return 0;
+}
+
+// B operand of the NS-GEMM exports: X^T when given, else X read k-major
+static void gemm_b_operand(NtArgs& g, const void* XT, int64_t ldxt, int64_t strideXT,
+                           const void* X, int64_t ldx, int64_t strideX) {
+  if (XT) {
+    g.B = static_cast<const uint16_t*>(XT); g.ldb = ldxt; g.sB = strideXT;
+  } else {
+    g.B = static_cast<const uint16_t*>(X); g.ldb = ldx; g.sB = strideX; g.b_kmajor = 1;
+  }
 }
 
 static int ns_gemm_impl(const char* who, int elt, const void* P, int64_t ldp, int64_t strideP, const void* XT, int64_t ldxt,
@@ -815,12 +830,13 @@ static int ns_gemm_impl(const char* who, int elt, const void* P, int64_t ldp, in
     return fail("%s: bad Xout", who);
   if (XTout && (!aligned16(XTout) || !ld_ok(ldxto) || ldxto < M || !stride_ok(strideXTo, batch)))
     return fail("%s: bad XTout", who);
-  if (XTout == XT) return fail("%s: XTout must not alias XT", who);
-  if (Xout == P || Xout == XT) return fail("%s: Xout must not alias P or XT", who);
+  if (XT && XTout == XT) return fail("%s: XTout must not alias XT", who);
+  if (Xout == P || (XT && Xout == XT)) return fail("%s: Xout must not alias P or XT", who);
+  if (!XT && Xout == X) return fail("%s: Xout must not alias X when X is the B operand", who);
   NtArgs g{};
   g.elt = elt;
   g.A = static_cast<const uint16_t*>(P); g.lda = ldp; g.sA = strideP;
-  g.B = static_cast<const uint16_t*>(XT); g.ldb = ldxt; g.sB = strideXT;
+  gemm_b_operand(g, XT, ldxt, strideXT, X, ldx, strideX);
   g.M = M; g.N = N; g.K = M; g.L = batch;
   g.mt = M / tile; g.nt = N / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
   g.mode = EPI_NS; g.alpha = alpha; g.beta = X ? beta : 0.f; g.alpha_dev = alpha_dev;
@@ -853,7 +869,7 @@ static int ns_gemm_final_impl(const char* who, int elt, const void* P, int64_t l
   NtArgs g{};
   g.elt = elt;
   g.A = static_cast<const uint16_t*>(P); g.lda = ldp; g.sA = strideP;
-  g.B = static_cast<const uint16_t*>(XT); g.ldb = ldxt; g.sB = strideXT;
+  gemm_b_operand(g, XT, ldxt, strideXT, X, ldx, strideX);
   g.M = M; g.N = N; g.K = M; g.L = batch;
   g.mt = M / tile; g.nt = N / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
   g.mode = EPI_FINAL; g.alpha = alpha; g.beta = X ? beta : 0.f; g.alpha_dev = alpha_dev;

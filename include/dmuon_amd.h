@@ -129,9 +129,12 @@ int dmuon_syrk_bf16(const void* A, int64_t lda, int64_t strideA, const void* B, 
 /*
  * One Newton-Schulz step X' = s_l * (P @ X + beta * X) for l < batch, given P ([M][M], the
  * polynomial b*A + c*A@A of A = X X^T) and XT = X^T ([N][M]); s_l = alpha * alpha_dev[l] (or
- * alpha). Writes X' into Xout ([M][N], may alias X) and X'^T into XTout ([N][M], must not
- * alias XT). Operands, X, Xout and XTout are 16-bit words of `dtype` (DMUON_DTYPE_F16 or
- * DMUON_DTYPE_BF16). tile 128 or 256; M % tile == 0, N % tile == 0 (the NS planner pads).
+ * alpha). Writes X' into Xout ([M][N], may alias X) and, when XTout != NULL, X'^T into XTout
+ * ([N][M], must not alias XT). XT == NULL: the product reads X ([M][N] as stored, like the
+ * reference's torch.mm(P, X)) as its B operand through transposing LDS loads -- same result,
+ * no transposed copy needed; Xout must then not alias X. Operands, X, Xout and XTout are
+ * 16-bit words of `dtype` (DMUON_DTYPE_F16 or DMUON_DTYPE_BF16). tile 128 or 256;
+ * M % tile == 0, N % tile == 0 (the NS planner pads).
  */
 int dmuon_ns_gemm(int dtype, const void* P, int64_t ldp, int64_t strideP, const void* XT,
                   int64_t ldxt, int64_t strideXT, const void* X, int64_t ldx, int64_t strideX,
@@ -155,7 +158,8 @@ int dmuon_ns_gemm_bf16(const void* P, int64_t ldp, int64_t strideP, const void* 
  *   pub_ptrs != NULL: pub[l] <- round(new W[l])         (dtype pub_dtype; needs w_ptrs): the
  *     forward copy of an owner's master weight, written in the same pass (the reference copies
  *     _owned_data into the packed forward buffer afterwards, fsdp2/group.py:766-781)
- * P, XT and X are 16-bit words of `dtype` (DMUON_DTYPE_F16 or DMUON_DTYPE_BF16); U stays fp32
+ * P, XT and X are 16-bit words of `dtype` (DMUON_DTYPE_F16 or DMUON_DTYPE_BF16); XT may be NULL
+ * (X is then the B operand, as in dmuon_ns_gemm). U stays fp32
  * up to the update (W <- round(fma(-lrs, U, round(W*decay))): one rounding, as add_(alpha=)).
  */
 int dmuon_ns_gemm_final(int dtype, const void* P, int64_t ldp, int64_t strideP, const void* XT,

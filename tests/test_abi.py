@@ -122,6 +122,13 @@ def test_pre_and_final_validation_without_gpu():
         p, 256, 0, p, 256, 0, p, 256, 0, 256, 256, 1, 1.0, 1.0, None, 256, 256, 0, p, 0, None,
         0, p, 1, 1.0, 0.0, 128, None))
     assert lib.dmuon_muon_pre_partials(128, 256) == 8
+    # NS-GEMM: X^T or X (read in place) must be given; X in place may not be overwritten
+    assert "one of XT / X" in _err(lib.dmuon_ns_gemm_bf16(
+        p, 256, 0, None, 256, 0, None, 256, 0, p, 256, 0, None, 256, 0, 256, 256, 1, 1.0, 1.0,
+        None, 128, None))
+    assert "alias X" in _err(lib.dmuon_ns_gemm_bf16(
+        p, 256, 0, None, 256, 0, ctypes.c_void_p(8192), 256, 0, ctypes.c_void_p(8192), 256, 0,
+        None, 256, 0, 256, 256, 1, 1.0, 1.0, None, 128, None))
 
 
 def test_syrk_any_shape_workspace_plan_without_gpu():

@@ -159,6 +159,53 @@ def test_ns_gemm_operand_dtypes(gpu, dtype, code):
         assert torch.equal(Xb, Xo)
 
 
+@pytest.mark.parametrize("dtype,code", [(torch.float16, _C.DTYPE_F16),
+                                        (torch.bfloat16, _C.DTYPE_BF16)])
+@pytest.mark.parametrize("M,N,tile", [(256, 768, 128), (512, 768, 256), (1024, 2048, 256)])
+def test_ns_gemm_reads_x_in_place(gpu, dtype, code, M, N, tile):
+    """XT == NULL: the NS-GEMM exports read X as stored (the reference's torch.mm(P, X)
+    operand) through transposing LDS loads. Same products in the same order as the X^T form,
+    so X' (and the fused final update) must match it bit for bit."""
+    L = 2
+    g = torch.Generator().manual_seed(5)
+    P = (torch.randn(L, M, M, generator=g) * 0.05).to(dtype).to(gpu)
+    X = (torch.randn(L, M, N, generator=g) * 0.05).to(dtype).to(gpu)
+    XT = X.transpose(1, 2).contiguous()
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for xt in (XT, None):
+        Xo = torch.empty_like(X)
+        _C.call("dmuon_ns_gemm", code, P.data_ptr(), M, M * M,
+                None if xt is None else xt.data_ptr(), M, M * N, X.data_ptr(), N, M * N,
+                Xo.data_ptr(), N, M * N, None, M, M * N, M, N, L, 0.5, 3.4445, None, tile, stream)
+        outs.append(Xo)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    _check_close(outs[1], 0.5 * (torch.bmm(P.float(), X.float()) + 3.4445 * X.float()))
+    # fused final step into fp32 weights, ragged real extent, both B forms
+    m_real, n_real = M - 3, N - 5
+    ws = []
+    for xt in (XT, None):
+        W = [(torch.randn(m_real, n_real, generator=g) * 0.02).to(gpu) for _ in range(L)]
+        if ws:
+            W = [w.clone() for w in ws[0][1]]
+        w0 = [w.clone() for w in W]
+        wp = torch.tensor([w.data_ptr() for w in W], dtype=torch.int64, device=gpu)
+        _C.call("dmuon_ns_gemm_final", code, P.data_ptr(), M, M * M,
+                None if xt is None else xt.data_ptr(), M, M * N, X.data_ptr(), N, M * N, M, N, L,
+                0.25, 1.5, None, m_real, n_real, 0, None, 0, wp.data_ptr(), _C.DTYPE_F32, None, 0,
+                0.998, 0.01, tile, stream)
+        torch.cuda.synchronize()
+        ws.append((W, w0))
+    for a, b in zip(ws[0][0], ws[1][0]):
+        assert torch.equal(a, b)
+    # X in place must not be overwritten by its own product
+    with pytest.raises(RuntimeError, match="alias"):
+        _C.call("dmuon_ns_gemm", code, P.data_ptr(), M, M * M, None, M, M * N, X.data_ptr(), N,
+                M * N, X.data_ptr(), N, M * N, None, M, M * N, M, N, L, 0.5, 3.4445, None, tile,
+                stream)
+
+
 def test_reference_basic_dp_loop(gpu):
     """The training loop of the reference's examples/basic_dp.py:63-93 through ``import dmuon``
     at world_size=1 (``dmuon.replicate`` for the non-dedicated params): loss finite, every
