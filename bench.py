@@ -23,6 +23,8 @@ sample of the same workload.
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import sys
@@ -191,14 +193,30 @@ def library_compare(torch, dev, _C, reps: int = 5) -> dict:
             fn()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
+        with quiet_gc():
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / reps
         out[name] = {"ms": round(ms, 3), "tflops": round(2.0 * M * N * M / (ms * 1e-3) / 1e12, 1)}
     return out
+
+
+@contextlib.contextmanager
+def quiet_gc():
+    """Python's cyclic garbage collector off inside a timed region (after one full collection):
+    a generation-2 pass over the optimizer's objects takes ~80 ms on the host, enough to stall
+    a timed leg whose calls synchronise with the device."""
+    gc.collect()
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
 
 
 def time_steps(torch, opt, warmup: int, steps: int) -> list:
@@ -207,11 +225,12 @@ def time_steps(torch, opt, warmup: int, steps: int) -> list:
         opt.step()
     torch.cuda.synchronize()
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    evs[0].record()
-    for k in range(steps):
-        opt.step()
-        evs[k + 1].record()
-    torch.cuda.synchronize()
+    with quiet_gc():
+        evs[0].record()
+        for k in range(steps):
+            opt.step()
+            evs[k + 1].record()
+        torch.cuda.synchronize()
     return [evs[k].elapsed_time(evs[k + 1]) for k in range(steps)]
 
 
@@ -256,11 +275,12 @@ def copy_leg(torch, dev, gib: int = 4, reps: int = 5) -> dict:
     dst.copy_(src)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    e1.record()
-    torch.cuda.synchronize()
+    with quiet_gc():
+        e0.record()
+        for _ in range(reps):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
     gbs = 2.0 * n * 4 / (ms * 1e-3) / 1e9
     del src, dst
@@ -352,13 +372,14 @@ def main():
     torch.cuda.synchronize()
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    evs[0].record()
-    for k in range(args.steps):
-        opt.step()
-        evs[k + 1].record()          # one event between steps: per-step times for the spread
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with quiet_gc():
+        t0 = time.perf_counter()
+        evs[0].record()
+        for k in range(args.steps):
+            opt.step()
+            evs[k + 1].record()          # one event between steps: per-step times for the spread
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     ms_per_step = evs[0].elapsed_time(evs[-1]) / args.steps
     per_step = sorted(evs[k].elapsed_time(evs[k + 1]) for k in range(args.steps))
 
@@ -369,9 +390,10 @@ def main():
     prof_steps = max(1, min(3, args.steps))
     _C.profile_collect()
     _C.profile_enable(True)
-    for _ in range(prof_steps):
-        opt.step()
-    torch.cuda.synchronize()
+    with quiet_gc():
+        for _ in range(prof_steps):
+            opt.step()
+        torch.cuda.synchronize()
     _C.profile_enable(False)
     prof = _C.profile_collect()
     classes = {}
@@ -418,11 +440,12 @@ def main():
         opt.clip_grad_norm_(1e30)          # coefficient 1: the values stay, the traffic is full
         torch.cuda.synchronize()
         c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        c0.record()
-        for _ in range(3):
-            opt.clip_grad_norm_(1e30)
-        c1.record()
-        torch.cuda.synchronize()
+        with quiet_gc():
+            c0.record()
+            for _ in range(3):
+                opt.clip_grad_norm_(1e30)
+            c1.record()
+            torch.cuda.synchronize()
         c_ms = c0.elapsed_time(c1) / 3
         c_bytes = n_elems * 2 * 3           # bf16: read for the norms, read + write to scale
         c_gbs = c_bytes / (c_ms * 1e-3) / 1e9

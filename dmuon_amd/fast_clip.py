@@ -144,6 +144,21 @@ class _JobTable:
         self.job_tensor_ids = b32 + 8 * n
         self.zero_segments = b32 + 8 * n + 4 * self.n_jobs
         self.device = device
+        self._dtypes = [g.dtype for g in tensors]
+        self._dtype_groups = None
+
+    def dtype_groups(self):
+        """(dtype, device index tensor of the table's tensors of that dtype, or None when all
+        have it), built once per table: no host-to-device copy on later calls."""
+        if self._dtype_groups is None:
+            groups = []
+            for dt in sorted(set(self._dtypes), key=str):
+                sel = [i for i, d in enumerate(self._dtypes) if d == dt]
+                idx = None if len(sel) == self.n else torch.tensor(sel).pin_memory().to(
+                    self.device, non_blocking=True)
+                groups.append((dt, idx))
+            self._dtype_groups = groups
+        return self._dtype_groups
 
     def _stream(self):
         return torch.cuda.current_stream(self.device).cuda_stream

@@ -118,10 +118,12 @@ def _total_norm(tensors, eligible, table, p, device) -> torch.Tensor:
         # per-tensor norms rounded to each gradient's dtype, as torch._foreach_norm returns them
         # (one rounding op per dtype present, not one per tensor)
         norms = torch.sqrt(sq)
-        dts = [t.dtype for t in eligible]
-        for dt in set(dts):
-            if dt != torch.float32:
-                idx = torch.tensor([i for i, d in enumerate(dts) if d == dt], device=device)
+        for dt, idx in table.dtype_groups():
+            if dt == torch.float32:
+                continue
+            if idx is None:                   # every tensor has this dtype
+                norms = norms.to(dt).float()
+            else:
                 norms[idx] = norms[idx].to(dt).float()
         parts.append(norms)
     others = [torch.linalg.vector_norm(t.detach(), p).to(device=device, dtype=torch.float32)
