@@ -30,7 +30,8 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.parametrize("rows,cols,batch,tile,m_pad,n_pad", [
-    (4096, 4096, 1, 128, 4096, 4096),       # single square: 136 tiles of 256 would underfill
+    (4096, 4096, 1, 256, 4096, 4096),       # single square: 1 wave of 256-tiles beats 2 of 128
+    (1024, 16384, 1, 128, 1024, 16384),     # small m: 36 tiles of 128 fill one wave
     (4096, 4096, 64, 256, 4096, 4096),
     (14336, 4096, 96, 256, 4096, 14336),    # tall: m = cols
     (1408, 2048, 128, 128, 1408, 2048),     # 1408 is not a multiple of 256
