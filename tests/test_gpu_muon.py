@@ -445,7 +445,7 @@ def test_restored_state_cpu_mapped_and_reference_dtype(gpu):
 
 
 # ------------------------------------------- oriented grouping: a shape and its transpose share
-def _run_muon(shapes, inits, grads_per_step, backend, gpu, profile=False):
+def _run_muon(shapes, inits, grads_per_step, backend, gpu, profile=False, ws_limit=64 << 20):
     m = Mats(shapes, torch.bfloat16, gpu)
     with torch.no_grad():
         for p, w in zip(m.parameters(), inits):
@@ -453,7 +453,7 @@ def _run_muon(shapes, inits, grads_per_step, backend, gpu, profile=False):
     dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2)        # fp32 masters + publish
     dmuon.replicate(m)
     opt = dmuon.Muon(m, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=backend,
-                     workspace_limit_bytes=64 << 20)
+                     workspace_limit_bytes=ws_limit)
     from dmuon_amd import _C
     launches = 0
     for gs in grads_per_step:
@@ -497,3 +497,9 @@ def test_mixed_orientation_group_matches_per_orientation_runs(gpu, backend):
             for k, i in enumerate(idx):
                 assert torch.equal(mixed[field][i], sub[field][k]), (field, shapes[i])
     assert mixed[3] < launches            # fewer launches than one group per orientation
+    # a workspace of ~two matrices: the 256x640 / 640x256 bucket runs in chunks, one of them
+    # holding both orientations
+    small = _run_muon(shapes, inits, steps, backend, gpu, ws_limit=5 << 20)
+    for field in range(3):
+        for i in range(len(shapes)):
+            assert torch.equal(mixed[field][i], small[field][i]), (field, shapes[i])
