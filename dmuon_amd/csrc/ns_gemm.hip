@@ -21,6 +21,8 @@
 //     per slice.
 #include "dmuon_amd_internal.h"
 
+#include <type_traits>
+
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -953,27 +955,32 @@ void nt_pp_kernel(const NtArgs a) {
   }
   phase_barrier();                                    // |0
   if (grp == 1) phase_barrier();                      // |1: group 1 starts one phase behind
-  for (int kt = 0; kt < KT; ++kt) {
-    // Group 1 refills slot kt % S with slice kt + S part by part, each part as soon as no wave
-    // can still read it: group 0 read the slot a phase earlier; the A rows 0-127 are read by
-    // group 0 only, the wave's B block by this wave only (in group 1), and A rows 128-255 by all
-    // of group 1, so that part waits for the barrier that ends this phase. No refill past the
-    // last slice: every DMA has landed when the loop ends, before the epilogue reuses the LDS.
-    const bool refill = grp == 1 && kt + S < KT;
+  // Group 1 refills slot kt % S with slice kt + S part by part, each part as soon as no wave can
+  // still read it: group 0 read the slot a phase earlier; the A rows 0-127 are read by group 0
+  // only, the wave's B block by this wave only (in group 1), and A rows 128-255 by all of group
+  // 1, so that part waits for the barrier that ends this phase. No refill past the last slice:
+  // every DMA has landed when the loop ends, before the epilogue reuses the LDS. The refilling
+  // iterations and the last S ones are two loops, so neither body branches around its DMA
+  // (measured: a runtime refill test inside one loop costs 3-11%).
+  auto iteration = [&](int kt, auto refill_c) {
+    constexpr bool REFILL = decltype(refill_c)::value;
     mem_phase(kt % S);
-    if (refill) DMUON_PP_ALO(rot(kt + S), kt % S);   // after the reads in program order
+    if (REFILL && grp == 1) DMUON_PP_ALO(rot(kt + S), kt % S);   // after the reads in program order
     // this wave's fragments are in registers
     __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0), vmcnt / expcnt untouched
     if (grp == 1) {
-      if (refill) DMUON_PP_B(rot(kt + S), kt % S);
-      // slice kt + 1 has landed (group 0 reads it right after the barrier); what was issued
-      // after its last part -- slices kt + 2 .. kt + S - 1 and the two parts of slice kt + S
-      // above -- may still be in flight
-      if (kt + S < KT) wait_vmcnt<(S - 2) * LPT1 + NAL + NB>();
-      else wait_vmcnt<0>();
+      if (REFILL) {
+        DMUON_PP_B(rot(kt + S), kt % S);
+        // slice kt + 1 has landed (group 0 reads it right after the barrier); what was issued
+        // after its last part -- slices kt + 2 .. kt + S - 1 and the two parts of slice kt + S
+        // above -- may still be in flight
+        wait_vmcnt<(S - 2) * LPT1 + NAL + NB>();
+      } else {
+        wait_vmcnt<0>();
+      }
     }
     phase_barrier();
-    if (refill) DMUON_PP_AHI(rot(kt + S), kt % S);
+    if (REFILL && grp == 1) DMUON_PP_AHI(rot(kt + S), kt % S);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -982,7 +989,10 @@ void nt_pp_kernel(const NtArgs a) {
         for (int y = 0; y < 4; ++y)
           acc[x][y] = mfma_16x16x32<E>(bfr[ks][y], af[ks][x], acc[x][y]);
     phase_barrier();
-  }
+  };
+  int kt = 0;
+  for (; kt + S < KT; ++kt) iteration(kt, std::true_type{});
+  for (; kt < KT; ++kt) iteration(kt, std::false_type{});
 #undef DMUON_PP_PART
 #undef DMUON_PP_ALO
 #undef DMUON_PP_AHI
