@@ -53,6 +53,19 @@ __device__ __forceinline__ float from_elt(uint16_t h) {
   if constexpr (E == ELT_F16) return static_cast<float>(__builtin_bit_cast(_Float16, h));
   else return bf2f(h);
 }
+// Two values rounded (nearest even) to E and packed, low half first: one packed convert
+// instruction on gfx950 instead of two converts and a pack.
+template <int E>
+__device__ __forceinline__ unsigned pack2_elt(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  if constexpr (E == ELT_F16) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
+  } else {
+    typedef __bf16 b16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2_t{lo, hi}, b16x2_t));
+  }
+}
 // v_mfma_f32_16x16x32: a lane holds row (l % 16) of both operands at k-chunk l / 16, and four
 // consecutive output columns of one row. It gives the same bits as the 32x32x16 form (measured:
 // the products accumulate in the same order and round identically), and on MI355X it sustains
@@ -139,11 +152,11 @@ struct Tile {
   static constexpr int RPL = 256 / ROWB;          // rows per 256-byte LDS bank line (64 banks)
   static constexpr int A_BYTES = BM * ROWB;
   static constexpr int STAGE = (BM + BN) * ROWB;
-  // epilogue staging per wave: one 32-row slab row-major at pitch EPN (WTN bf16 + 8 B, so the
-  // 32 rows of a lane column fall on distinct banks), two slabs transposed at pitch EPT (64 bf16
-  // + 16 B: the four lane groups of a scatter hit different banks), and
-  // the fp32 slab of the final step (32 rows of WTN + 4 floats)
-  static constexpr int EPN = WTN * 2 + 8;
+  // epilogue staging per wave: one 32-row slab row-major at pitch EPN (WTN values + 16 B: rows
+  // stay 16-byte aligned for the 16-byte reads of the stores), two slabs transposed at pitch EPT
+  // (64 values + 16 B: the four lane groups of a scatter hit different banks), and the fp32 slab
+  // of the final step (32 rows of WTN + 4 floats)
+  static constexpr int EPN = WTN * 2 + 16;
   static constexpr int EPT = 64 * 2 + 16;
   static constexpr int EPF = 32 * (WTN + 4) * 4;
   static constexpr int EPI_MAX2 = 32 * EPN + WTN * EPT;
@@ -351,57 +364,95 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
 #pragma unroll
     for (int x = 0; x < Acc::SLABS; ++x) {
       if (Cb && x + 1 < Acc::SLABS) load_c(x + 1, cbuf[(x + 1) & 1]);
+      // r = s v + beta c (SYM; + diag where i == j) or s (v + beta c) (NS), rounded to E. The
+      // tests that do not depend on the element -- an addend at all, a slab that meets the
+      // diagonal -- are taken once per slab; without C the addend term is the constant
+      // beta * 0, so every element takes the same operations as with C.
       u32x2_t o2[NQ];
+      const bool slab_diag = MODE == EPI_SYM && iw + 32 * x < jw + T::WTN && jw < iw + 32 * x + 32;
+      const float bz = a.beta * 0.f;
+      float r[NQ][4];
+      if (Cb) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const u32x2_t c2 = cbuf[x & 1][q];
+          const float cv[4] = {from_elt<E>(c2.x & 0xffff), from_elt<E>(c2.x >> 16),
+                               from_elt<E>(c2.y & 0xffff), from_elt<E>(c2.y >> 16)};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float v = acc.val(x, q, e);
+            if constexpr (MODE == EPI_SYM) r[q][e] = s * v + a.beta * cv[e];
+            else r[q][e] = s * (v + a.beta * cv[e]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float v = acc.val(x, q, e);
+            if constexpr (MODE == EPI_SYM) r[q][e] = s * v + bz;
+            else r[q][e] = s * (v + bz);
+          }
+      }
+      if (slab_diag) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (iw + 32 * x + acc.row(q) == jw + acc.col(q) + e) r[q][e] += a.diag;
+      }
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
-        const int ro = acc.row(q), co = acc.col(q);
-        float cv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (Cb) {
-          const u32x2_t c2 = cbuf[x & 1][q];
-          cv[0] = from_elt<E>(c2.x & 0xffff); cv[1] = from_elt<E>(c2.x >> 16);
-          cv[2] = from_elt<E>(c2.y & 0xffff); cv[3] = from_elt<E>(c2.y >> 16);
-        }
-        uint16_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float v = acc.val(x, q, e);
-          float r;
-          if constexpr (MODE == EPI_SYM) {
-            r = s * v + a.beta * cv[e];
-            if (iw + 32 * x + ro == jw + co + e) r += a.diag;
-          } else {
-            r = s * (v + a.beta * cv[e]);
-          }
-          o[e] = to_elt<E>(r);
-        }
-        o2[q].x = (unsigned)o[0] | ((unsigned)o[1] << 16);
-        o2[q].y = (unsigned)o[2] | ((unsigned)o[3] << 16);
-        *reinterpret_cast<u32x2_t*>(reg + ro * T::EPN + co * 2) = o2[q];
+        o2[q].x = pack2_elt<E>(r[q][0], r[q][1]);
+        o2[q].y = pack2_elt<E>(r[q][2], r[q][3]);
+        *reinterpret_cast<u32x2_t*>(reg + acc.row(q) * T::EPN + acc.col(q) * 2) = o2[q];
       }
       {
-        constexpr int CPRW = T::WTN / 4;          // 8-byte chunks per slab row
+        // the slab as whole 16-byte row chunks (8 lanes per 64-value row), all of its LDS reads
+        // ahead of the stores
+        static_assert(T::EPN % 16 == 0, "16-byte slab rows");
+        constexpr int CPRW = T::WTN / 8;          // 16-byte chunks per slab row
         constexpr int RPIT = 64 / CPRW;           // slab rows per wave instruction
+        constexpr int NR = 32 / RPIT;
         const int cr = lane / CPRW, cc = lane % CPRW;
-        const long long doff = (long long)(iw + 32 * x + cr) * a.ldd + jw + 4 * cc;
+        const long long doff = (long long)(iw + 32 * x + cr) * a.ldd + jw + 8 * cc;
+        u32x4_t dv[NR];
 #pragma unroll
-        for (int r0 = 0; r0 < 32; r0 += RPIT) {
-          const u32x2_t v = *reinterpret_cast<const u32x2_t*>(reg + (r0 + cr) * T::EPN + 8 * cc);
-          const long long o = doff + (long long)r0 * a.ldd;
-          // diagonal tile: row i keeps columns j >= i (chunk j0 .. j0+3)
-          const int di = iw + 32 * x + r0 + cr, dj = jw + 4 * cc;
-          if (!diag || dj > di) {
-            // non-temporal: the outputs of a launch exceed L2 and the next product streams
-            // them back from HBM / Infinity Cache anyway (measured 0.9% on the c5 step)
-            __builtin_nontemporal_store(v, reinterpret_cast<u32x2_t*>(Db + o));
-            if (D2b) __builtin_nontemporal_store(v, reinterpret_cast<u32x2_t*>(D2b + o));
-          } else if (dj + 3 >= di) {
+        for (int k = 0; k < NR; ++k)
+          dv[k] = *reinterpret_cast<const u32x4_t*>(reg + (k * RPIT + cr) * T::EPN + 16 * cc);
+        if (!diag) {
+          // non-temporal: the outputs of a launch exceed L2 and the next product streams them
+          // back from HBM / Infinity Cache anyway (measured 0.9% on the c5 step)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              if (dj + e < di) continue;
-              const unsigned word = e < 2 ? v.x : v.y;
-              const uint16_t h = (uint16_t)((e & 1) ? (word >> 16) : (word & 0xffff));
-              Db[o + e] = h;
-              if (D2b) D2b[o + e] = dj + e == di ? to_elt<E>(from_elt<E>(h) + a.diag2) : h;
+          for (int k = 0; k < NR; ++k)
+            __builtin_nontemporal_store(
+                dv[k], reinterpret_cast<u32x4_t*>(Db + doff + (long long)k * RPIT * a.ldd));
+          if (D2b) {
+#pragma unroll
+            for (int k = 0; k < NR; ++k)
+              __builtin_nontemporal_store(
+                  dv[k], reinterpret_cast<u32x4_t*>(D2b + doff + (long long)k * RPIT * a.ldd));
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < NR; ++k) {
+            const u32x4_t v = dv[k];
+            const long long o = doff + (long long)k * RPIT * a.ldd;
+            // diagonal tile: row i keeps columns j >= i (chunk j0 .. j0+7)
+            const int di = iw + 32 * x + k * RPIT + cr, dj = jw + 8 * cc;
+            if (dj > di) {
+              __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(Db + o));
+              if (D2b) __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(D2b + o));
+            } else if (dj + 7 >= di) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                if (dj + e < di) continue;
+                const unsigned word = v[e >> 1];
+                const uint16_t h = (uint16_t)((e & 1) ? (word >> 16) : (word & 0xffff));
+                Db[o + e] = h;
+                if (D2b) D2b[o + e] = dj + e == di ? to_elt<E>(from_elt<E>(h) + a.diag2) : h;
+              }
             }
           }
         }
@@ -421,7 +472,10 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
         }
       }
       if (DTb && (x & 1)) {
-        // the pair (slabs x - 1, x): D^T rows j of 64 values i = iw + 32 (x - 1) .. + 63
+        // the pair (slabs x - 1, x): D^T rows j of 64 values i = iw + 32 (x - 1) .. + 63; the
+        // 16-byte chunks of a D^T row are 8 lanes, so a store writes 8 whole 128-byte row
+        // segments (a transposing read of a row-major pair would give 16 lanes one row each and
+        // 64-byte segments: measured 1-4% slower)
         const int cr = lane >> 3, cc = lane & 7;  // 8 lanes x 16 B per 64-value row
         const int ip = iw + 32 * (x - 1);
         const long long toff = (long long)(jw + cr) * ldt + ip + 8 * cc;
@@ -654,8 +708,11 @@ void nt_mfma_kernel(const NtArgs a) {
   const int wi = wave / WN, wj = wave % WN;
 
   // ---- tile decode -------------------------------------------------------------------
+  // the decode is the same for every lane; readfirstlane states it, so the buffer descriptors
+  // and offsets built from it stay scalar whatever the compiler's uniformity analysis proves
   const TilePos tp = decode_tile(a, blockIdx.x, gridDim.x);
-  const int l = tp.l, bi = tp.bi, bj = tp.bj;
+  const int l = __builtin_amdgcn_readfirstlane(tp.l);
+  const int bi = __builtin_amdgcn_readfirstlane(tp.bi), bj = __builtin_amdgcn_readfirstlane(tp.bj);
   const int i0 = bi * BM, j0 = bj * BN;
 
   const uint16_t* __restrict__ Ab = a.A + (long long)l * a.sA + (long long)i0 * a.lda;
@@ -725,7 +782,7 @@ void nt_mfma_kernel(const NtArgs a) {
     for (int y = 0; y < BJ; ++y) acc[x][y] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int KT = a.K / BK;
-  const int kt0 = first_slice(a, i0, j0, BK, KT);
+  const int kt0 = __builtin_amdgcn_readfirstlane(first_slice(a, i0, j0, BK, KT));
   auto rot = [&](int t) { return t + kt0 >= KT ? t + kt0 - KT : t + kt0; };
   constexpr int KS = BK / 32;                     // MFMA substeps per slice
   static_assert(KS % 2 == 0, "fragment double buffer alternates per substep");
@@ -848,8 +905,11 @@ void nt_pp_kernel(const NtArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2, wj = wave & 3, wi = grp;
 
+  // the decode is the same for every lane; readfirstlane states it, so the buffer descriptors
+  // and offsets built from it stay scalar whatever the compiler's uniformity analysis proves
   const TilePos tp = decode_tile(a, blockIdx.x, gridDim.x);
-  const int l = tp.l, bi = tp.bi, bj = tp.bj;
+  const int l = __builtin_amdgcn_readfirstlane(tp.l);
+  const int bi = __builtin_amdgcn_readfirstlane(tp.bi), bj = __builtin_amdgcn_readfirstlane(tp.bj);
   const int i0 = bi * 256, j0 = bj * 256;
   const uint16_t* __restrict__ Ab = a.A + (long long)l * a.sA + (long long)i0 * a.lda;
   const uint16_t* __restrict__ Bb =
@@ -862,23 +922,26 @@ void nt_pp_kernel(const NtArgs a) {
   // fetches the global chunk the swizzle places there
   const int v = wave & 3;
   const int lrow = lane / T::CPR, lsl = lane % T::CPR;
-  unsigned offal[4], offah[4], offb[8];
+  // The swizzle of a row (and of a k-major row) repeats every 16 rows, so instructions q and
+  // q + 2 of a part differ by 16 rows: two per-lane offsets per operand, the rest of the
+  // distance (16 rows per q / 2, and 128 rows for A's upper half) in the scalar offset. That
+  // keeps 12 VGPRs free for the whole kernel.
+  static_assert(T::RPI == 8 && T::RPL * T::CPR == 16, "swizzle period of 16 rows");
+  unsigned offa2[2], offb2[2];
 #pragma unroll
-  for (int q = 0; q < NAL; ++q) {
-    const int r = v * 32 + q * T::RPI + lrow, r2 = r + 128;
-    offal[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8) * 2u;
-    offah[q] = (unsigned)(r2 * a.lda + T::slot(lsl, r2) * 8) * 2u;
-  }
-#pragma unroll
-  for (int q = 0; q < NB; ++q) {
+  for (int q = 0; q < 2; ++q) {
+    const int r = v * 32 + q * T::RPI + lrow;
+    offa2[q] = (unsigned)(r * a.lda + T::slot(lsl, r) * 8) * 2u;
     if constexpr (BKM) {
       const int kr = q * 8 + (lane >> 3), sl = lane & 7;
-      offb[q] = (unsigned)(kr * a.ldb + v * 64 + 8 * (sl ^ kswz64(kr))) * 2u;
+      offb2[q] = (unsigned)(kr * a.ldb + v * 64 + 8 * (sl ^ kswz64(kr))) * 2u;
     } else {
-      const int r = v * 64 + q * T::RPI + lrow;
-      offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
+      const int rb = v * 64 + q * T::RPI + lrow;
+      offb2[q] = (unsigned)(rb * a.ldb + T::slot(lsl, rb) * 8) * 2u;
     }
   }
+  const unsigned a16 = 16u * (unsigned)a.lda * 2u, b16 = 16u * (unsigned)a.ldb * 2u;
+  const unsigned ahi = 128u * (unsigned)a.lda * 2u;
   typedef __attribute__((address_space(3))) void* lds_ptr_t;
   const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(Ab), (short)0, (int)((long long)256 * a.lda * 2), 0x00020000);
@@ -890,19 +953,19 @@ void nt_pp_kernel(const NtArgs a) {
   char* const a_hi = smem + (128 + v * 32) * T::ROWB;
   char* const b_own = smem + T::A_BYTES + v * 64 * T::ROWB;
   static_assert(64 * T::ROWB == KBLK, "B block of a wave column");
-#define DMUON_PP_PART(rs_, base_, off_, n_, soff_, slot_)                                      \
+#define DMUON_PP_PART(rs_, base_, off_, step_, n_, soff_, slot_)                               \
   do {                                                                                         \
     _Pragma("unroll") for (int q = 0; q < (n_); ++q)                                           \
         __builtin_amdgcn_raw_ptr_buffer_load_lds(                                              \
-            rs_, (lds_ptr_t)((base_) + (slot_) * T::STAGE + q * 1024), 16, off_[q], soff_, 0,  \
-            0);                                                                                \
+            rs_, (lds_ptr_t)((base_) + (slot_) * T::STAGE + q * 1024), 16, off_[q & 1],        \
+            (soff_) + (unsigned)(q >> 1) * (step_), 0, 0);                                     \
   } while (0)
 #define DMUON_PP_ALO(slice_, slot_) \
-  DMUON_PP_PART(rsA, a_lo, offal, NAL, (unsigned)((slice_) * BK * 2), slot_)
+  DMUON_PP_PART(rsA, a_lo, offa2, a16, NAL, (unsigned)((slice_) * BK * 2), slot_)
 #define DMUON_PP_AHI(slice_, slot_) \
-  DMUON_PP_PART(rsA, a_hi, offah, NAL, (unsigned)((slice_) * BK * 2), slot_)
+  DMUON_PP_PART(rsA, a_hi, offa2, a16, NAL, (unsigned)((slice_) * BK * 2) + ahi, slot_)
 #define DMUON_PP_B(slice_, slot_) \
-  DMUON_PP_PART(rsB, b_own, offb, NB, (unsigned)((slice_) * BK * 2) * kstepB, slot_)
+  DMUON_PP_PART(rsB, b_own, offb2, b16, NB, (unsigned)((slice_) * BK * 2) * kstepB, slot_)
 
   // the wave's 128x64 sub-tile as 8 x 4 blocks of 16x16
   f32x4_t acc[8][4];
@@ -944,7 +1007,7 @@ void nt_pp_kernel(const NtArgs a) {
   };
 
   const int KT = a.K / BK;
-  const int kt0 = first_slice(a, i0, j0, BK, KT);
+  const int kt0 = __builtin_amdgcn_readfirstlane(first_slice(a, i0, j0, BK, KT));
   auto rot = [&](int t) { return t + kt0 >= KT ? t + kt0 - KT : t + kt0; };
   if (grp == 1) {
     // slices 0 .. S-1 (past the end: the last slice again, into a slot never read)
