@@ -874,8 +874,8 @@ void nt_mfma_kernel(const NtArgs a) {
 // Ping-pong schedule of the 256x256 tile with 8 waves of 128x64 (wave w and w + 4 share a SIMD).
 // Group 0 (waves 0-3) owns tile rows 0-127, group 1 (waves 4-7) rows 128-255; the groups run one
 // phase apart, every phase ending at a workgroup barrier:
-//   group 0:  |0 M0 |1 C0 |2 M1 |3 C1 |4 ... M(KT-1) |2KT-1 C(KT-1) |2KT        |2KT+1
-//   group 1:  |0    |1 M0 |2 C0 |3 M1 |4 ...         |2KT-1 M(KT-1) |2KT C(KT-1) |2KT+1
+//   group 0:  |0 M0 |1 C0 |2 M1 |3 C1 |4 ... M(KT-1) |2KT-1 C(KT-1) |2KT epilogue
+//   group 1:  |0    |1 M0 |2 C0 |3 M1 |4 ...         |2KT-1 M(KT-1) |2KT C(KT-1), epilogue
 // M(k) reads all of the wave's fragments of K slice k from LDS into registers; C(k) issues its
 // 16x16x32 MFMAs on them. While one wave of a SIMD runs its MFMAs back to back, its partner does the LDS
 // reads, so the MFMA pipe never waits on a fragment read or a barrier. The operand DMA is issued
@@ -1027,8 +1027,9 @@ void nt_pp_kernel(const NtArgs a) {
   // last slice, and every DMA has landed when the loop ends, before the epilogue reuses the LDS.
   // The four iteration kinds are separate instances, so no body branches around its DMA
   // (measured: a runtime refill test inside one loop costs 3-11%).
-  auto iteration = [&](int kt, auto ra_c, auto rb_c) {
+  auto iteration = [&](int kt, auto ra_c, auto rb_c, auto last_c) {
     constexpr bool RA = decltype(ra_c)::value, RB = decltype(rb_c)::value;
+    constexpr bool LAST = decltype(last_c)::value;
     mem_phase(kt % S);
     if (RA && grp == 0) {
       DMUON_PP_ALO(rot(kt + 1), (kt + 1) % S);
@@ -1053,22 +1054,27 @@ void nt_pp_kernel(const NtArgs a) {
         for (int y = 0; y < 4; ++y)
           acc[x][y] = mfma_16x16x32<E>(bfr[ks][y], af[ks][x], acc[x][y]);
     if (RA && grp == 0) wait_vmcnt<0>();             // slice kt + 1's A rows have landed
-    phase_barrier();
+    // Last slice: group 1 stops at the barrier before its MFMAs (|2KT), which is also the one
+    // after group 0's; no wave reads the ring after it, so group 0's epilogue overlaps group 1's
+    // last MFMA phase. Both groups pass 2KT + 1 barriers.
+    if (!(LAST && grp == 1)) phase_barrier();
   };
+  const std::false_type no{};
+  const std::true_type yes{};
   if (KT >= 3) {
-    iteration(0, std::false_type{}, std::true_type{});
+    iteration(0, no, yes, no);
     int kt = 1;
-    for (; kt + 2 < KT; ++kt) iteration(kt, std::true_type{}, std::true_type{});
-    iteration(kt, std::true_type{}, std::false_type{});            // kt = KT - 2
-    iteration(kt + 1, std::false_type{}, std::false_type{});
+    for (; kt + 2 < KT; ++kt) iteration(kt, yes, yes, no);
+    iteration(kt, yes, no, no);                      // kt = KT - 2
+    iteration(kt + 1, no, no, yes);
   } else {
-    for (int kt = 0; kt < KT; ++kt) iteration(kt, std::false_type{}, std::false_type{});
+    for (int kt = 0; kt + 1 < KT; ++kt) iteration(kt, no, no, no);
+    iteration(KT - 1, no, no, yes);
   }
 #undef DMUON_PP_PART
 #undef DMUON_PP_ALO
 #undef DMUON_PP_AHI
 #undef DMUON_PP_B
-  if (grp == 0) phase_barrier();                      // |2KT+1
   wait_vmcnt<0>();
 
   nt_epilogue<T, MODE, E>(a, smem, Acc16<8, 4>{acc, lane}, l, bi, bj, i0, j0, lane, wave, wi,
@@ -1080,6 +1086,8 @@ void nt_pp_kernel(const NtArgs a) {
 hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   const long long nb = (long long)a.tiles_per_mat * a.L;
   if (nb <= 0) return hipSuccess;
+  // the K loops run whole 64-wide slices, at least one
+  if (a.K <= 0 || a.K % 64 != 0) return hipErrorInvalidValue;
   // the second output relies on the exactly symmetric diagonal-tile path for its diagonal
   if (a.D2 && !(a.mode == EPI_SYM && a.tri && a.sym_exact)) return hipErrorInvalidValue;
   // k-major B: whole-panel buffer range and slice offsets in 32 bits, rows of whole tiles
