@@ -31,6 +31,7 @@ _SIGNATURES = {
     "dmuon_profile_enable": (c_int, [c_int]),
     "dmuon_profile_collect": (c_int, [ctypes.POINTER(c_d), ctypes.POINTER(c_i64),
                                       ctypes.POINTER(c_d), ctypes.POINTER(c_d), c_int]),
+    "dmuon_stream_copy": (c_int, [c_vp, c_vp, c_i64, c_vp]),
     "dmuon_syrk": (c_int, [c_int, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64,
                            c_vp, c_i64, c_i64, c_int, c_int, c_int, c_f, c_f, c_f, c_vp, c_int,
                            c_vp, c_i64, c_vp]),

@@ -584,6 +584,20 @@ extern "C" {
 
 const char* dmuon_last_error(void) { return g_last_error.c_str(); }
 
+int dmuon_stream_copy(const void* src, void* dst, int64_t bytes, void* stream) {
+  const char* who = "dmuon_stream_copy";
+  if (bytes == 0) return 0;
+  if (!src || !dst || bytes < 0) return fail("%s: NULL buffer or negative size", who);
+  if (!aligned16(src) || !aligned16(dst) || bytes % 16)
+    return fail("%s: buffers must be 16-byte aligned and the size a multiple of 16 (got %lld)",
+                who, (long long)bytes);
+  const uintptr_t s = reinterpret_cast<uintptr_t>(src), d = reinterpret_cast<uintptr_t>(dst);
+  if (s < d + (uintptr_t)bytes && d < s + (uintptr_t)bytes)
+    return fail("%s: source and destination overlap", who);
+  return check_launch(launch_stream_copy(src, dst, bytes / 16, static_cast<hipStream_t>(stream)),
+                      who);
+}
+
 int dmuon_profile_enable(int on) {
   g_prof.on = on != 0;
   return 0;

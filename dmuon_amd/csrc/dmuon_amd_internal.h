@@ -97,6 +97,8 @@ hipError_t launch_norm_finalize_est(const float* partials, int nparts, int L, fl
                                     hipStream_t stream);
 
 // dst[l][r][c] = r < rows && c < cols ? src[l][r][c] : 0 over rows_out x cols_out (16-bit)
+// dst = src, n16 chunks of 16 bytes (both 16-byte aligned, not overlapping)
+hipError_t launch_stream_copy(const void* src, void* dst, long long n16, hipStream_t stream);
 hipError_t launch_pad_copy(const uint16_t* src, long long lds, long long ss, uint16_t* dst,
                            long long ldd, long long sd, int rows, int cols, int rows_out,
                            int cols_out, int L, hipStream_t stream);

@@ -72,7 +72,7 @@ extern "C" {
 const char* dmuon_last_error(void);
 
 /* ABI version (major*100 + minor): DMUON_ABI_VERSION of the header the library was built with. */
-#define DMUON_ABI_VERSION 105
+#define DMUON_ABI_VERSION 106
 int dmuon_abi_version(void);
 
 /*
@@ -88,6 +88,15 @@ int dmuon_abi_version(void);
 int dmuon_profile_enable(int on);
 int dmuon_profile_collect(double* ms, int64_t* launches, double* flops, double* bytes,
                           int n_classes);
+
+/*
+ * dst = src, `bytes` bytes (no reference counterpart; measurement support for the benchmark
+ * harness): one 16-byte chunk per thread with non-temporal loads and stores, the pattern that
+ * reaches this HBM's streaming ceiling, so bench.py can report the bandwidth-bound kernels
+ * against what the device actually sustains. Both buffers 16-byte aligned, `bytes` a multiple
+ * of 16, no overlap. Asynchronous on `stream`.
+ */
+int dmuon_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
 /*
  * D[l] = alpha * s_l * A[l] @ B[l]^T + beta * C[l] + diag_add * I     for l < batch

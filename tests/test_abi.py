@@ -132,6 +132,17 @@ def test_pre_and_final_validation_without_gpu():
         None, 256, 0, 256, 256, 1, 1.0, 1.0, None, 128, None))
 
 
+def test_stream_copy_validation_without_gpu():
+    lib = _C.lib()
+    a, b = ctypes.c_void_p(1 << 20), ctypes.c_void_p(1 << 24)
+    assert lib.dmuon_stream_copy(a, b, 0, None) == 0              # nothing to do, no launch
+    assert "NULL" in _err(lib.dmuon_stream_copy(None, b, 64, None))
+    assert "negative" in _err(lib.dmuon_stream_copy(a, b, -16, None))
+    assert "aligned" in _err(lib.dmuon_stream_copy(ctypes.c_void_p((1 << 20) + 8), b, 64, None))
+    assert "multiple of 16" in _err(lib.dmuon_stream_copy(a, b, 40, None))
+    assert "overlap" in _err(lib.dmuon_stream_copy(a, ctypes.c_void_p((1 << 20) + 32), 64, None))
+
+
 def test_syrk_any_shape_workspace_plan_without_gpu():
     """dmuon_syrk_workspace_size: 0 for operands the kernel reads in place; otherwise the
     zero-padded copies (A, a distinct B, C and D) rounded to the tile and the 64-wide slice."""

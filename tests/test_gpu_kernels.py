@@ -243,3 +243,14 @@ def test_ns_group_mixed_orientation_equals_separate_calls(gpu, backend, rows, co
     for i in range(n_b):
         x, y = pair[i].float(), pair[n_b + i].t().float()
         assert ((x - y).norm() / x.norm()).item() < 1e-2
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 16, 3 << 20])
+def test_stream_copy_bit_exact(gpu, nbytes):
+    # the streaming-ceiling copy the bench times: every byte lands, nothing past the end
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, generator=torch.Generator().manual_seed(nbytes)).to(gpu)
+    dst = torch.zeros(nbytes + 64, dtype=torch.uint8, device=gpu)
+    _C.call("dmuon_stream_copy", src.data_ptr(), dst.data_ptr(), nbytes, _stream())
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes], src)
+    assert int(dst[nbytes:].sum().item()) == 0
