@@ -269,12 +269,14 @@ def config_leg(torch, dmuon, dev, shapes, ns, steps, warmup, seed, momentum_init
     ms = per[len(per) // 2]
     flops = sum(ns_useful_flops(*s, 5, ns.backend, ns.restart_iterations) for s in shapes)
     tf = flops / (ms * 1e-3) / 1e12
+    tf_base = sum(ns_useful_flops(*s, 5, "direct") for s in shapes) / (ms * 1e-3) / 1e12
     from dmuon_amd import _C
     tile, m_pad, n_pad, _ = _C.plan(*shapes[0], 1, 0, 0, _C.NS_GRAM if ns.backend == "gram"
                                     else _C.NS_DIRECT)
     out = {"ms_per_step_median": round(ms, 3), "steps": steps,
            "useful_ns_tflop": round(flops / 1e12, 4), "tflops": round(tf, 1),
            "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+           "frac_baseline_flop_model": round(tf_base / MFMA_BF16_PEAK_TFLOPS, 4),
            "ns_shape": [min(shapes[0]), max(shapes[0])]}
     del opt, model
     torch.cuda.empty_cache()
@@ -396,6 +398,9 @@ def main():
     n_elems = sum(p.numel() for p in mats)
     rest_elems = sum(p.numel() for n, p in model.named_parameters() if not n.startswith("mats."))
     flops = sum(ns_useful_flops(*p.shape, 5, ns.backend, ns.restart_iterations) for p in mats)
+    # BASELINE.md's own count of useful NS FLOPs (the direct form: T*[m(m+1)n + m(m+1)m + 2m^2n],
+    # 471.81 TF for c5), whatever form the step computes
+    flops_baseline = sum(ns_useful_flops(*p.shape, 5, "direct") for p in mats)
 
     # ---- timed region: exactly K optimizer steps (Muon matrices + AdamW rest) -----------------
     for _ in range(args.warmup):
@@ -546,6 +551,12 @@ def main():
                    "parallelism": "single GPU (world_size=1 owner)"},
         "ns_tflops": round(flops / (ms_per_step * 1e-3) / 1e12, 1),
         "ns_frac_mfma_peak_step": round(flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "ns_baseline_flop_model": {
+            "useful_tflop_per_step": round(flops_baseline / 1e12, 2),
+            "definition": "BASELINE.md section 2: T*[m(m+1)n + m(m+1)m + 2m^2n] per matrix",
+            "tflops": round(flops_baseline / (ms_per_step * 1e-3) / 1e12, 1),
+            "frac": round(flops_baseline / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "ms_at_50pct_peak": round(flops_baseline / (0.5 * MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3, 1)},
         "roofline": {
             "kernel": ("nt_pp_kernel / nt_mfma_kernel<..., fp16> (Gram X X^T, R/Z/W triangle "
                        "products, Q update, restart Q X, final Q X + update)" if args.ns == "gram"

@@ -46,7 +46,11 @@ def _check_close(out, ref, rel=1e-2):
 
 
 @pytest.mark.parametrize("tile", [128, 256])
-@pytest.mark.parametrize("M,K,L", [(256, 64, 1), (512, 1024, 3), (768, 320, 2), (1024, 4096, 1)])
+# K of 64 .. 256 walks the 256-tile kernel's short-loop paths: 1, 2, 3 and 4 slices (the split
+# refill has separate iteration kinds for the first, the refilling, the last-but-one and the
+# last slice)
+@pytest.mark.parametrize("M,K,L", [(256, 64, 1), (256, 128, 2), (512, 192, 1), (256, 256, 1),
+                                   (512, 1024, 3), (768, 320, 2), (1024, 4096, 1)])
 def test_syrk_vs_torch(gpu, tile, M, K, L):
     if M % tile:
         pytest.skip("M not a multiple of the tile")
