@@ -148,17 +148,19 @@ int tri_tiles(int m_pad, int tile) {
 
 // Output tile of a group's products, by the estimated time of its triangle products (the bulk
 // of the work) in units of one 256-tile of work: a wave of 256-tiles gives every CU one tile (4
-// units of 128-tile work), a wave of 128-tiles gives it two (2 units) at about 1/1.2 of the
-// 256-tile rate (measured). Ceil'd waves charge the last, partial wave in full; the padding each
-// tile size adds to m and n counts too. Measured on MI355X: one 4096^2 matrix runs 20% faster on
-// 256-tiles (136 tiles on 256 CUs) than on 128-tiles (528 tiles on 512 slots), one 1024x16384
-// or 2048x8192 matrix 35-55% faster on 128-tiles.
+// units of 128-tile work), a wave of 128-tiles gives it two (2 units) at about 1/1.35 of the
+// 256-tile rate (fitted to grouped Gram runs: 32 x 4096^2, 64 x 1024x4096, 64 and 128 x
+// 1408x2048, one 2048x8192). Ceil'd waves charge the last, partial wave in full; the padding
+// each tile size adds to m and n counts too. Measured on MI355X: one 4096^2 matrix runs 20%
+// faster on 256-tiles (136 tiles on 256 CUs) than on 128-tiles (528 tiles on 512 slots), one
+// 1024x16384 or 2048x8192 matrix 25-55% faster on 128-tiles, 128 experts of 1408x2048 5% faster
+// on 256-tiles padded to 1536.
 int auto_tile(int64_t m, int64_t n, int64_t batch, int num_cus) {
   const int64_t m256 = round_up(m, 256) / 256, m128 = round_up(m, 128) / 128;
   const int64_t t256 = batch * m256 * (m256 + 1) / 2, t128 = batch * m128 * (m128 + 1) / 2;
   const double npad = (double)round_up(n, 256) / (double)round_up(n, 128);
   const double c256 = 4.0 * (double)((t256 + num_cus - 1) / num_cus) * npad;
-  const double c128 = 2.4 * (double)((t128 + 2 * num_cus - 1) / (2 * num_cus));
+  const double c128 = 2.7 * (double)((t128 + 2 * num_cus - 1) / (2 * num_cus));
   return c256 <= c128 ? 256 : 128;
 }
 

@@ -44,7 +44,8 @@ struct NtArgs {
   // (C_IS_A: C is A, C_IS_B: C is B, the matrix symmetric): the slices of the 256-column block
   // that holds the tile's C values run last, so the epilogue reads C from lines the block has
   // just brought into L2. Per-element summation order depends only on the 256-block, so the
-  // 128- and 256-tile kernels still give the same bits.
+  // 128- and 256-tile kernels give the same bits for the same K (a K padded differently for the
+  // two tile sizes moves the start).
   int c_in;
   // B stored k-major, [L][K][N] with row stride ldb (X itself rather than a transposed copy):
   // the kernels stage its slices as BK rows of the tile's N values and assemble the MFMA

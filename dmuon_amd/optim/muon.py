@@ -409,7 +409,7 @@ class Muon(torch.optim.Optimizer):
         """Split a bucket of L same-shape matrices into chunks whose NS workspace fits
         ``workspace_limit_bytes``: the fewest chunks, or a few more when that wastes less of the
         last wave of tiles. Cost of a split = sum over chunks of the waves its triangle products
-        take (tiles / tiles resident at once, rounded up; a 128-tile wave counts 0.6 of a
+        take (tiles / tiles resident at once, rounded up; a 128-tile wave counts 0.675 of a
         256-tile wave, the library's own tile-choice model), the launches that dominate both NS
         forms."""
         per = _C.plan(rows, cols, 1, 0, num_cus, backend)[3]
@@ -424,7 +424,7 @@ class Muon(torch.optim.Optimizer):
             tiles = size * mt * (mt + 1) // 2
             if tile == 256:
                 return float(-(-tiles // num_cus))
-            return 0.6 * (-(-tiles // (2 * num_cus)))
+            return 0.675 * (-(-tiles // (2 * num_cus)))
 
         best = None
         n_min = -(-L // most)

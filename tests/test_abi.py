@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
     (1024, 16384, 1, 128, 1024, 16384),     # small m: 36 tiles of 128 fill one wave
     (4096, 4096, 64, 256, 4096, 4096),
     (14336, 4096, 96, 256, 4096, 14336),    # tall: m = cols
-    (1408, 2048, 128, 128, 1408, 2048),     # 1408 is not a multiple of 256
+    (1408, 2048, 128, 256, 1536, 2048),     # 128 experts: 256-tiles padded to 1536 beat 128-tiles
     (1000, 3000, 2, 128, 1024, 3072),       # padded
 ])
 def test_plan(rows, cols, batch, tile, m_pad, n_pad):

@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import dmuon_amd as dmuon
+from dmuon_amd import _C as dmuon_C
 from dmuon_amd.optim.newton_schulz import newton_schulz_batched
 from oracle import ns_oracle as o
 
@@ -234,7 +235,11 @@ def test_moe_batch_gram_full_size(gpu):
             ref = _closed_form_gpu(mats[i], o.POLAR_EXPRESS)
             err = ((outs[i].double() - ref).norm() / ref.norm()).item()
             assert err < BF16_TOL, (mats[i].shape, i, err)
-        single = newton_schulz_batched([mats[37]], o.POLAR_EXPRESS, backend="gram",
+        # at the batch's tile size a single matrix gets the same bits (the tile choice itself
+        # follows the batch: 64 experts take 256-tiles, one takes 128, and with m = 1408 the two
+        # pad K differently)
+        tile = dmuon_C.plan(*mats[0].shape, len(mats), 0, 0, dmuon_C.NS_GRAM)[0]
+        single = newton_schulz_batched([mats[37]], o.POLAR_EXPRESS, tile=tile, backend="gram",
                                        restart_iterations=[2])[0]
         assert torch.equal(single, outs[37])
 
