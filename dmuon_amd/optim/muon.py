@@ -350,6 +350,50 @@ class Muon(torch.optim.Optimizer):
             return 0, 0
         dev = chunks[0][3]
         main = torch.cuda.current_stream(dev)
+        self._run_pipeline(chunks, dev, main, (lr, mu, wd, coeffs, T, backend, rst, n_rst))
+        for c in chunks:
+            for dp, _, _ in c[6]:
+                dp._reduced_grad = None
+        return count, numel
+
+    def _stage_chunk(self, chunk, ws, stream, args) -> None:
+        """Momentum, norm and NS operands of one chunk into ``ws``, on ``stream`` (the pointer
+        arrays and any contiguous gradient copies are made on that stream too)."""
+        rows, cols, n_t, dev, first, _, part, tile, _ = chunk
+        _, mu, _, _, _, backend, _, _ = args
+        L = len(part)
+        with torch.cuda.stream(stream):
+            gs = [g if g.is_contiguous() else g.contiguous() for _, g, _ in part]
+            ests = ([self.state[id(dp)]["ns_scale"].data_ptr() for dp, _, _ in part]
+                    if self._single_pass else [])
+            ptrs = _pinned_ptrs([t.data_ptr() for t in gs]
+                                + [self.state[id(dp)]["momentum_buffer"].data_ptr()
+                                   for dp, _, _ in part] + ests, dev)
+            _C.call("dmuon_muon_stage_group", ptrs.data_ptr(), _float_dtype_code(gs[0]),
+                    ptrs.data_ptr() + 8 * L,
+                    ptrs.data_ptr() + 16 * L if ests else None, rows, cols, L, n_t, mu,
+                    int(self._nesterov), int(first), backend, self._ns_eps, ws.data_ptr(),
+                    ws.numel(), tile, stream.cuda_stream)
+
+    def _apply_chunk(self, chunk, ws, stream, args) -> None:
+        """NS products and the fused weight update of one staged chunk, on ``stream``."""
+        rows, cols, n_t, dev, _, has_pub, part, tile, _ = chunk
+        lr, _, wd, coeffs, T, backend, rst, n_rst = args
+        L = len(part)
+        with torch.cuda.stream(stream):
+            W = [dp._owned_data for dp, _, _ in part]
+            pubs = [dp.publish_target() for dp, _, _ in part] if has_pub else []
+            wptrs = _pinned_ptrs([t.data_ptr() for t in W] + [t.data_ptr() for t in pubs], dev)
+            # the forward copies (master != parameter) are written by the same epilogue
+            _C.call("dmuon_muon_apply_group", wptrs.data_ptr(), _float_dtype_code(W[0]),
+                    wptrs.data_ptr() + 8 * L if pubs else None,
+                    _float_dtype_code(pubs[0]) if pubs else 0, rows, cols, L, n_t, lr, wd,
+                    coeffs, T, backend, rst, n_rst, ws.data_ptr(), ws.numel(), tile,
+                    stream.cuda_stream)
+
+    def _run_pipeline(self, chunks, dev, main, args) -> None:
+        """The chunks one after another on ``main``; with ``overlap_staging`` chunk k+1 is
+        staged on a side stream into the other workspace while chunk k's NS runs."""
         overlap = self._overlap_staging and len(chunks) > 1
         side = self._side_stream(dev) if overlap else main
         # both workspaces exist before the hand-over event, so no block the side stream writes
@@ -363,47 +407,21 @@ class Muon(torch.optim.Optimizer):
             start.record(main)           # gradients, buffers and weights are ready on `main`
             side.wait_event(start)
         free = [None, None]
-        for k, (rows, cols, n_t, dev, first, has_pub, part, tile, nbytes) in enumerate(chunks):
+        for k, chunk in enumerate(chunks):
             slot = k % nslots
             ws = wss[slot]
-            L = len(part)
-            with torch.cuda.stream(side):
-                if free[slot] is not None:
-                    side.wait_event(free[slot])
-                # contiguous copies (if any) on the staging stream, ordered before the staging
-                gs = [g if g.is_contiguous() else g.contiguous() for _, g, _ in part]
-                ests = ([self.state[id(dp)]["ns_scale"].data_ptr() for dp, _, _ in part]
-                        if self._single_pass else [])
-                ptrs = _pinned_ptrs([t.data_ptr() for t in gs]
-                                    + [self.state[id(dp)]["momentum_buffer"].data_ptr()
-                                       for dp, _, _ in part] + ests, dev)
-                _C.call("dmuon_muon_stage_group", ptrs.data_ptr(), _float_dtype_code(gs[0]),
-                        ptrs.data_ptr() + 8 * L,
-                        ptrs.data_ptr() + 16 * L if ests else None, rows, cols, L, n_t, mu,
-                        int(self._nesterov), int(first), backend, self._ns_eps, ws.data_ptr(), ws.numel(), tile,
-                        side.cuda_stream)
-                if overlap:
-                    staged = torch.cuda.Event()
-                    staged.record(side)
+            if free[slot] is not None:
+                side.wait_event(free[slot])
+            self._stage_chunk(chunk, ws, side, args)
             if overlap:
+                staged = torch.cuda.Event()
+                staged.record(side)
                 main.wait_event(staged)
-            W = [dp._owned_data for dp, _, _ in part]
-            pubs = [dp.publish_target() for dp, _, _ in part] if has_pub else []
-            wptrs = _pinned_ptrs([t.data_ptr() for t in W] + [t.data_ptr() for t in pubs], dev)
-            # the forward copies (master != parameter) are written by the same epilogue
-            _C.call("dmuon_muon_apply_group", wptrs.data_ptr(), _float_dtype_code(W[0]),
-                    wptrs.data_ptr() + 8 * L if pubs else None,
-                    _float_dtype_code(pubs[0]) if pubs else 0, rows, cols, L, n_t, lr, wd,
-                    coeffs, T,
-                    backend, rst, n_rst, ws.data_ptr(), ws.numel(), tile, main.cuda_stream)
+            self._apply_chunk(chunk, ws, main, args)
             if overlap:
                 done = torch.cuda.Event()
                 done.record(main)
                 free[slot] = done
-        for c in chunks:
-            for dp, _, _ in c[6]:
-                dp._reduced_grad = None
-        return count, numel
 
     def _chunk_sizes(self, rows: int, cols: int, L: int, num_cus: int, backend: int) -> list:
         """Split a bucket of L same-shape matrices into chunks whose NS workspace fits
