@@ -8,7 +8,7 @@ between a CuTeDSL / quack SYRK and cuBLAS per shape; here one kernel family serv
 upper-triangle tiles with the mirror written by the epilogue, fp32 accumulation, fp16 or bf16
 operands (``dmuon_syrk``). Shapes the kernel cannot read in place (M not a multiple of the
 tile, K not a multiple of 64, unaligned rows) run on zero-padded copies in a workspace this
-module keeps per device, which is where the reference would fall back to cuBLAS.
+module keeps per device and stream, which is where the reference would fall back to cuBLAS.
 
 As in the reference, ``B`` other than ``A`` is allowed only when ``A @ B^T`` is symmetric (the
 caller's responsibility: only one triangle is computed), a non-K-contiguous operand is copied
@@ -32,18 +32,23 @@ _OPERAND_CODES = {torch.float16: _C.DTYPE_F16, torch.bfloat16: _C.DTYPE_BF16}
 
 
 class _ScratchCache:
-    """One growing device byte buffer per device (the padded path's operand copies). Calls run
-    on the current stream in submission order, so successive calls reuse it safely."""
+    """One growing device byte buffer per (device, stream) for the padded path's operand
+    copies. Calls on one stream run in submission order, so they reuse its buffer safely; each
+    buffer is allocated on its own stream, so when a larger one replaces it the allocator hands
+    the old memory out again only in that stream's order. (A buffer shared between streams
+    would let a call on one stream overwrite operands a call on another is still reading.)"""
 
     def __init__(self) -> None:
-        self._bufs: dict[torch.device, Tensor] = {}
+        self._bufs: dict[tuple, Tensor] = {}
 
-    def get(self, device: torch.device, nbytes: int) -> Tensor:
-        buf = self._bufs.get(device)
+    def get(self, device: torch.device, stream: "torch.cuda.Stream", nbytes: int) -> Tensor:
+        key = (device, stream.cuda_stream)
+        buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
-            self._bufs.pop(device, None)
-            buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-            self._bufs[device] = buf
+            self._bufs.pop(key, None)
+            with torch.cuda.stream(stream):
+                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
         return buf
 
 
@@ -115,17 +120,17 @@ def syrk_or_cublas(
             D.data_ptr(), D.stride(-2), _batch_stride(D), M, K, L)
     need = ctypes.c_int64()
     _C.call("dmuon_syrk_workspace_size", code, *args, int(tile), ctypes.byref(need))
-    ws = _SCRATCH.get(A.device, need.value) if need.value > 0 else None
-    stream = torch.cuda.current_stream(A.device).cuda_stream
+    stream = torch.cuda.current_stream(A.device)
+    ws = _SCRATCH.get(A.device, stream, need.value) if need.value > 0 else None
     _C.call("dmuon_syrk", code, *args, float(alpha), float(beta), float(diag_add), None,
             int(tile), None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
-            stream)
+            stream.cuda_stream)
 
 
 def get_ns_backend() -> str:
     """One-line description of the NS kernel (``syrk_dispatch.py:42-66``)."""
     return ("Gram-space NS with restarts / direct NS in SYRK form · kernel=hip_gfx950 "
-            "(MI355X CDNA4, fp16 MFMA 32x32x16)")
+            "(MI355X CDNA4, fp16 / bf16 MFMA 16x16x32)")
 
 
 def get_backend_status() -> dict:

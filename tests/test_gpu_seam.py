@@ -101,6 +101,32 @@ def test_padded_path_equals_in_place_path(gpu):
     assert torch.equal(R2, R4)
 
 
+def test_padded_path_on_two_streams(gpu):
+    """Padded-path calls issued on two streams, interleaved without waiting, each use their own
+    stream's workspace: both results equal the same calls made one after another on one
+    stream, and the two streams hold separate workspace buffers."""
+    from dmuon.optim import syrk_dispatch as sd
+    m, k = 300, 1000                            # M and K both need padding
+    Xs = [_x(m, k, 60 + i, gpu) for i in range(4)]
+    ref = []
+    for X in Xs:
+        R = torch.empty(m, m, dtype=torch.float16, device=gpu)
+        syrk_or_cublas(X, R)
+        ref.append(R)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [torch.empty(m, m, dtype=torch.float16, device=gpu) for _ in Xs]
+    for i, X in enumerate(Xs):
+        with torch.cuda.stream(s1 if i % 2 == 0 else s2):
+            syrk_or_cublas(X, outs[i])
+    torch.cuda.synchronize()
+    for o, r in zip(outs, ref):
+        assert torch.equal(o, r)
+    b1 = sd._SCRATCH._bufs[(Xs[0].device, s1.cuda_stream)]
+    b2 = sd._SCRATCH._bufs[(Xs[0].device, s2.cuda_stream)]
+    assert b1.data_ptr() != b2.data_ptr()
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_batched_and_tiles(gpu, dtype):
     L, m, n = 3, 384, 640
