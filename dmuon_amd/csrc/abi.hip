@@ -287,26 +287,44 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
                  [&] { return launch_nt(g, tile, stream); });
   };
   // Q <- P Q = Z Q + a Q as a full product (Q is a product of polynomials that no longer
-  // commute once rounded; its factor order must match R's), written with its transpose: the
-  // next update reads Q^T as the B operand. A Q that is still P itself is symmetric, so its
-  // transpose slot holds the same matrix.
-  uint16_t* qbuf[2] = {w.Q0, w.Q1};
-  const uint16_t* qtbuf[2] = {w.Q0, w.Q1};   // where the transpose of each slot's Q lives
-  auto q_update = [&](const uint16_t* Zm, int from, float a_) -> int {
+  // commute once rounded; its factor order must match R's). Z is symmetric, so the same update
+  // also runs transposed, Q^T <- Q^T Z + a Q^T, reading Q^T as its A operand and addend and
+  // writing Q^T alone. A segment's updates (between a (re)start and the Q X that consumes Q)
+  // therefore run transposed and write only Q^T, except the last two: the second-to-last writes
+  // Q^T and, as its transposed output, Q (the last one reads both), and the last runs as
+  // Z Q + a Q and writes Q, the row form Q X reads. A Q that is still P itself is symmetric: one
+  // buffer serves as both forms.
+  uint16_t* qbuf[2] = {w.Q0, w.Q1};          // row form of each slot's Q (when written)
+  const uint16_t* qtbuf[2] = {w.Q0, w.Q1};   // its transpose
+  enum { Q_TRANS = 0, Q_TRANS_BOTH = 1, Q_ROW = 2 };
+  auto q_update = [&](const uint16_t* Zm, int from, float a_, int form) -> int {
     const int to = 1 - from;
-    qtbuf[to] = to ? w.Q1T : w.Q0T;
     NtArgs g{};
     g.elt = ELT_F16;
-    g.A = Zm; g.lda = m_pad; g.sA = as;
-    g.B = qtbuf[from]; g.ldb = m_pad; g.sB = as;
     g.M = m_pad; g.N = m_pad; g.K = m_pad; g.L = batch;
     g.mt = g.nt = m_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.mode = EPI_NS; g.alpha = 1.f; g.beta = a_;
-    g.C = qbuf[from]; g.ldc = m_pad; g.sC = as;
-    g.D = qbuf[to]; g.ldd = m_pad; g.sD = as;
-    g.DT = const_cast<uint16_t*>(qtbuf[to]); g.lddt = m_pad; g.sDT = as;
+    g.lda = g.ldb = g.ldc = g.ldd = g.lddt = m_pad;
+    g.sA = g.sB = g.sC = g.sD = g.sDT = as;
+    if (form == Q_ROW) {
+      g.A = Zm; g.B = qtbuf[from]; g.C = qbuf[from];
+      g.D = qbuf[to];
+    } else {
+      uint16_t* qt_to = to ? w.Q1T : w.Q0T;
+      g.A = qtbuf[from]; g.B = Zm; g.C = qtbuf[from];
+      g.c_in = C_IS_A;                         // the addend is the A panel's last slices
+      g.D = qt_to;
+      if (form == Q_TRANS_BOTH) g.DT = qbuf[to];
+      qtbuf[to] = qt_to;
+    }
     return timed(PC_POLY, full_sq_flops, 0.0, stream, who,
                  [&] { return launch_nt(g, tile, stream); });
+  };
+  // iterations from it up to the next restart (or T): the Q updates the segment has left
+  auto updates_left = [&](int it) {
+    int end = it + 1;
+    while (end < T && !is_restart(end)) ++end;
+    return end - it;
   };
   int kr = 1;
   while (kr * 2 <= m && kr < 4096) kr *= 2;
@@ -340,7 +358,9 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
       qs = 0;
     } else {
       if (sq(R, R, R, Z, zr2, zr1, 0.f, true)) return 1;   // Z = c R^2 + b R
-      if (q_update(Z, qs, ca)) return 1;   // Q <- Z Q + a Q
+      const int left = updates_left(it);
+      const int form = left == 1 ? Q_ROW : left == 2 ? Q_TRANS_BOTH : Q_TRANS;
+      if (q_update(Z, qs, ca, form)) return 1;              // Q <- Z Q + a Q
       qs = 1 - qs;
     }
     if (evolve) {
