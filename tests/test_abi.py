@@ -20,6 +20,69 @@ def test_header_and_binding_agree():
     assert _declared() == sorted(_C.EXPORTED_SYMBOLS)
 
 
+def _header_params():
+    """name -> coarse class of each parameter ('p' pointer, 'l' int64, 'i' int, 'f' float,
+    'd' double), from the declarations in include/dmuon_amd.h."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(?:int|const char\*)\s+(dmuon_[a-z0-9_]+)\s*\(([^;]*?)\)\s*;",
+                                   text, flags=re.S):
+        cls = []
+        for prm in (q.strip() for q in params.split(",")):
+            if prm in ("", "void"):
+                continue
+            if "*" in prm:
+                cls.append("p")
+            elif prm.startswith("int64_t"):
+                cls.append("l")
+            elif prm.startswith("int"):
+                cls.append("i")
+            elif prm.startswith("float"):
+                cls.append("f")
+            elif prm.startswith("double"):
+                cls.append("d")
+            else:
+                raise AssertionError(f"{name}: unclassified parameter {prm!r}")
+        out[name] = cls
+    return out
+
+
+def _ctypes_class(t):
+    if t is ctypes.c_void_p or t is ctypes.c_char_p or isinstance(t, type) and issubclass(
+            t, ctypes._Pointer):
+        return "p"
+    return {ctypes.c_int64: "l", ctypes.c_int: "i", ctypes.c_float: "f",
+            ctypes.c_double: "d"}[t]
+
+
+def test_binding_argument_types_match_the_header():
+    """_C.py's argtypes and the INTEGRATION.md ctypes stubs take each declared parameter with
+    its width: a wrong count or a 32/64-bit mix-up would pass garbage through ctypes."""
+    hdr = _header_params()
+    assert set(hdr) == set(_C.EXPORTED_SYMBOLS)
+    for name, (_, argtypes) in _C._SIGNATURES.items():
+        assert [_ctypes_class(t) for t in argtypes] == hdr[name], name
+    doc = (HEADER.parent.parent / "INTEGRATION.md").read_text()
+    cls = {"_vp": "p", "_i64": "l", "_i": "i", "_f": "f", "_d": "d",
+           "ctypes.POINTER(_i64)": "p"}
+    stubs = re.findall(r"_lib\.(dmuon_[a-z0-9_]+)\.argtypes = ([^\n]*(?:\n {20,}[^\n]*)*)", doc)
+    assert len(stubs) >= 5
+    for name, expr in stubs:
+        expr = " ".join(expr.split())
+        parts = []
+        for m in re.finditer(r"\[([^\]]*)\](?: \* (\d+))?", expr):
+            items = [cls[t.strip()] for t in m.group(1).split(",") if t.strip()]
+            parts += items * int(m.group(2) or 1)
+        assert parts == hdr[name], name
+
+
+def test_docs_cite_the_abi_version():
+    version = re.search(r"#define DMUON_ABI_VERSION (\d+)", HEADER.read_text()).group(1)
+    root = HEADER.parent.parent
+    assert f"DMUON_ABI_VERSION` {version}" in (root / "DESIGN.md").read_text()
+    assert f"dmuon_abi_version() == {version}" in (root / "INTEGRATION.md").read_text()
+
+
 def test_library_exports_every_declared_symbol():
     lib = _C.lib()
     for name in _declared():
