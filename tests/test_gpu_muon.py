@@ -115,6 +115,44 @@ def test_multi_step_momentum_and_update(gpu):
             W[i] = Wg.copy()
 
 
+@pytest.mark.parametrize("backend", ["gram", "direct"])
+def test_zero_and_non_contiguous_gradients(gpu, backend):
+    """One group of three 256x640 fp32 weights over two steps: an all-zero gradient (the
+    normaliser divides by eps and the NS input is exactly zero, so the weight only decays, bit
+    for bit, and its momentum stays zero), a gradient given as a transposed view (not
+    contiguous: the same bits as the same values given contiguously) and an ordinary one."""
+    shapes = [(256, 640)] * 3
+    lr, mu, wd = 0.02, 0.95, 0.1
+    runs = []
+    for view in (False, True):
+        m = Mats(shapes, torch.float32, gpu, seed=11)
+        dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2)
+        dmuon.replicate(m)
+        opt = dmuon.Muon(m, lr=lr, momentum=mu, weight_decay=wd, ns_backend=backend)
+        ps = list(m.parameters())
+        W0 = ps[0].detach().cpu().clone()
+        gen = torch.Generator().manual_seed(5)
+        for step in range(2):
+            g1 = (torch.randn(640, 256, generator=gen) * 0.02).to(gpu)
+            g2 = (torch.randn(256, 640, generator=gen) * 0.02).to(gpu)
+            ps[0].grad = torch.zeros(256, 640, device=gpu)
+            ps[1].grad = g1.t() if view else g1.t().contiguous()
+            assert ps[1].grad.is_contiguous() != view
+            ps[2].grad = g2
+            opt.step()
+        torch.cuda.synchronize()
+        dps = dmuon.get_owned_params(m)
+        bufs = [opt.state[id(dp)]["momentum_buffer"].detach().clone() for dp in dps]
+        runs.append(([p.detach().clone() for p in ps], bufs))
+        dec = torch.tensor(np.float32(1.0 - lr * wd))
+        assert torch.equal(ps[0].detach().cpu(), (W0 * dec) * dec)
+        assert torch.count_nonzero(bufs[0]) == 0
+        assert torch.isfinite(ps[1]).all() and not torch.equal(ps[1].detach().cpu(), ps[0].detach().cpu())
+    for a, b in zip(runs[0], runs[1]):
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+
+
 @pytest.mark.parametrize("shapes", [
     [(256, 4096), (4096, 256), (1024, 3584), (3584, 1024), (512, 2048)],   # c3 aspect ratios / 4
     [(176, 256)] * 8 + [(256, 176)] * 8,                                    # c4 MoE batch / 8
