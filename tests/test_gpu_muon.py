@@ -225,6 +225,38 @@ def test_c5_layer_full_size_bit_exact_chain(gpu, backend):
             assert torch.equal(ps[i].detach().cpu(), exp), shape
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_update_without_weight_decay_bit_exact(gpu, dtype):
+    """weight_decay=0: the reference skips W *= 1 - lr*wd (muon.py:1733-1734) and the fused
+    epilogue skips the decay rounding; the weight is W - lr*s*U in one FMA, bit for bit, with
+    U from the stand-alone NS entry point (Gram, the reference defaults)."""
+    lr, mu = 0.02, 0.95
+    shapes = [(256, 640), (640, 256), (384, 384)]
+    m = Mats(shapes, dtype, gpu, seed=4)
+    dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2,
+                          param_policy=BF16_MASTER if dtype == torch.bfloat16 else None)
+    dmuon.replicate(m)
+    ns = dmuon.NewtonSchulz("gram")
+    opt = dmuon.Muon(m, ns_backend=ns, lr=lr, momentum=mu, weight_decay=0.0,
+                     single_pass_staging=False)
+    ps = list(m.parameters())
+    dps = dmuon.get_owned_params(m)
+    W0 = [p.detach().clone() for p in ps]
+    gs = [g.to(gpu) for g in _grads(m, seed=9)]
+    opt.step()
+    torch.cuda.synchronize()
+    for i, p in enumerate(ps):
+        ns_in = _fma(mu, gs[i].float(), gs[i]).to(gpu)      # first step: buf = g
+        (u,) = newton_schulz_batched([ns_in], ns.resolved_coefficients(), backend=ns.backend,
+                                     restart_iterations=ns.restart_iterations)
+        rows, cols = p.shape
+        lrs = np.float32(lr * (0.2 * math.sqrt(max(rows, cols))))
+        exp = _fma(-lrs, u, W0[i].float())
+        exp = exp.to(torch.bfloat16) if dtype == torch.bfloat16 else exp
+        assert torch.equal(p.detach().cpu(), exp), (p.shape, dtype)
+        assert torch.equal(opt.state[id(dps[i])]["momentum_buffer"], gs[i].float())
+
+
 # ------------------------------------------------------------ Gram NS backend (the default)
 @pytest.mark.parametrize("shapes,dtype", [
     ([(256, 1024), (1024, 256), (300, 1000)], torch.float32),

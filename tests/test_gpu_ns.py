@@ -76,6 +76,23 @@ def test_gram_device_path_vs_oracle(gpu, shape, restart):
     assert e_cf < BF16_TOL
 
 
+@pytest.mark.parametrize("T,restart", [(1, []), (2, []), (2, [1]), (3, [1]), (3, [2])])
+def test_gram_short_schedules(gpu, T, restart):
+    """Coefficient lists shorter than five steps (the first T Polar-Express triples), with and
+    without a restart: a segment with no Q update, one or two, and a restart right before the
+    last step, against the restatement of the device pipeline and the closed form."""
+    coeffs = o.POLAR_EXPRESS[:T]
+    G = _g((256, 768), seed=T * 10 + len(restart))
+    U = dmuon.gram_newton_schulz(G.to(gpu), coefficients=[tuple(c) for c in coeffs],
+                                 restart_iterations=restart).cpu().numpy()
+    Gn = G.numpy()
+    e_self = o.rel_fro(U, o.syrk_emulated_gram_ns(Gn, coeffs, restart))
+    e_cf = o.rel_fro(U, o.closed_form_ns(Gn, coeffs))
+    print(f"T={T} restarts {restart}: vs restatement {e_self:.2e}, vs closed form {e_cf:.2e}")
+    assert e_self < SELF_TOL
+    assert e_cf < BF16_TOL
+
+
 def test_gram_batched_keller_and_ragged(gpu):
     Gs = [_g((256, 640), seed=s) for s in range(3)]
     outs = newton_schulz_batched([g.to(gpu) for g in Gs], o.KELLER, backend="gram",
