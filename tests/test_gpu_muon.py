@@ -115,6 +115,42 @@ def test_multi_step_momentum_and_update(gpu):
             W[i] = Wg.copy()
 
 
+def test_param_groups_and_plain_momentum(gpu):
+    """User param_groups with their own lr / momentum / weight_decay (muon.py:598-616, read per
+    group in _step_muon_params :1586-1588) and nesterov=False (the NS input is the buffer
+    itself, :1693-1694): momentum bit-exact per group, each weight against the oracle's step
+    with its group's hyperparameters, over two steps."""
+    shapes = [(256, 640), (640, 256), (256, 640), (384, 384)]
+    m = Mats(shapes, torch.float32, gpu, seed=8)
+    dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2)
+    dmuon.replicate(m)
+    ps = list(m.parameters())
+    hp = [dict(lr=0.02, momentum=0.95, weight_decay=0.1), dict(lr=0.01, momentum=0.9,
+                                                            weight_decay=0.0)]
+    groups = [dict(params=[ps[0], ps[1]], **hp[0]), dict(params=[ps[2], ps[3]], **hp[1])]
+    opt = dmuon.Muon(m, param_groups=groups, nesterov=False,
+                     ns_backend=dmuon.NewtonSchulz("direct", coefficients=dmuon.KELLER_COEFFICIENTS))
+    muon_groups = [g for g in opt.param_groups if g.get("use_muon")]
+    assert [g["lr"] for g in muon_groups] == [0.02, 0.01]
+    W = [p.detach().cpu().numpy().copy() for p in ps]
+    bufs = [None] * 4
+    dps = dmuon.get_owned_params(m)
+    for step in range(2):
+        gs = _grads(m, seed=40 + step)
+        opt.step()
+        for i, (p, g) in enumerate(zip(ps, gs)):
+            h = hp[i // 2]
+            Wn, bufs[i], _ = o.muon_step(W[i], g.numpy(), bufs[i], lr=h["lr"], mu=h["momentum"],
+                                         wd=h["weight_decay"], nesterov=False,
+                                         coefficients=o.KELLER, ns="syrk")
+            gb = opt.state[id(dps[i])]["momentum_buffer"].cpu().numpy()
+            assert np.array_equal(gb, bufs[i]), (step, i)
+            Wg = p.detach().cpu().numpy()
+            dec = np.float32(1 - h["lr"] * h["weight_decay"])
+            assert o.rel_fro(Wg - W[i] * dec, Wn - W[i] * dec) < 1e-2, (step, i)
+            W[i] = Wg.copy()
+
+
 @pytest.mark.parametrize("backend", ["gram", "direct"])
 def test_zero_and_non_contiguous_gradients(gpu, backend):
     """One group of three 256x640 fp32 weights over two steps: an all-zero gradient (the
