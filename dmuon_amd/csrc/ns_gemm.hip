@@ -18,9 +18,12 @@
 //     the operands, so barrier and memory waits overlap MFMA work;
 //   128x128 tiles (nt_mfma_kernel): 4 waves of 64x64, two blocks per CU, for batches too small
 //     to fill the machine with 256-tiles; fragments double-buffered per substep, one barrier
-//     per slice.
+//     per slice. A launch with no more tiles than CUs runs one block per CU with a four-slot
+//     ring instead (three slices in flight: such a loop waits on load latency, not bandwidth);
+//     the ring depth changes where operands wait, not the arithmetic, so both give the same bits.
 #include "dmuon_amd_internal.h"
 
+#include <atomic>
 #include <type_traits>
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -245,10 +248,13 @@ __device__ __forceinline__ void sched_substeps() {
 }
 
 // Waves per SIMD: a 128x128 wave tile holds 256 accumulator registers, so its block runs one
-// wave per SIMD with the whole 512-entry register file; smaller wave tiles run two.
-template <int BM, int BN, int WM, int WN>
+// wave per SIMD with the whole 512-entry register file; smaller wave tiles run two, unless the
+// block's LDS (more than half of the CU's 160 KiB) leaves room for one block per CU only.
+template <int BM, int BN, int BK, int S, int WM, int WN>
 struct Occupancy {
-  static constexpr int WPE = (BM / WM) * (BN / WN) >= 128 * 128 ? 1 : 2;
+  static constexpr int WPE =
+      (BM / WM) * (BN / WN) >= 128 * 128 || Tile<BM, BN, BK, S, WM, WN>::LDS_BYTES > 80 * 1024
+          ? 1 : 2;
 };
 
 // First K slice of the tile's loop (see NtArgs::c_in): the slices that hold the tile's addend
@@ -694,7 +700,8 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
 
 template <int BM, int BN, int BK, int S, int WM, int WN, int MODE, int E, bool BKM>
 __global__ __launch_bounds__(64 * WM * WN)
-__attribute__((amdgpu_waves_per_eu(Occupancy<BM, BN, WM, WN>::WPE, Occupancy<BM, BN, WM, WN>::WPE)))
+__attribute__((amdgpu_waves_per_eu(Occupancy<BM, BN, BK, S, WM, WN>::WPE,
+                                   Occupancy<BM, BN, BK, S, WM, WN>::WPE)))
 void nt_mfma_kernel(const NtArgs a) {
   using T = Tile<BM, BN, BK, S, WM, WN>;
   __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
@@ -1081,6 +1088,20 @@ void nt_pp_kernel(const NtArgs a) {
                           wj);
 }
 
+// Compute units of the current device, queried once per device (0 if the query fails).
+int current_device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int v = cus[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cus[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 }  // namespace
 
 hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
@@ -1128,15 +1149,19 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
     else DMUON_PP3(E, false);                                                                  \
   } while (0)
   // 256-tiles: the ping-pong kernel, 8 waves, 64-wide K slices in a two-slot ring; 128-tiles:
-  // 4 waves, two blocks per CU. Measured and not kept: 32-wide slices in a four-slot ring for the
+  // 4 waves, two blocks per CU, or, when every tile has a CU to itself, one block per CU with a
+  // four-slot ring (128 KiB). Measured and not kept: 32-wide slices in a four-slot ring for the
   // ping-pong kernel (7-12% slower: twice the phases and barriers), the in-phase 8-wave schedule
   // it replaced (3-11% slower on the c5 product shapes), 256-tiles of 4 waves with 128x128 per
   // wave, and 32x32x16 MFMAs (identical results; 5-15% slower under the board power limit).
+  const bool deep = tile != 256 && nb <= current_device_cus();
   if (a.elt == ELT_F16) {
     if (tile == 256) DMUON_PP(ELT_F16);
+    else if (deep) DMUON_NT(128, 64, 4, 2, 2, ELT_F16);
     else DMUON_NT(128, 64, 2, 2, 2, ELT_F16);
   } else {
     if (tile == 256) DMUON_PP(ELT_BF16);
+    else if (deep) DMUON_NT(128, 64, 4, 2, 2, ELT_BF16);
     else DMUON_NT(128, 64, 2, 2, 2, ELT_BF16);
   }
 #undef DMUON_NT
