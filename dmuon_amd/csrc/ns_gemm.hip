@@ -167,7 +167,7 @@ struct Tile {
   static constexpr int EPI_REGION = (EPI_REGION_RAW + 15) / 16 * 16;
   static constexpr int LDS_BYTES = (S * STAGE > NW * EPI_REGION ? S * STAGE : NW * EPI_REGION);
   static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0, "tile rows vs DMA rows");
-  static_assert((S - 1) * LPT <= 63 && S <= 4, "vmcnt range");
+  static_assert(S * LPT <= 63 && S <= 8, "vmcnt range (the prologue has S slices in flight)");
   // LDS slot of 16-byte chunk kc of row r. A ds_read_b128 serves 16 lanes (256 B, all 64
   // banks) per pass; a fragment read has those 16 lanes on 16 consecutive rows at one chunk,
   // so rows sharing a bank line (r % RPL) must take distinct slots along r / RPL.
@@ -202,12 +202,10 @@ __device__ __forceinline__ void phase_barrier() {
 }
 
 template <class T>
-__device__ __forceinline__ void wait_slices(int ahead) {
-  // wait until at most `ahead` newer slices (T::LPT loads each) are still in flight
-  if constexpr (3 * T::LPT <= 63) { if (ahead >= 3) { wait_vmcnt<3 * T::LPT>(); return; } }
-  if constexpr (2 * T::LPT <= 63) { if (ahead >= 2) { wait_vmcnt<2 * T::LPT>(); return; } }
-  if (ahead >= 1) { wait_vmcnt<T::LPT>(); return; }
-  wait_vmcnt<0>();
+__device__ __forceinline__ void wait_slices() {
+  // wait until slice 0 of the ring has landed: at most S - 1 newer slices (T::LPT loads each)
+  // still in flight
+  wait_vmcnt<(T::S - 1) * T::LPT>();
 }
 
 // End-of-slice meeting point: wait until at most N loads of this wave are in flight (its share
@@ -831,7 +829,7 @@ void nt_mfma_kernel(const NtArgs a) {
   // which keeps the number of loads per iteration, and so the vmcnt targets, uniform.
 #pragma unroll
   for (int s0 = 0; s0 < S; ++s0) DMUON_ISSUE(rot(min(s0, KT - 1)), s0);
-  wait_slices<T>(S - 1);
+  wait_slices<T>();
   bare_barrier();
   load_frags(smem, smem + T::A_BYTES, 0, af[0], bfr[0]);
 
@@ -1154,7 +1152,39 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   // ping-pong kernel (7-12% slower: twice the phases and barriers), the in-phase 8-wave schedule
   // it replaced (3-11% slower on the c5 product shapes), 256-tiles of 4 waves with 128x128 per
   // wave, and 32x32x16 MFMAs (identical results; 5-15% slower under the board power limit).
-  const bool deep = tile != 256 && nb <= current_device_cus();
+  const int cus = current_device_cus();
+  if (tile == 128 && !a.b_kmajor) {
+    // The same products on 64x64 tiles (2 waves of 64x32, a seven-slot ring of 16 KiB slots,
+    // one block per CU) when those still fit one wave of blocks on the device: four times the
+    // CUs on a launch that waits on load latency. Every value keeps its K order -- the slice
+    // rotation depends only on the 256-aligned block of the tile's columns -- so the bits match
+    // the 128-tile kernel's.
+    NtArgs s = a;
+    s.mt = 2 * a.mt;
+    s.nt = 2 * a.nt;
+    s.tiles_per_mat = a.tri ? s.mt * (s.mt + 1) / 2 : s.mt * s.nt;
+    const long long nb64 = (long long)s.tiles_per_mat * a.L;
+    if (nb64 <= cus) {
+      dim3 g64((unsigned)nb64), b64(128);
+#define DMUON_NT64(E)                                                                          \
+  do {                                                                                         \
+    if (s.mode == EPI_SYM)                                                                     \
+      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_SYM, E, false>), g64, b64, 0, \
+                         stream, s);                                                           \
+    else if (s.mode == EPI_NS)                                                                 \
+      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_NS, E, false>), g64, b64, 0,  \
+                         stream, s);                                                           \
+    else                                                                                       \
+      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_FINAL, E, false>), g64, b64,  \
+                         0, stream, s);                                                        \
+  } while (0)
+      if (a.elt == ELT_F16) DMUON_NT64(ELT_F16);
+      else DMUON_NT64(ELT_BF16);
+#undef DMUON_NT64
+      return hipGetLastError();
+    }
+  }
+  const bool deep = tile != 256 && nb <= cus;
   if (a.elt == ELT_F16) {
     if (tile == 256) DMUON_PP(ELT_F16);
     else if (deep) DMUON_NT(128, 64, 4, 2, 2, ELT_F16);
