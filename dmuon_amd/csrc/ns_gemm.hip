@@ -1153,6 +1153,24 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   // it replaced (3-11% slower on the c5 product shapes), 256-tiles of 4 waves with 128x128 per
   // wave, and 32x32x16 MFMAs (identical results; 5-15% slower under the board power limit).
   const int cus = current_device_cus();
+  if (tile == 128 && a.M % 256 == 0 && a.N % 256 == 0 && cus > 0) {
+    // A launch of more than two 128-tiles per CU whose result also splits into 256-tiles runs
+    // on the ping-pong kernel when that takes fewer units of work per CU, by the cost model of
+    // the planner (a wave of 256-tiles: 4 units; a wave of two 128-tiles per CU: 2.7). With
+    // both sides multiples of 256 the two kernels give the same bits, so only the time changes
+    // (e.g. Q X of one 1024 x 16384 matrix: 256 tiles in one wave instead of 1024 in two).
+    const int mt2 = a.M / 256, nt2 = a.N / 256;
+    const long long n256 = (long long)(a.tri ? mt2 * (mt2 + 1) / 2 : mt2 * nt2) * a.L;
+    const double c256 = 4.0 * (double)((n256 + cus - 1) / cus);
+    const double c128 = 2.7 * (double)((nb + 2LL * cus - 1) / (2LL * cus));
+    if (nb > 2LL * cus && c256 < c128) {
+      NtArgs s = a;
+      s.mt = mt2;
+      s.nt = nt2;
+      s.tiles_per_mat = (int)(n256 / a.L);
+      return launch_nt(s, 256, stream);
+    }
+  }
   if (tile == 128 && !a.b_kmajor) {
     // The same products on 64x64 tiles (2 waves of 64x32, a seven-slot ring of 16 KiB slots,
     // one block per CU) when those still fit one wave of blocks on the device: four times the
