@@ -18,9 +18,11 @@
 //     the operands, so barrier and memory waits overlap MFMA work;
 //   128x128 tiles (nt_mfma_kernel): 4 waves of 64x64, two blocks per CU, for batches too small
 //     to fill the machine with 256-tiles; fragments double-buffered per substep, one barrier
-//     per slice. A launch with no more tiles than CUs runs one block per CU with a four-slot
-//     ring instead (three slices in flight: such a loop waits on load latency, not bandwidth);
-//     the ring depth changes where operands wait, not the arithmetic, so both give the same bits.
+//     per slice. Per launch (launch_nt), a 128-tile product that leaves CUs idle runs on 64x64
+//     tiles (2 waves, seven-slot ring) or with a four-slot ring, one block per CU, and one with
+//     more than two 128-tiles per CU may take 256-tiles: such small launches wait on load
+//     latency, not bandwidth. Tile size and ring depth change where operands wait, not the
+//     arithmetic, so every variant gives the same bits.
 #include "dmuon_amd_internal.h"
 
 #include <atomic>
