@@ -141,6 +141,83 @@ def test_batched_and_tiles(gpu, dtype):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
+def _variant(n64, n128, n256, cus):
+    """The kernel launch_nt runs for a 128-tile plan with both sides multiples of 256, from the
+    launch's tile counts: 256-tiles when there are more than two 128-tiles per CU and the
+    planner's cost model (4 units per wave of 256-tiles, 2.7 per wave of two 128-tiles per CU)
+    favours them, else 64-tiles when those fit one block per CU, else the four-slot 128-tile
+    ring when the 128-tiles do, else two 128-tile blocks per CU."""
+    if n128 > 2 * cus and 4 * -(-n256 // cus) < 2.7 * -(-n128 // (2 * cus)):
+        return "256"
+    if n64 <= cus:
+        return "64"
+    return "128x4" if n128 <= cus else "128x2"
+
+
+def _batches_per_variant(per64, per128, per256, cus):
+    """The smallest batch size that selects each of the four variants."""
+    found = {}
+    for L in range(1, 64):
+        v = _variant(L * per64, L * per128, L * per256, cus)
+        found.setdefault(v, L)
+    return found
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_small_launch_variants_same_bits(gpu, dtype):
+    """One 1024 x 1024 product replicated in batches sized so that launch_nt runs it on each
+    of its kernels for a 128-tile plan -- 64-tiles, 128-tiles with a four-slot ring, 128-tiles
+    two per CU, 256-tiles -- for the triangle product with its addend (Z = c R R^T + b R, C = R),
+    the full NS product (X' = s (P X + beta X) with X'^T) and the fused final weight update:
+    every variant must give the same bits for every matrix of every batch."""
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    m = 1024
+    a, b, c = PE[0]
+    tri = _batches_per_variant(16 * 17 // 2, 8 * 9 // 2, 4 * 5 // 2, cus)
+    full = _batches_per_variant(16 * 16, 8 * 8, 4 * 4, cus)
+    if len(tri) < 4 or len(full) < 4:
+        pytest.skip(f"{cus} CUs: not every launch variant is reachable with 1024^2 products")
+    R = torch.empty(m, m, dtype=dtype, device=gpu)
+    syrk_or_cublas(_x(m, 2 * m, 71, gpu, dtype), R)
+    zs = {}
+    for v, L in tri.items():
+        Rb = R.expand(L, m, m).contiguous()
+        Zb = torch.empty_like(Rb)
+        syrk_or_cublas(Rb, Zb, C=Rb, alpha=c, beta=b, tile=128)
+        torch.cuda.synchronize()
+        assert all(torch.equal(Zb[i], Zb[0]) for i in range(L)), v
+        zs[v] = Zb[0].clone()
+    assert all(torch.equal(z, zs["64"]) for z in zs.values()), {v: L for v, L in tri.items()}
+    _check_close(zs["64"], c * _mm(R, R) + b * R.float())
+
+    code = _C.DTYPE_F16 if dtype == torch.float16 else _C.DTYPE_BF16
+    g = torch.Generator().manual_seed(8)
+    P = (torch.randn(m, m, generator=g) * 0.05).to(dtype).to(gpu)
+    X = (torch.randn(m, m, generator=g) * 0.05).to(dtype).to(gpu)
+    W0 = (torch.randn(m - 3, m - 5, generator=g) * 0.02).to(gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+    xs, ws = {}, {}
+    for v, L in full.items():
+        Pb, Xb = P.expand(L, m, m).contiguous(), X.expand(L, m, m).contiguous()
+        XTb = Xb.transpose(1, 2).contiguous()
+        Xo, XTo = torch.empty_like(Xb), torch.empty_like(Xb)
+        _C.call("dmuon_ns_gemm", code, Pb.data_ptr(), m, m * m, XTb.data_ptr(), m, m * m,
+                Xb.data_ptr(), m, m * m, Xo.data_ptr(), m, m * m, XTo.data_ptr(), m, m * m, m,
+                m, L, 0.5, a, None, 128, stream)
+        W = [W0.clone() for _ in range(L)]
+        wp = torch.tensor([w.data_ptr() for w in W], dtype=torch.int64, device=gpu)
+        _C.call("dmuon_ns_gemm_final", code, Pb.data_ptr(), m, m * m, XTb.data_ptr(), m, m * m,
+                Xb.data_ptr(), m, m * m, m, m, L, 0.25, 1.5, None, m - 3, m - 5, 0, None, 0,
+                wp.data_ptr(), _C.DTYPE_F32, None, 0, 0.998, 0.01, 128, stream)
+        torch.cuda.synchronize()
+        assert all(torch.equal(Xo[i], Xo[0]) and torch.equal(W[i], W[0]) for i in range(L)), v
+        assert torch.equal(XTo[0], Xo[0].t()), v
+        xs[v], ws[v] = Xo[0].clone(), W[0].clone()
+    assert all(torch.equal(x, xs["64"]) for x in xs.values()), {v: L for v, L in full.items()}
+    assert all(torch.equal(w, ws["64"]) for w in ws.values())
+    _check_close(xs["64"], 0.5 * (_mm(P, X) + a * X.float()))
+
+
 def test_seam_argument_errors(gpu, caplog):
     X = _x(128, 256, 9, gpu)
     R = torch.empty(128, 128, dtype=torch.float16, device=gpu)
