@@ -107,7 +107,9 @@ int dmuon_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
  * symmetric (always true for B = A; the caller guarantees it when B != A, as syrk_or_cublas
  * requires). Only the upper triangle of tiles is computed; the lower triangle is written as its
  * mirror. C may be NULL (then beta is ignored) and may alias A, but D must not alias A, B or C.
- * tile: 0 (automatic), 128 or 256 (output tile edge).
+ * tile: 0 (automatic), 128 or 256 (output tile edge of the plan: padding and operand
+ * alignment). A launch of a 128-tile plan may run on 64- or 256-tiles when those fit the device
+ * better, with the same bits as the 128-tile kernel.
  * Any M >= 0 and K >= 0 are accepted. When M is a multiple of the tile, K of 64, and every base
  * is 16-byte aligned with leading dimensions and batch strides that are multiples of 8, the
  * kernel reads the operands in place and `workspace` may be NULL; otherwise the call runs on
