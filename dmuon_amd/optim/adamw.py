@@ -58,6 +58,11 @@ def fused_adamw_(params: Sequence[Tensor], grads: Sequence[Tensor], exp_avgs: Se
     dev = params[0].device
     if dev.type != "cuda":
         raise RuntimeError("fused_adamw_: tensors must live on the GPU (HIP kernel only)")
+    if torch.cuda.is_current_stream_capturing():
+        # the bias correction follows the host step count and the job table is copied from a
+        # temporary host buffer: a replay would repeat a stale step from freed memory
+        raise RuntimeError("fused_adamw_ cannot be captured into a graph (host step count and "
+                           "per-call job table); step AdamW-routed parameters eagerly")
     pdt, gdt = params[0].dtype, grads[0].dtype
     if pdt not in _CODES or gdt not in _CODES:
         raise ValueError(f"fused_adamw_: unsupported dtypes param {pdt}, grad {gdt}")

@@ -83,7 +83,11 @@ class Muon(torch.optim.Optimizer):
     the first NS products correct the estimate exactly when it is within a factor of 4 of the
     new scale, and the operand is staged again otherwise (always on a parameter's first step).
     This saves the second pass over the gradient and the momentum buffer; results differ from
-    ``single_pass_staging=False`` by the fp16 rounding of that operand.
+    ``single_pass_staging=False`` by the fp16 rounding of that operand. After one eager step a
+    step of the Muon groups copies nothing to the device (the kernels' pointer tables are kept
+    per chunk until a tensor moves), so a caller may capture it into a graph
+    (``torch.cuda.graph``) with gradients written into the same tensors between replays;
+    AdamW-routed parameters cannot be captured (host step count).
     """
 
     def __init__(
@@ -126,6 +130,7 @@ class Muon(torch.optim.Optimizer):
         self._record_step_profile = bool(record_step_profile)
         self._workspace_limit = int(workspace_limit_bytes)
         self._workspaces: list = [None, None]
+        self._ptr_tables: dict = {}
         self._overlap_staging = bool(overlap_staging)
         self._single_pass = bool(single_pass_staging)
         self._side_streams: dict = {}
@@ -366,9 +371,10 @@ class Muon(torch.optim.Optimizer):
             gs = [g if g.is_contiguous() else g.contiguous() for _, g, _ in part]
             ests = ([self.state[id(dp)]["ns_scale"].data_ptr() for dp, _, _ in part]
                     if self._single_pass else [])
-            ptrs = _pinned_ptrs([t.data_ptr() for t in gs]
-                                + [self.state[id(dp)]["momentum_buffer"].data_ptr()
-                                   for dp, _, _ in part] + ests, dev)
+            ptrs = self._ptr_table(("stage",) + tuple(id(dp) for dp, _, _ in part),
+                                   [t.data_ptr() for t in gs]
+                                   + [self.state[id(dp)]["momentum_buffer"].data_ptr()
+                                      for dp, _, _ in part] + ests, dev)
             _C.call("dmuon_muon_stage_group", ptrs.data_ptr(), _float_dtype_code(gs[0]),
                     ptrs.data_ptr() + 8 * L,
                     ptrs.data_ptr() + 16 * L if ests else None, rows, cols, L, n_t, mu,
@@ -383,13 +389,34 @@ class Muon(torch.optim.Optimizer):
         with torch.cuda.stream(stream):
             W = [dp._owned_data for dp, _, _ in part]
             pubs = [dp.publish_target() for dp, _, _ in part] if has_pub else []
-            wptrs = _pinned_ptrs([t.data_ptr() for t in W] + [t.data_ptr() for t in pubs], dev)
+            wptrs = self._ptr_table(("apply",) + tuple(id(dp) for dp, _, _ in part),
+                                    [t.data_ptr() for t in W] + [t.data_ptr() for t in pubs],
+                                    dev)
             # the forward copies (master != parameter) are written by the same epilogue
             _C.call("dmuon_muon_apply_group", wptrs.data_ptr(), _float_dtype_code(W[0]),
                     wptrs.data_ptr() + 8 * L if pubs else None,
                     _float_dtype_code(pubs[0]) if pubs else 0, rows, cols, L, n_t, lr, wd,
                     coeffs, T, backend, rst, n_rst, ws.data_ptr(), ws.numel(), tile,
                     stream.cuda_stream)
+
+    def _ptr_table(self, slot: tuple, ptrs: list, device: torch.device) -> Tensor:
+        """The device array of ``ptrs`` (int64 addresses) that a group entry point reads, kept
+        per ``slot`` (role and the chunk's parameters) and rebuilt only when an address
+        changes: a steady-state step copies nothing to the device, which also lets a caller
+        capture it into a graph after one eager step. The array is built on the current
+        stream, so a replaced one returns to the allocator in that stream's order."""
+        key = tuple(ptrs)
+        hit = self._ptr_tables.get(slot)
+        if hit is not None and hit[0] == key and hit[1].device == device:
+            return hit[1]
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                "Muon.step under graph capture: a weight, gradient or state tensor moved since "
+                "the last eager step (its pointer table would be copied from a temporary host "
+                "buffer); run one eager step with the same tensors before capturing")
+        table = _pinned_ptrs(list(key), device)
+        self._ptr_tables[slot] = (key, table)
+        return table
 
     def _run_pipeline(self, chunks, dev, main, args) -> None:
         """The chunks one after another on ``main``; with ``overlap_staging`` chunk k+1 is

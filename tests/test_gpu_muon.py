@@ -609,3 +609,67 @@ def test_mixed_orientation_group_matches_per_orientation_runs(gpu, backend):
     for field in range(3):
         for i in range(len(shapes)):
             assert torch.equal(mixed[field][i], small[field][i]), (field, shapes[i])
+
+
+# ------------------------------------------------------------------------ graph capture
+@pytest.mark.parametrize("backend", ["gram", "direct"])
+def test_step_graph_capture_replays_bit_exact(gpu, backend, monkeypatch):
+    """Muon.step captured into a graph after eager steps (the steady state copies no pointer
+    tables): each replay, with new gradient values written into the same gradient tensors and
+    the program's own eager work and synchronisations in between, gives the weights and
+    momentum of an eager twin optimizer bit for bit. A capture whose tensors moved since the
+    last eager step raises instead of recording a copy from a temporary host buffer."""
+    shapes = [(256, 640), (640, 256), (384, 384), (130, 250)]
+    twins = []
+    for _ in range(2):
+        m = Mats(shapes, torch.bfloat16, gpu, seed=21)
+        dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2, param_policy=BF16_MASTER)
+        dmuon.replicate(m)
+        opt = dmuon.Muon(m, lr=0.02, momentum=0.95, weight_decay=0.1,
+                         ns_backend=dmuon.NewtonSchulz(backend))
+        twins.append((m, opt))
+    (ma, opta), (mb, optb) = twins
+    gen = torch.Generator().manual_seed(22)
+
+    def new_grads():
+        gs = [(torch.randn(s, generator=gen) * 0.02).to(torch.bfloat16) for s in shapes]
+        for p, g in zip(ma.parameters(), gs):
+            if p.grad is None:
+                p.grad = g.to(gpu)
+            else:
+                p.grad.copy_(g)                   # same tensor: the graph reads its address
+        for p, g in zip(mb.parameters(), gs):
+            p.grad = g.to(gpu)
+
+    def same():
+        torch.cuda.synchronize()
+        for pa, pb in zip(ma.parameters(), mb.parameters()):
+            assert torch.equal(pa, pb)
+        for da, db in zip(dmuon.get_owned_params(ma), dmuon.get_owned_params(mb)):
+            assert torch.equal(opta.state[id(da)]["momentum_buffer"],
+                               optb.state[id(db)]["momentum_buffer"])
+
+    for _ in range(2):                            # eager steps: state, workspace, tables
+        new_grads()
+        opta.step()
+        optb.step()
+    same()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        opta.step()
+    for _ in range(3):
+        new_grads()
+        graph.replay()
+        optb.step()
+        same()
+    # a moved gradient (new tensor) while the stream reports a capture is refused before its
+    # pointer table is copied
+    list(ma.parameters())[0].grad = list(ma.parameters())[0].grad.clone()
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    with pytest.raises(RuntimeError, match="graph capture"):
+        opta.step()
+    # AdamW (host step count, per-call job table) refuses capture outright
+    z = [torch.zeros(4, device=gpu)]
+    with pytest.raises(RuntimeError, match="cannot be captured"):
+        dmuon.fused_adamw_(z, z, z, z, step=1, lr=1e-3, betas=(0.9, 0.999), weight_decay=0.0,
+                           eps=1e-8)
