@@ -612,8 +612,9 @@ def test_mixed_orientation_group_matches_per_orientation_runs(gpu, backend):
 
 
 # ------------------------------------------------------------------------ graph capture
+@pytest.mark.parametrize("policy", ["bf16_master", "fp32_master_publish"])
 @pytest.mark.parametrize("backend", ["gram", "direct"])
-def test_step_graph_capture_replays_bit_exact(gpu, backend, monkeypatch):
+def test_step_graph_capture_replays_bit_exact(gpu, backend, policy, monkeypatch):
     """Muon.step captured into a graph after eager steps (the steady state copies no pointer
     tables): each replay, with new gradient values written into the same gradient tensors and
     the program's own eager work and synchronisations in between, gives the weights and
@@ -623,7 +624,8 @@ def test_step_graph_capture_replays_bit_exact(gpu, backend, monkeypatch):
     twins = []
     for _ in range(2):
         m = Mats(shapes, torch.bfloat16, gpu, seed=21)
-        dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2, param_policy=BF16_MASTER)
+        dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2,
+                              param_policy=BF16_MASTER if policy == "bf16_master" else None)
         dmuon.replicate(m)
         opt = dmuon.Muon(m, lr=0.02, momentum=0.95, weight_decay=0.1,
                          ns_backend=dmuon.NewtonSchulz(backend))
@@ -646,6 +648,7 @@ def test_step_graph_capture_replays_bit_exact(gpu, backend, monkeypatch):
         for pa, pb in zip(ma.parameters(), mb.parameters()):
             assert torch.equal(pa, pb)
         for da, db in zip(dmuon.get_owned_params(ma), dmuon.get_owned_params(mb)):
+            assert torch.equal(da._owned_data, db._owned_data)      # the master (fp32 or bf16)
             assert torch.equal(opta.state[id(da)]["momentum_buffer"],
                                optb.state[id(db)]["momentum_buffer"])
 
