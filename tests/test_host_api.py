@@ -196,3 +196,33 @@ def test_restored_state_is_converted_or_rejected():
         _state_tensor(torch.zeros(5), (4, 6), dev, torch.float32, "momentum_buffer", "w")
     with pytest.raises(TypeError, match="tensor"):
         _state_tensor([0.0] * 24, (4, 6), dev, torch.float32, "momentum_buffer", "w")
+
+
+def test_pointer_table_cache(monkeypatch):
+    """Muon._ptr_table: one device table per slot, reused while the addresses are unchanged,
+    rebuilt when one moves; under graph capture a hit is fine and a rebuild raises (it would
+    record a copy from a temporary host buffer). The pinned copy is stubbed: host logic only."""
+    from dmuon_amd.optim import muon as mm
+    made = []
+
+    def fake_pinned(ptrs, device):
+        t = torch.tensor(ptrs, dtype=torch.int64)
+        made.append(t)
+        return t
+
+    monkeypatch.setattr(mm, "_pinned_ptrs", fake_pinned)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    opt = object.__new__(mm.Muon)
+    opt._ptr_tables = {}
+    cpu = torch.device("cpu")
+    a = mm.Muon._ptr_table(opt, ("stage", 1, 2), [10, 20], cpu)
+    assert mm.Muon._ptr_table(opt, ("stage", 1, 2), [10, 20], cpu) is a and len(made) == 1
+    other = mm.Muon._ptr_table(opt, ("apply", 1, 2), [10, 20], cpu)
+    assert other is not a and len(made) == 2          # slots are independent
+    b = mm.Muon._ptr_table(opt, ("stage", 1, 2), [10, 30], cpu)
+    assert b is not a and b.tolist() == [10, 30] and len(made) == 3
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    assert mm.Muon._ptr_table(opt, ("stage", 1, 2), [10, 30], cpu) is b
+    with pytest.raises(RuntimeError, match="graph capture"):
+        mm.Muon._ptr_table(opt, ("stage", 1, 2), [11, 30], cpu)
+    assert len(made) == 3
