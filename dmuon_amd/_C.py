@@ -24,6 +24,11 @@ c_ip = ctypes.POINTER(ctypes.c_int)
 NS_DIRECT = 0
 NS_GRAM = 1
 
+# DMUON_ABI_VERSION of include/dmuon_amd.h: the argument lists below are those of this
+# version, and a library that reports another one is refused (its entry points would be
+# called with the wrong arguments).
+ABI_VERSION = 107
+
 # name -> (restype, argtypes); mirrors include/dmuon_amd.h
 _SIGNATURES = {
     "dmuon_last_error": (ctypes.c_char_p, []),
@@ -68,6 +73,7 @@ _SIGNATURES = {
                                               c_int, c_int, c_int, c_int, c_d, c_d, c_d, c_int,
                                               c_int, c_fp, c_int, c_int, c_ip, c_int, c_f, c_int,
                                               c_vp]),
+    "dmuon_noalloc_init": (c_int, [ctypes.POINTER(c_vp), ctypes.POINTER(c_i64)]),
     "dmuon_muon_stage_group": (c_int, [c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int, c_d,
                                        c_int, c_int, c_int, c_f, c_vp, c_i64, c_int, c_vp]),
     "dmuon_muon_apply_group": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int, c_d,
@@ -101,13 +107,28 @@ def lib() -> ctypes.CDLL:
             f"{_LIB_PATH} is missing: build the HIP kernels first "
             "(python -m dmuon_amd.csrc.build). dmuon_amd has no CPU fallback."
         )
-    handle = ctypes.CDLL(os.fspath(_LIB_PATH))
+    _lib = _bind(ctypes.CDLL(os.fspath(_LIB_PATH)), _LIB_PATH)
+    return _lib
+
+
+def _bind(handle, path) -> ctypes.CDLL:
+    """Checks the library's ABI version, then sets every entry point's argument types."""
+    version_fn = getattr(handle, "dmuon_abi_version", None)
+    if version_fn is None:
+        raise RuntimeError(f"{path} does not export dmuon_abi_version: not a dmuon_amd library")
+    version_fn.restype = c_int
+    version_fn.argtypes = []
+    version = int(version_fn())
+    if version != ABI_VERSION:
+        raise RuntimeError(
+            f"{path} reports ABI version {version}, this binding expects {ABI_VERSION}: the "
+            "library is stale or from another checkout; rebuild it (python -m "
+            "dmuon_amd.csrc.build)")
     for name, (res, args) in _SIGNATURES.items():
         fn = getattr(handle, name)
         fn.restype = res
         fn.argtypes = args
-    _lib = handle
-    return _lib
+    return handle
 
 
 def check(rc: int) -> None:

@@ -577,13 +577,25 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_of_current_device(const char* who, void** out) {
+// The device address of the current GPU's copy of `scratch`, resolved once per device. The
+// first resolution may load the library's code object, so it is not itself allocation-free:
+// dmuon_noalloc_init does it at set-up. With `capture_stream_checked`, a first resolution while
+// `stream` is being captured is refused instead (it would run inside the capture).
+int scratch_of_current_device(const char* who, void** out, bool capture_stream_checked = false,
+                              hipStream_t stream = nullptr) {
   int dev = -1;
   const hipError_t ge = hipGetDevice(&dev);
   if (ge != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return fail("%s: no current HIP device (%s)", who, hipGetErrorString(ge));
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    if (capture_stream_checked) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail("%s: first use on device %d while its stream is being captured: call "
+                    "dmuon_noalloc_init() (or the entry point once, eagerly) on this device "
+                    "before capturing", who, dev);
+    }
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
@@ -690,6 +702,12 @@ int syrk_plan(const char* who, const void* A, int64_t lda, int64_t strideA, cons
   if (batch > 1 && (strideA < 0 || strideB < 0 || strideD < 0 || (C && strideC < 0)))
     return fail("%s: batch strides must be non-negative", who);
   if (D == A || D == B || (C && D == C)) return fail("%s: D must not alias A, B or C", who);
+  // C is an M x M matrix; an operand is M x K. The two can be one matrix only when K == M
+  // (the polynomial Z = c R R^T + b R); otherwise the epilogue would read an M x M addend
+  // over an M x K operand's rows.
+  if (C && (C == A || C == B) && K != M)
+    return fail("%s: C aliases %s but K=%d != M=%d (an M x M addend cannot be an M x K operand)",
+                who, C == A ? "A" : "B", K, M);
   int t = tile_req;
   if (t == 0) {
     t = auto_tile(M, K > 0 ? K : 1, batch, 256);
@@ -1155,7 +1173,7 @@ int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const
                 "entry point holds per GPU; split the group or use dmuon_muon_step_group with "
                 "a workspace", who, (long long)need, (long long)kScratchBytes);
   void* ws = nullptr;
-  if (scratch_of_current_device(who, &ws)) return 1;
+  if (scratch_of_current_device(who, &ws, true, static_cast<hipStream_t>(stream))) return 1;
   NoEvents no_events;
   const double scale = 0.2 * sqrt((double)(rows > cols ? rows : cols));
   const float decay = wd > 0.0 ? (float)(1.0 - lr * wd) : 1.f;
@@ -1164,6 +1182,14 @@ int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const
                    nullptr, 0, rows, cols, batch, n_transposed, (float)mu, nesterov, first_step,
                    decay, lrs, coeffs, T, backend, restarts, n_restarts, eps, ws, kScratchBytes, tile,
                    static_cast<hipStream_t>(stream), who);
+}
+
+int dmuon_noalloc_init(void** scratch_out, int64_t* scratch_bytes) {
+  void* p = nullptr;
+  if (scratch_of_current_device("dmuon_noalloc_init", &p)) return 1;
+  if (scratch_out) *scratch_out = p;
+  if (scratch_bytes) *scratch_bytes = kScratchBytes;
+  return 0;
 }
 
 int dmuon_newton_schulz_group(void* const* g_ptrs, int g_dtype, void* const* out_ptrs,

@@ -1114,6 +1114,17 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   // k-major B: whole-panel buffer range and slice offsets in 32 bits, rows of whole tiles
   if (a.b_kmajor && ((long long)a.K * a.ldb * 2 >= (1LL << 31) || a.ldb < a.N))
     return hipErrorInvalidValue;
+  // An addend named as one of the operands (the K-loop rotation's C_IS_A / C_IS_B) is read by
+  // the epilogue as an M x N matrix at ldc: that is the operand itself only for a square
+  // product (K == M == N) with the operand's own layout. Anything else would read the addend
+  // past the operand's rows (a 4096 x 64 panel read as 4096 x 4096), so it is refused.
+  if (a.c_in == C_IS_A &&
+      !(a.C == a.A && a.K == a.M && a.M == a.N && a.ldc == a.lda && (a.L <= 1 || a.sC == a.sA)))
+    return hipErrorInvalidValue;
+  if (a.c_in == C_IS_B &&
+      !(a.C == a.B && a.K == a.M && a.M == a.N && a.ldc == a.ldb && (a.L <= 1 || a.sC == a.sB)))
+    return hipErrorInvalidValue;
+  if (a.c_in != C_NONE && a.c_in != C_IS_A && a.c_in != C_IS_B) return hipErrorInvalidValue;
   dim3 grid((unsigned)nb);
 #define DMUON_NT3(TILE, BK, S, WM, WN, E, KM)                                                  \
   do {                                                                                         \

@@ -131,6 +131,7 @@ class Muon(torch.optim.Optimizer):
         self._workspace_limit = int(workspace_limit_bytes)
         self._workspaces: list = [None, None]
         self._ptr_tables: dict = {}
+        self._captured_tables: dict = {}      # tables a graph capture has read (kept alive)
         self._overlap_staging = bool(overlap_staging)
         self._single_pass = bool(single_pass_staging)
         self._side_streams: dict = {}
@@ -404,10 +405,20 @@ class Muon(torch.optim.Optimizer):
         per ``slot`` (role and the chunk's parameters) and rebuilt only when an address
         changes: a steady-state step copies nothing to the device, which also lets a caller
         capture it into a graph after one eager step. The array is built on the current
-        stream, so a replaced one returns to the allocator in that stream's order."""
+        stream, so a replaced one returns to the allocator in that stream's order. A table
+        that a graph capture has used is kept alive for the optimizer's lifetime, so an earlier
+        graph still reads valid tables after an eager step with moved tensors rebuilt the
+        slot's table (the graph keeps operating on the tensors it was captured with)."""
         key = tuple(ptrs)
         hit = self._ptr_tables.get(slot)
         if hit is not None and hit[0] == key and hit[1].device == device:
+            if torch.cuda.is_current_stream_capturing():
+                # a graph now reads this table's memory: keep it for the life of the optimizer,
+                # even after a later eager step with moved tensors replaces the slot's table
+                kept = getattr(self, "_captured_tables", None)
+                if kept is None:
+                    kept = self._captured_tables = {}
+                kept[id(hit[1])] = hit[1]
             return hit[1]
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError(

@@ -39,6 +39,7 @@ import torch
 from torch import Tensor
 
 from dmuon_amd import _C
+from dmuon_amd._scratch import StreamScratch
 from dmuon_amd.optim.syrk_dispatch import KERNEL_NAME, get_backend_status, get_ns_backend  # noqa: F401
 
 logger = logging.getLogger(__name__)
@@ -129,25 +130,9 @@ def _ptr_array(tensors: Sequence[Tensor], device: torch.device) -> Tensor:
     return host.to(device, non_blocking=True)
 
 
-class _WorkspaceCache:
-    """One growing device byte buffer per device for the stand-alone NS functions.
-
-    Kernels run on the current stream in submission order, so successive calls reuse it safely;
-    concurrent use from several streams of one device is not supported (it would race).
-    """
-
-    def __init__(self) -> None:
-        self._bufs: dict[torch.device, Tensor] = {}
-
-    def get(self, device: torch.device, nbytes: int) -> Tensor:
-        buf = self._bufs.get(device)
-        if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
-            self._bufs[device] = buf
-        return buf
-
-
-_WORKSPACE = _WorkspaceCache()
+# NS scratch of the stand-alone functions, one buffer per (device, stream): calls on two
+# streams of one device do not share it
+_WORKSPACE = StreamScratch()
 
 
 def newton_schulz_batched(
@@ -189,10 +174,11 @@ def newton_schulz_batched(
     rst, n_rst = _C.restart_array(restart_iterations if code == _C.NS_GRAM else ())
     num_cus = torch.cuda.get_device_properties(G0.device).multi_processor_count
     t, _mp, _np, nbytes = _C.plan(rows, cols, L, tile, num_cus, code)
-    ws = _WORKSPACE.get(G0.device, nbytes)
+    cur = torch.cuda.current_stream(G0.device)
+    ws = _WORKSPACE.get(G0.device, cur, nbytes)
     gp = _ptr_array(ins, G0.device)
     op = _ptr_array(outs, G0.device)
-    stream = torch.cuda.current_stream(G0.device).cuda_stream
+    stream = cur.cuda_stream
     _C.call("dmuon_newton_schulz_group", gp.data_ptr(), _float_dtype_code(ins[0]), op.data_ptr(),
             _float_dtype_code(outs[0]), rows, cols, L, 0, coeff, T, code, rst, n_rst, float(eps),
             ws.data_ptr(), ws.numel(), t, stream)

@@ -24,6 +24,7 @@ import torch
 from torch import Tensor
 
 from dmuon_amd import _C
+from dmuon_amd._scratch import StreamScratch
 
 logger = logging.getLogger(__name__)
 
@@ -31,28 +32,8 @@ KERNEL_NAME = "hip_gfx950"
 _OPERAND_CODES = {torch.float16: _C.DTYPE_F16, torch.bfloat16: _C.DTYPE_BF16}
 
 
-class _ScratchCache:
-    """One growing device byte buffer per (device, stream) for the padded path's operand
-    copies. Calls on one stream run in submission order, so they reuse its buffer safely; each
-    buffer is allocated on its own stream, so when a larger one replaces it the allocator hands
-    the old memory out again only in that stream's order. (A buffer shared between streams
-    would let a call on one stream overwrite operands a call on another is still reading.)"""
-
-    def __init__(self) -> None:
-        self._bufs: dict[tuple, Tensor] = {}
-
-    def get(self, device: torch.device, stream: "torch.cuda.Stream", nbytes: int) -> Tensor:
-        key = (device, stream.cuda_stream)
-        buf = self._bufs.get(key)
-        if buf is None or buf.numel() < nbytes:
-            self._bufs.pop(key, None)
-            with torch.cuda.stream(stream):
-                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
-            self._bufs[key] = buf
-        return buf
-
-
-_SCRATCH = _ScratchCache()
+# the padded path's operand copies, one buffer per (device, stream)
+_SCRATCH = StreamScratch()
 
 
 def _k_contiguous(t: Tensor, name: str) -> Tensor:

@@ -72,7 +72,7 @@ extern "C" {
 const char* dmuon_last_error(void);
 
 /* ABI version (major*100 + minor): DMUON_ABI_VERSION of the header the library was built with. */
-#define DMUON_ABI_VERSION 106
+#define DMUON_ABI_VERSION 107
 int dmuon_abi_version(void);
 
 /*
@@ -293,7 +293,10 @@ int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_pt
  * call on one GPU shares that GPU's array and leaves its contents behind; a step needs none of
  * them (it writes every scratch byte it reads), but calls that overlap on one GPU (two streams,
  * two threads) race. `stream` must belong to the current device. Results equal
- * dmuon_muon_step_group's bit for bit.
+ * dmuon_muon_step_group's bit for bit. The scratch address of each GPU is resolved once, by
+ * dmuon_noalloc_init or the first call on that GPU; that first resolution may load the library's
+ * code object, so a caller that captures the step must make it happen before capturing (a first
+ * call on a capturing stream is refused with an error).
  */
 #define DMUON_NOALLOC_SCRATCH_BYTES (256LL << 20)
 int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
@@ -303,6 +306,13 @@ int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const
                                   int nesterov, int first_step, const float* coeffs, int T, int backend,
                                   const int* restarts, int n_restarts, float eps, int tile,
                                   void* stream);
+
+/* Set-up of dmuon_muon_step_group_noalloc on the current device (no counterpart in the
+ * reference; for the same callers, those that cannot allocate): resolves the device address of
+ * this GPU's scratch array outside any capture and returns it (*scratch_out, may be NULL) with
+ * its size in bytes (*scratch_bytes, may be NULL). Call it once per device before capturing the
+ * allocation-free step. Allocates no device memory of its own. */
+int dmuon_noalloc_init(void** scratch_out, int64_t* scratch_bytes);
 
 /* direct_newton_schulz / gram_newton_schulz (by `backend`, as above) for `batch` matrices of one
  * oriented shape (the last n_transposed are cols x rows, as above): out[l] <- NS(g[l]). */

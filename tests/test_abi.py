@@ -276,3 +276,84 @@ def test_noalloc_step_refuses_groups_beyond_its_scratch_without_gpu():
                                                                None))
     assert lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 64, 64, 0, 0, 0.02, 0.95,
                                              0.1, 1, 1, coeff, 5, 0, None, 0, 1e-7, 0, None) == 0
+
+
+def test_syrk_refuses_an_addend_aliasing_an_operand_of_another_shape_without_gpu():
+    """C is M x M; an operand is M x K. C == A (or B) with K != M would make the epilogue read
+    an M x M addend over an M x K operand's rows, so dmuon_syrk and its workspace query refuse
+    it as an argument error before any launch. C == A with K == M (the reference's
+    Z = c R R^T + b R) stays valid."""
+    lib = _C.lib()
+    need = ctypes.c_int64()
+    a = ctypes.c_void_p(1 << 20)
+    b = ctypes.c_void_p(1 << 24)
+    d = ctypes.c_void_p(1 << 30)
+    # C == A, K = 64 < M = 4096 (the shape of the probe that faulted)
+    msg = _err(lib.dmuon_syrk(_C.DTYPE_F16, a, 64, 0, None, 0, 0, a, 4096, 0, d, 4096, 0, 4096,
+                              64, 1, 1.0, 1.0, 0.0, None, 0, None, 0, None))
+    assert "C aliases A" in msg and "K=64" in msg
+    msg = _err(lib.dmuon_syrk_workspace_size(_C.DTYPE_F16, a, 64, 0, None, 0, 0, a, 4096, 0, d,
+                                             4096, 0, 4096, 64, 1, 0, ctypes.byref(need)))
+    assert "C aliases A" in msg
+    # C == B (a distinct B), K != M
+    msg = _err(lib.dmuon_syrk(_C.DTYPE_F16, a, 512, 0, b, 512, 0, b, 256, 0, d, 256, 0, 256, 512,
+                              1, 1.0, 1.0, 0.0, None, 0, None, 0, None))
+    assert "C aliases B" in msg
+    # bf16 entry point, same rule
+    msg = _err(lib.dmuon_syrk_bf16(a, 512, 0, None, 0, 0, a, 256, 0, d, 256, 0, 256, 512, 1, 1.0,
+                                   1.0, 0.0, None, 256, None))
+    assert "C aliases A" in msg
+    # K == M with C == A is the polynomial's legitimate form: planned, not refused
+    assert lib.dmuon_syrk_workspace_size(_C.DTYPE_F16, a, 512, 0, None, 0, 0, a, 512, 0, d, 512,
+                                         0, 512, 512, 1, 0, ctypes.byref(need)) == 0
+
+
+def test_launch_nt_refuses_mismatched_addend_alias(tmp_path):
+    """launch_nt itself (the one launcher every product goes through) refuses an addend named
+    as an operand (C_IS_A / C_IS_B) unless it really is that operand of a square product with
+    its layout. The harness tests/cpp/nt_guard.cpp calls the library's launch_nt on the host
+    with such arguments; every case must come back hipErrorInvalidValue without a device."""
+    import shutil
+    import subprocess
+    gxx = shutil.which("g++")
+    rocm = Path("/opt/rocm")
+    if gxx is None or not (rocm / "include" / "hip" / "hip_runtime.h").exists():
+        pytest.skip("needs g++ and the ROCm headers")
+    src = Path(__file__).resolve().parent / "cpp" / "nt_guard.cpp"
+    lib_dir = _C.lib_path().parent
+    exe = tmp_path / "nt_guard"
+    cmd = [gxx, "-std=c++17", "-D__HIP_PLATFORM_AMD__", f"-I{rocm / 'include'}", str(src),
+           f"-L{lib_dir}", "-ldmuon_amd", f"-L{rocm / 'lib'}", "-lamdhip64",
+           f"-Wl,-rpath,{lib_dir}", f"-Wl,-rpath,{rocm / 'lib'}", "-o", str(exe)]
+    build = subprocess.run(cmd, capture_output=True, text=True)
+    assert build.returncode == 0, build.stderr
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    print(run.stdout)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert run.stdout.count("refused") >= 8 and "NOT REFUSED" not in run.stdout
+
+
+def test_binding_refuses_a_library_of_another_abi_version():
+    """_C.lib() checks dmuon_abi_version() against the version its argument lists are written
+    for (the header's DMUON_ABI_VERSION) and refuses a stale library before binding any entry
+    point; a library without the version export is refused too."""
+    version = int(re.search(r"#define DMUON_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert _C.ABI_VERSION == version
+
+    class _Fn:
+        def __init__(self, value):
+            self.value = value
+
+        def __call__(self):
+            return self.value
+
+    class _FakeLib:
+        def __init__(self, value):
+            self.dmuon_abi_version = _Fn(value)
+
+    with pytest.raises(RuntimeError, match=rf"ABI version {version - 1}, this binding expects "
+                                           rf"{version}"):
+        _C._bind(_FakeLib(version - 1), "stale.so")
+    with pytest.raises(RuntimeError, match="does not export dmuon_abi_version"):
+        _C._bind(object(), "other.so")
+    assert _C.lib() is _C._bind(_C.lib(), _C.lib_path())     # the real library binds

@@ -21,8 +21,16 @@ from oracle import ns_oracle as o
 pytestmark = pytest.mark.gpu
 
 BF16_TOL = 2e-2       # north-star bf16 gate: relative Frobenius vs the reference pipeline
-SELF_TOL = 1e-2       # GPU vs the CPU restatement of the same pipeline (accumulation order
-                      # differs; Keller's a=3.44 amplifies tiny-sigma differences)
+# GPU vs the CPU restatement of the same fp16 pipeline (only the fp32 accumulation order of the
+# products differs). Both sides are deterministic, so these bounds sit a few times above the
+# largest error measured on MI355X for each family of cases, and a kernel change that made the
+# device several times less accurate fails them:
+SELF_TOL_DIRECT = 3e-3    # direct Keller x5, 256..1024-wide shapes: measured 5.0e-4 - 7.3e-4
+SELF_TOL_GRAM = 5e-3      # Gram, Polar-Express x5, any restart schedule: 5.5e-4 - 3.7e-3
+                          # (384 x 384 without a restart or with [2] is the largest)
+SELF_TOL_SHORT = 1e-3     # Gram with 1-3 steps: 6.4e-6 - 3.4e-4
+SELF_TOL_RAGGED = 1e-2    # tiny and ragged shapes (1 x 1 .. 257 x 129) through padded operands:
+                          # a handful of singular values, the rounding does not average out
 
 
 def _g(shape, seed, std=0.02):
@@ -39,9 +47,9 @@ def test_direct_ns_keller_vs_oracle(gpu, shape):
     e_self = o.rel_fro(U, o.syrk_emulated_ns(Gn, o.KELLER))
     e_ref = o.rel_fro(U, o.direct_ns(Gn, o.KELLER, dtype="fp16"))
     e_cf = o.rel_fro(U, o.closed_form_ns(Gn, o.KELLER))
-    print(f"{shape}: vs bf16 restatement {e_self:.2e}, vs fp16 reference {e_ref:.2e}, "
+    print(f"{shape}: vs fp16 restatement {e_self:.2e}, vs fp16 reference {e_ref:.2e}, "
           f"vs closed form {e_cf:.2e}")
-    assert e_self < SELF_TOL
+    assert e_self < SELF_TOL_DIRECT
     assert e_ref < BF16_TOL
     assert e_cf < BF16_TOL
 
@@ -71,7 +79,7 @@ def test_gram_device_path_vs_oracle(gpu, shape, restart):
     e_cf = o.rel_fro(U, o.closed_form_ns(Gn, o.POLAR_EXPRESS))
     print(f"{shape} restarts {restart}: vs fp16 restatement {e_self:.2e}, "
           f"vs fp16 reference {e_ref:.2e}, vs closed form {e_cf:.2e}")
-    assert e_self < SELF_TOL
+    assert e_self < SELF_TOL_GRAM
     assert e_ref < BF16_TOL
     assert e_cf < BF16_TOL
 
@@ -89,7 +97,7 @@ def test_gram_short_schedules(gpu, T, restart):
     e_self = o.rel_fro(U, o.syrk_emulated_gram_ns(Gn, coeffs, restart))
     e_cf = o.rel_fro(U, o.closed_form_ns(Gn, coeffs))
     print(f"T={T} restarts {restart}: vs restatement {e_self:.2e}, vs closed form {e_cf:.2e}")
-    assert e_self < SELF_TOL
+    assert e_self < SELF_TOL_SHORT
     assert e_cf < BF16_TOL
 
 
@@ -106,7 +114,9 @@ def test_gram_batched_keller_and_ragged(gpu):
         G = _g(shape, seed=sum(shape))
         U = dmuon.gram_newton_schulz(G.to(gpu)).cpu().numpy()
         assert np.isfinite(U).all() and U.shape == shape
-        assert o.rel_fro(U, o.syrk_emulated_gram_ns(G.numpy())) < SELF_TOL, shape
+        e = o.rel_fro(U, o.syrk_emulated_gram_ns(G.numpy()))
+        print(f"gram ragged {shape}: vs restatement {e:.2e}")
+        assert e < SELF_TOL_RAGGED, shape
     Z = torch.zeros(256, 640, device=gpu)
     assert torch.count_nonzero(dmuon.gram_newton_schulz(Z)) == 0
 
@@ -150,7 +160,9 @@ def test_zero_and_edge_inputs(gpu):
         G = _g(shape, seed=sum(shape))
         U = dmuon.direct_newton_schulz(G.to(gpu), coefficients=o.KELLER).cpu().numpy()
         assert np.isfinite(U).all() and U.shape == shape
-        assert o.rel_fro(U, o.syrk_emulated_ns(G.numpy(), o.KELLER)) < SELF_TOL, shape
+        e = o.rel_fro(U, o.syrk_emulated_ns(G.numpy(), o.KELLER))
+        print(f"direct ragged {shape}: vs restatement {e:.2e}")
+        assert e < SELF_TOL_RAGGED, shape
         tol = BF16_TOL if min(shape) >= 16 else 5e-2
         assert o.rel_fro(U, o.direct_ns(G.numpy(), o.KELLER, dtype="fp16")) < tol, shape
 

@@ -334,3 +334,47 @@ def test_reference_basic_dp_loop(gpu):
         assert not torch.equal(dp.param.detach(), w0)
         assert torch.isfinite(dp.param).all()
         assert optimizer.state[id(dp)]["momentum_buffer"].shape == tuple(dp.full_shape)
+
+
+def test_standalone_ns_on_two_streams_uses_one_workspace_each(gpu):
+    """gram_newton_schulz / direct_newton_schulz issued on two streams, interleaved without
+    waiting: each stream gets its own NS workspace, and every result equals the same call made
+    alone on the default stream."""
+    from dmuon_amd.optim import newton_schulz as nsm
+    Gs = [torch.randn(512, 1536, generator=torch.Generator().manual_seed(70 + i)).to(gpu)
+          for i in range(6)]
+    ref = [nsm.gram_newton_schulz(g) if i % 3 else nsm.direct_newton_schulz(g)
+           for i, g in enumerate(Gs)]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [None] * len(Gs)
+    for i, g in enumerate(Gs):
+        with torch.cuda.stream(s1 if i % 2 == 0 else s2):
+            outs[i] = nsm.gram_newton_schulz(g) if i % 3 else nsm.direct_newton_schulz(g)
+    torch.cuda.synchronize()
+    for o, r in zip(outs, ref):
+        assert torch.equal(o, r)
+    held = nsm._WORKSPACE.streams(gpu)
+    assert s1.cuda_stream in held and s2.cuda_stream in held
+    b1 = nsm._WORKSPACE._bufs[(torch.device(gpu), s1.cuda_stream)]
+    b2 = nsm._WORKSPACE._bufs[(torch.device(gpu), s2.cuda_stream)]
+    assert b1.data_ptr() != b2.data_ptr()
+
+
+def test_stream_scratch_keeps_the_most_recent_streams(gpu):
+    """The per-stream scratch cache holds at most max_streams buffers per device and drops the
+    least recently used one beyond that."""
+    from dmuon_amd._scratch import StreamScratch
+    sc = StreamScratch(max_streams=2)
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    handles = [s.cuda_stream for s in streams]
+    if len(set(handles)) < 3:
+        pytest.skip("the stream pool handed out a repeated handle")
+    a = sc.get(gpu, streams[0], 1024)
+    sc.get(gpu, streams[1], 1024)
+    assert sc.get(gpu, streams[0], 512) is a          # reused, and now most recent
+    sc.get(gpu, streams[2], 1024)                     # evicts streams[1]
+    assert sc.streams(gpu) == [handles[0], handles[2]]
+    big = sc.get(gpu, streams[0], 4096)               # grows in place of the old buffer
+    assert big.numel() >= 4096 and big is not a
+    assert sc.streams(gpu) == [handles[2], handles[0]]

@@ -226,3 +226,10 @@ def test_pointer_table_cache(monkeypatch):
     with pytest.raises(RuntimeError, match="graph capture"):
         mm.Muon._ptr_table(opt, ("stage", 1, 2), [11, 30], cpu)
     assert len(made) == 3
+    # the captured table b outlives its slot: an eager step with a moved tensor rebuilds the
+    # slot, and b (which the graph reads) stays referenced by the optimizer
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    c = mm.Muon._ptr_table(opt, ("stage", 1, 2), [12, 30], cpu)
+    assert c is not b and len(made) == 4
+    assert any(t is b for t in opt._captured_tables.values())
+    assert not any(t is c or t is a for t in opt._captured_tables.values())

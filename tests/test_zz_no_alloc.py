@@ -1,8 +1,11 @@
 """dmuon_muon_step_group_noalloc (scratch in a static device array) against
 dmuon_muon_step_group (a torch-allocated workspace), through the C ABI: identical inputs give
 identical weights, momentum buffers, kept scales and forward copies, bit for bit, over calls in a
-row whose second is smaller than the first (the scratch keeps the first call's contents). The
-refusal of a group larger than the scratch is checked on the CPU (tests/test_abi.py)."""
+row whose second is smaller than the first (the scratch keeps the first call's contents). Before
+every call both scratch areas are filled with 0xFF bytes (NaN in fp16 and fp32), so a read of a
+scratch byte the step did not write first shows up as a NaN or a mismatch. The step is also
+captured into a graph (after dmuon_noalloc_init) and replayed against eager workspace calls.
+The refusal of a group larger than the scratch is checked on the CPU (tests/test_abi.py)."""
 import ctypes
 
 import pytest
@@ -69,19 +72,47 @@ def _args(grp, rows, cols, first, backend, coeffs):
             1 if backend == _C.NS_GRAM else 0, 1e-7]
 
 
-def _run_both(grp, rows, cols, first, backend, coeffs, dev):
-    other = grp.clone()
-    args = _args(grp, rows, cols, first, backend, coeffs)
+def _scratch():
+    """(device address, bytes) of the current GPU's static scratch (dmuon_noalloc_init)."""
+    ptr, nbytes = ctypes.c_void_p(), ctypes.c_int64()
+    _C.call("dmuon_noalloc_init", ctypes.byref(ptr), ctypes.byref(nbytes))
+    assert ptr.value and nbytes.value > 0
+    return ptr.value, nbytes.value
+
+
+def _poison_scratch(dev):
+    """0xFF over the whole static scratch, copied from a torch buffer by the library's copy."""
+    addr, nbytes = _scratch()
+    src = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=dev)
+    _C.call("dmuon_stream_copy", src.data_ptr(), addr, nbytes, _stream())
+    torch.cuda.synchronize()
+
+
+def _workspace_step(grp, rows, cols, first, backend, coeffs, dev):
+    """The workspace entry point on a freshly poisoned workspace."""
     L = len(grp.g)
     _, _, _, nbytes = _C.plan(rows, cols, L, 0, 0, backend)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    _C.call("dmuon_muon_step_group", *args, ws.data_ptr(), ws.numel(), 0, _stream())
-    _C.call("dmuon_muon_step_group_noalloc", *_args(other, rows, cols, first, backend, coeffs),
-            0, _stream())
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=dev)
+    _C.call("dmuon_muon_step_group", *_args(grp, rows, cols, first, backend, coeffs),
+            ws.data_ptr(), ws.numel(), 0, _stream())
+    return nbytes
+
+
+def _assert_same_and_finite(grp, other):
     torch.cuda.synchronize()
     for a, b in zip(grp.tensors(), other.tensors()):
         assert torch.equal(a, b)
-    assert nbytes <= (256 << 20)
+        assert not torch.isnan(a).any()
+
+
+def _run_both(grp, rows, cols, first, backend, coeffs, dev):
+    other = grp.clone()
+    nbytes = _workspace_step(grp, rows, cols, first, backend, coeffs, dev)
+    _poison_scratch(dev)
+    _C.call("dmuon_muon_step_group_noalloc", *_args(other, rows, cols, first, backend, coeffs),
+            0, _stream())
+    _assert_same_and_finite(grp, other)
+    assert nbytes <= _scratch()[1]
     return other
 
 
@@ -101,3 +132,30 @@ def test_noalloc_matches_workspace_entry_point(gpu):
         t.copy_((torch.randn(t.shape, generator=gen) * 0.03).to(torch.bfloat16))
     _run_both(big, 512, 1536, 0, _C.NS_GRAM, pe, gpu)
 
+
+
+def test_noalloc_step_captured_and_replayed(gpu):
+    """After dmuon_noalloc_init, the allocation-free step is captured into a graph and replayed
+    three times with new gradients written into the captured tensors, eager work and
+    synchronisations in between; every replay equals an eager call of the workspace entry point
+    on a copy of the same state, bit for bit. The scratch is poisoned before each replay."""
+    _scratch()
+    pe = dmuon.POLAR_EXPRESS_COEFFICIENTS
+    rows, cols = 384, 1280
+    grp = _Group(rows, cols, 2, torch.bfloat16, False, 7, gpu)
+    # a first, eager step establishes the momentum buffers and the kept scales
+    grp = _run_both(grp, rows, cols, 1, _C.NS_GRAM, pe, gpu)
+    args = _args(grp, rows, cols, 0, _C.NS_GRAM, pe)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _C.call("dmuon_muon_step_group_noalloc", *args, 0, _stream())
+    gen = torch.Generator().manual_seed(8)
+    for r in range(3):
+        for t in grp.g:
+            t.copy_((torch.randn(t.shape, generator=gen) * 0.02 * (1 + r)).to(torch.bfloat16))
+        ref = grp.clone()
+        _poison_scratch(gpu)
+        graph.replay()
+        torch.cuda.synchronize()
+        _workspace_step(ref, rows, cols, 0, _C.NS_GRAM, pe, gpu)
+        _assert_same_and_finite(ref, grp)
