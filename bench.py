@@ -80,8 +80,10 @@ def build_model(torch, device, dtype, n_layers, with_rest):
     return m
 
 
-def build_set(torch, device, shapes, seed):
-    """bf16 matrices of the given shapes with N(0, 0.02^2) weights and gradients."""
+def build_set(torch, device, shapes, seed, dtype=None):
+    """Matrices of the given shapes (bf16 unless `dtype`) with N(0, 0.02^2) weights and
+    gradients."""
+    dtype = torch.bfloat16 if dtype is None else dtype
     from torch import nn
 
     class MatrixSet(nn.Module):
@@ -90,7 +92,7 @@ def build_set(torch, device, shapes, seed):
             gen = torch.Generator(device=device).manual_seed(seed)
             self.mats = nn.ParameterList()
             for shape in shapes:
-                w = torch.empty(shape, device=device, dtype=torch.bfloat16)
+                w = torch.empty(shape, device=device, dtype=dtype)
                 w.normal_(0.0, 0.02, generator=gen)
                 self.mats.append(nn.Parameter(w))
 
@@ -101,6 +103,17 @@ def build_set(torch, device, shapes, seed):
         g.normal_(0.0, 0.02, generator=gen)
         p.grad = g
     return m
+
+
+def nt_sources_sha256() -> str:
+    """SHA-256 over the sources that decide the NT kernels' memory traffic (the kernels and the
+    launch sequence), in a fixed order."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in ("dmuon_amd/csrc/ns_gemm.hip", "dmuon_amd/csrc/abi.hip"):
+        with open(os.path.join(HERE, rel), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
 
 
 def cpu_info() -> dict:
@@ -164,6 +177,60 @@ def cpu_baseline(budget_s: float = 60.0, ns: str = "gram") -> dict:
                    "extrapolated as 32 x layer 0 (Muon matrices only, no AdamW)"),
         "per_matrix_s": per,
     }
+
+
+def _blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        return None
+
+
+def cpu_config(shapes, ns: str, dtype: str, rounds: int, seed: int, scale: float = 1.0,
+               sample: str = "") -> dict:
+    """One BASELINE config on the host: the oracle's Muon step (momentum
+    from a zero buffer, Nesterov, the NS of `ns` -- "direct" with Keller's coefficients or
+    "gram" with Polar-Express and a restart at 2 --, weight decay 0.1 and the update) over
+    `shapes`, with every tensor op rounded to `dtype` ("fp16": the reference's literal
+    pipeline; "fp32": its fp32-compute variant, the same cast points). One untimed warm-up
+    pass, then the median of `rounds` timed passes; `scale` extrapolates a sample of the
+    config's matrices to all of them."""
+    import numpy as np
+
+    from oracle import ns_oracle as o
+
+    rng = np.random.default_rng(seed)
+    mats = [(rng.standard_normal(s, dtype=np.float32) * 0.02,
+             rng.standard_normal(s, dtype=np.float32) * 0.02) for s in shapes]
+    coeffs = o.KELLER if ns == "direct" else o.POLAR_EXPRESS
+
+    def one_pass():
+        t0 = time.perf_counter()
+        for W, g in mats:
+            o.muon_step(W, g, None, lr=0.02, mu=0.95, wd=0.1, coefficients=coeffs, ns=ns,
+                        dtype=dtype)
+        return time.perf_counter() - t0
+
+    one_pass()
+    times = sorted(one_pass() for _ in range(rounds))
+    med = times[len(times) // 2] * scale
+    info = cpu_info()
+    return {"cpu_ms": round(med * 1e3, 1), "cpu_cores": _blas_threads() or info["cpu_count"],
+            "cpu_kind": "port", "cpu_model": info["cpu_model"],
+            "cpu_sample": (f"oracle/ns_oracle.muon_step(ns={ns!r}, dtype={dtype!r}) over "
+                           f"{len(shapes)} matrices, 1 warm-up + median of {rounds}"
+                           + (f"; {sample}" if sample else ""))}
+
+
+def with_cpu(leg: dict, cpu: dict) -> dict:
+    """A config leg with its CPU baseline and the GPU/CPU speed-up."""
+    out = dict(leg)
+    out.update(cpu)
+    gpu_ms = leg.get("ms_per_step_median")
+    if gpu_ms and cpu.get("cpu_ms"):
+        out["speedup_vs_cpu"] = round(cpu["cpu_ms"] / gpu_ms, 1)
+    return out
 
 
 def library_compare(torch, dev, _C, reps: int = 10, rounds: int = 3) -> dict:
@@ -249,14 +316,17 @@ def time_steps(torch, opt, warmup: int, steps: int) -> list:
     return [evs[k].elapsed_time(evs[k + 1]) for k in range(steps)]
 
 
-def config_leg(torch, dmuon, dev, shapes, ns, steps, warmup, seed, momentum_init=False):
-    """One BASELINE config on its own matrices (bf16 weights updated in place, fp32 momentum):
-    ms per optimizer step and useful NS TFLOP/s."""
+def config_leg(torch, dmuon, dev, shapes, ns, steps, warmup, seed, momentum_init=False,
+               dtype=None):
+    """One BASELINE config on its own matrices (bf16 weights updated in place unless `dtype`
+    -- then weights of that dtype, their own masters --, fp32 momentum): median ms per
+    optimizer step and useful NS TFLOP/s."""
     from dmuon_amd.optim.newton_schulz import ns_useful_flops
 
-    model = build_set(torch, dev, shapes, seed)
+    dtype = torch.bfloat16 if dtype is None else dtype
+    model = build_set(torch, dev, shapes, seed, dtype)
     dmuon.dedicate_params(model, None, lambda n, p: p.dim() == 2,
-                          param_policy={"defaults": {"master_dtype": torch.bfloat16}})
+                          param_policy={"defaults": {"master_dtype": dtype}})
     dmuon.replicate(model)
     opt = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, ns_backend=ns)
     if momentum_init:
@@ -281,6 +351,49 @@ def config_leg(torch, dmuon, dev, shapes, ns, steps, warmup, seed, momentum_init
     del opt, model
     torch.cuda.empty_cache()
     return out
+
+
+def measure_step(torch, _C, opt, warmup: int, steps: int, prof_steps: int):
+    """`warmup` untimed optimizer steps, then exactly `steps` timed ones (one event between
+    steps), then `prof_steps` more with the library's per-launch hipEvents. Returns (ms per
+    step over the timed region, sorted per-step ms, host wall seconds of the timed region,
+    per-class profile of the library's launches)."""
+    for _ in range(warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    with quiet_gc():
+        t0 = time.perf_counter()
+        evs[0].record()
+        for k in range(steps):
+            opt.step()
+            evs[k + 1].record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    ms_per_step = evs[0].elapsed_time(evs[-1]) / steps
+    per_step = sorted(evs[k].elapsed_time(evs[k + 1]) for k in range(steps))
+    _C.profile_collect()
+    _C.profile_enable(True)
+    with quiet_gc():
+        for _ in range(prof_steps):
+            opt.step()
+        torch.cuda.synchronize()
+    _C.profile_enable(False)
+    return ms_per_step, per_step, wall, _C.profile_collect()
+
+
+def nt_roofline(prof: dict, prof_steps: int) -> dict:
+    """The NT MFMA family (X X^T / SYRK, the polynomial products, the NS products and the final
+    product) from a per-class profile: useful TFLOP/s over the summed launch time."""
+    mf = [prof[c] for c in ("syrk", "poly", "gemm", "final")]
+    mf_ms = sum(r["ms"] for r in mf)
+    mf_launch = sum(r["launches"] for r in mf)
+    achieved = sum(r["flops"] for r in mf) / (mf_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+            "avg_launch_us": round(1e3 * mf_ms / max(mf_launch, 1), 2),
+            "launches_per_step": mf_launch // prof_steps}
 
 
 def copy_leg(torch, dev, _C, gib: int = 4, reps: int = 5) -> dict:
@@ -402,36 +515,15 @@ def main():
     # 471.81 TF for c5), whatever form the step computes
     flops_baseline = sum(ns_useful_flops(*p.shape, 5, "direct") for p in mats)
 
-    # ---- timed region: exactly K optimizer steps (Muon matrices + AdamW rest) -----------------
-    for _ in range(args.warmup):
-        opt.step()
-    torch.cuda.synchronize()
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    torch.cuda.synchronize()
-    with quiet_gc():
-        t0 = time.perf_counter()
-        evs[0].record()
-        for k in range(args.steps):
-            opt.step()
-            evs[k + 1].record()          # one event between steps: per-step times for the spread
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    ms_per_step = evs[0].elapsed_time(evs[-1]) / args.steps
-    per_step = sorted(evs[k].elapsed_time(evs[k + 1]) for k in range(args.steps))
+    # ---- timed region: exactly K optimizer steps (Muon matrices + AdamW rest), then the same
+    # steps with the library's per-launch hipEvents (kernel breakdown) ------------------------
+    prof_steps = max(1, min(3, args.steps))
+    ms_per_step, per_step, wall, prof = measure_step(torch, _C, opt, args.warmup, args.steps,
+                                                     prof_steps)
 
     def pct(q):
         return per_step[min(len(per_step) - 1, int(round(q * (len(per_step) - 1))))]
 
-    # ---- kernel breakdown: the same steps with the library's per-launch hipEvents -------------
-    prof_steps = max(1, min(3, args.steps))
-    _C.profile_collect()
-    _C.profile_enable(True)
-    with quiet_gc():
-        for _ in range(prof_steps):
-            opt.step()
-        torch.cuda.synchronize()
-    _C.profile_enable(False)
-    prof = _C.profile_collect()
     classes = {}
     for name, r in prof.items():
         if r["launches"] == 0:
@@ -444,11 +536,7 @@ def main():
         if r["bytes"] > 0 and r["flops"] == 0:
             ent["gbs"] = round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)
         classes[name] = ent
-    mf = [prof[c] for c in ("syrk", "poly", "gemm", "final")]
-    mf_ms = sum(r["ms"] for r in mf)
-    mf_launch = sum(r["launches"] for r in mf)
-    mf_flops = sum(r["flops"] for r in mf)
-    achieved_tf = mf_flops / (mf_ms * 1e-3) / 1e12
+    nt = nt_roofline(prof, prof_steps)
     pre = prof["pre"]
     pre_gbs = pre["bytes"] / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
     # what the staging actually moves per element: gradient (2 B), momentum (4 + 4 B) and the
@@ -491,17 +579,49 @@ def main():
                 "roofline": {"bound": "hbm", "achieved": round(c_gbs, 1), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(c_gbs / HBM_PEAK_GBS, 4),
                              "algorithmic_bytes_per_elem": 6}}
-    del opt, model, mats
+    del opt
+    torch.cuda.empty_cache()
+
+    # ---- the same c5 step with 5 direct Keller NS steps (the north star's "X <- P X" form and
+    # BASELINE.md's FLOP model, 471.81 useful TFLOP, with its 50%-of-peak line) ---------------
+    c5_direct = None
+    if not args.no_configs and args.ns == "gram" and args.layers == N_LAYERS:
+        opt_d = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, adamw_lr=1e-3,
+                           ns_backend=dmuon.NewtonSchulz("direct", coefficients=KELLER))
+        d_ms, d_per, _, d_prof = measure_step(torch, _C, opt_d, 2, 5, 1)
+        d_tf = flops_baseline / (d_ms * 1e-3) / 1e12
+        line = flops_baseline / (0.5 * MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3
+        c5_direct = {
+            "ms_per_step": round(d_ms, 3), "ms_per_step_median": round(d_per[len(d_per) // 2], 3),
+            "steps": 5, "warmup": 2,
+            "workload": "the c5 step (224 matrices, fp32 momentum, bf16 weights updated in "
+                        "place, AdamW rest) with 5 direct NS steps of Keller's (3.4445, "
+                        "-4.7750, 2.0315), fp16 MFMA",
+            "useful_ns_tflop": round(flops_baseline / 1e12, 2),
+            "tflops": round(d_tf, 1), "frac": round(d_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "ms_at_50pct_peak": round(line, 1),
+            "ms_over_50pct_line": round(d_ms / line, 4),
+            "roofline": nt_roofline(d_prof, 1)}
+        del opt_d
+        torch.cuda.empty_cache()
+    del model, mats
     torch.cuda.empty_cache()
 
     copy = copy_leg(torch, dev, _C)
 
     configs = None
     if not args.no_configs:
-        configs = {"c2": dict(config_leg(torch, dmuon, dev, [(4096, 4096)], ns, 100, 3, 20,
-                                         momentum_init=True),
-                              workload="one bf16 4096x4096 matrix, momentum ~N(0, 0.02^2), "
-                                       "100 timed steps")}
+        keller = dmuon.NewtonSchulz("direct", coefficients=KELLER)
+        configs = {"c1": dict(config_leg(torch, dmuon, dev, [(1024, 1024)], keller, 10, 1, 10,
+                                         dtype=torch.float32),
+                              workload="one fp32 1024x1024 weight (its own master), fp32 "
+                                       "gradient, zero momentum; lr 0.02, mu 0.95 Nesterov, "
+                                       "wd 0.1, 5 direct Keller NS steps; median of 10 steps "
+                                       "after the first")}
+        configs["c2"] = dict(config_leg(torch, dmuon, dev, [(4096, 4096)], ns, 100, 3, 20,
+                                        momentum_init=True),
+                             workload="one bf16 4096x4096 matrix, momentum ~N(0, 0.02^2), "
+                                      "100 timed steps")
         configs["c3"] = {}
         for i, shape in enumerate(C3_SHAPES):
             configs["c3"][f"{shape[0]}x{shape[1]}"] = config_leg(torch, dmuon, dev, [shape], ns,
@@ -510,15 +630,34 @@ def main():
                              workload="64 x (1408x2048) + 64 x (2048x1408) bf16 expert matrices")
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget, args.ns)
+    if configs is not None and not args.no_cpu_baseline:
+        # c1 the reference's literal fp16 pipeline, median of 10; c2-c4
+        # its fp32-compute variant (fp16 GEMMs are impractically slow on the host), median of 3,
+        # the NS form of the GPU legs; c4 on a sample of its experts
+        configs["c1"] = with_cpu(configs["c1"], cpu_config([(1024, 1024)], "direct", "fp16", 10,
+                                                           10))
+        configs["c2"] = with_cpu(configs["c2"], cpu_config([(4096, 4096)], ns.backend, "fp32",
+                                                           3, 20))
+        for i, shape in enumerate(C3_SHAPES):
+            key = f"{shape[0]}x{shape[1]}"
+            configs["c3"][key] = with_cpu(configs["c3"][key],
+                                          cpu_config([shape], ns.backend, "fp32", 3, 30 + i))
+        configs["c4"] = with_cpu(configs["c4"], cpu_config(
+            [(1408, 2048)] * 8 + [(2048, 1408)] * 8, ns.backend, "fp32", 3, 40, scale=8.0,
+            sample="8 + 8 of the 64 + 64 experts, reported x 8"))
+    if c5_direct is not None:
+        configs = dict(configs or {}, c5_direct=c5_direct)
 
     # HBM (L2-miss) bytes per NT launch: counters cannot be read from inside this process, so
-    # the figure comes from the committed rocprofv3 --pmc summary of this same workload
+    # the figure comes from the committed rocprofv3 --pmc summary of this same workload -- and
+    # only while the kernel sources it was measured on are the ones built here (their SHA-256
+    # is recorded with it); after a kernel change it is null until profiled again
     traffic = None
     tpath = os.path.join(HERE, "profiles", "nt_mfma_traffic.json")
     if os.path.exists(tpath) and args.layers == N_LAYERS:
         with open(tpath) as fh:
             tj = json.load(fh)
-        if tj.get("ns_backend") == args.ns:
+        if tj.get("ns_backend") == args.ns and tj.get("sources_sha256") == nt_sources_sha256():
             traffic = tj.get("traffic_bytes_per_launch")
 
     out = {
@@ -557,17 +696,13 @@ def main():
             "tflops": round(flops_baseline / (ms_per_step * 1e-3) / 1e12, 1),
             "frac": round(flops_baseline / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
             "ms_at_50pct_peak": round(flops_baseline / (0.5 * MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3, 1)},
-        "roofline": {
-            "kernel": ("nt_pp_kernel / nt_mfma_kernel<..., fp16> (Gram X X^T, R/Z/W triangle "
-                       "products, Q update, restart Q X, final Q X + update)" if args.ns == "gram"
-                       else "nt_pp_kernel / nt_mfma_kernel<..., fp16> (SYRK X X^T, SYRK-poly, "
-                            "NS GEMM, final GEMM+update)"),
-            "bound": "mfma", "achieved": round(achieved_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(achieved_tf / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": traffic,
-            "avg_launch_us": round(1e3 * mf_ms / max(mf_launch, 1), 2),
-            "launches_per_step": mf_launch // prof_steps,
-        },
+        "roofline": dict(
+            {"kernel": ("nt_pp_kernel / nt_mfma_kernel<..., fp16> (Gram X X^T, R/Z/W triangle "
+                        "products, Q update, restart Q X, final Q X + update)"
+                        if args.ns == "gram" else
+                        "nt_pp_kernel / nt_mfma_kernel<..., fp16> (SYRK X X^T, SYRK-poly, "
+                        "NS GEMM, final GEMM+update)")},
+            **nt, traffic=traffic),
         "roofline_elementwise": {
             "kernel": ("muon_pre_kernel: momentum + Nesterov + norm partials + fp16 staging of "
                        "ns_in with the kept scale in one pass (a second pass only for matrices "

@@ -51,7 +51,13 @@ struct NtArgs {
   // the kernels stage its slices as BK rows of the tile's N values and assemble the MFMA
   // operand with transposing LDS reads. C_IS_B then means C is B as stored.
   int b_kmajor;
+  // EPI_SYM + tri + sym_exact, 256-tiles: how much of a diagonal tile's work below the diagonal
+  // (whose values the epilogue drops) is skipped. DIAG_SKIP_NONE computes every block;
+  // DIAG_SKIP_WAVES skips the two waves that hold no kept value; DIAG_SKIP_BLOCKS also skips the
+  // 16x16 blocks strictly below the diagonal in the waves that straddle it. Same bits each way.
+  int diag_skip;
 };
+enum { DIAG_SKIP_NONE = 0, DIAG_SKIP_WAVES = 1, DIAG_SKIP_BLOCKS = 2 };
 enum { C_NONE = 0, C_IS_A = 1, C_IS_B = 2 };
 
 // Launches the NT MFMA kernel; picks the tile configuration from args (tile = 256 or 128).

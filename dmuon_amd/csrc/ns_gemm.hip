@@ -892,16 +892,19 @@ void nt_mfma_kernel(const NtArgs a) {
 // group 1's M(k) refills each wave's own B block with slice k + 2 and waits for slice k + 1's B
 // before the barrier that opens group 0's M(k + 1). (Measured against all refill DMA issued by
 // group 1, part of it in its compute phase: 5-10% faster, bit-identical.)
-template <int BK, int S, int MODE, int E, bool BKM>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void nt_pp_kernel(const NtArgs a) {
+// One 256 x 256 tile of the ping-pong schedule, this wave's part of it. LIM: the wave computes
+// the 16x16 blocks (x, y) of its 128 x 64 sub-tile with x - y <= LIM -- all of them (LIM = 7),
+// or, on a diagonal tile of an exactly symmetric triangle product (whose values below the
+// diagonal the epilogue drops), those on or above the diagonal (see nt_pp_kernel); LIM = -8:
+// none (no fragment reads, no MFMAs, no epilogue). Each LIM is its own straight-line copy of the
+// whole schedule: a runtime choice inside the loop made the compiler spill ~1000 VGPRs.
+template <int BK, int S, int MODE, int E, bool BKM, int LIM>
+__device__ __forceinline__ void pp_tile(const NtArgs& a, char* smem, int l, int bi, int bj) {
   using T = Tile<256, 256, BK, S, 2, 4>;
-  __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
-  static_assert(T::LDS_BYTES <= 160 * 1024, "LDS budget");
   constexpr int KS = BK / 32;                        // 16x16x32 MFMA substeps per slice
   // Wave v of either group moves, per slice, three parts of a ring slot (RPI rows per
   // instruction): A rows v*32 .. +31 and 128 + v*32 .. +31 (group 0 in the loop, group 1 in the
-  // prologue) and the B block of wave column v (rows / values v*64 .. +63; group 1).
+  // prologue) and the B block v (rows / values v*64 .. +63; group 1).
   static_assert(S == 2, "the refill split between the groups assumes a two-slot ring");
   constexpr int NAL = 32 / T::RPI, NB = 64 / T::RPI;
   constexpr int LPT1 = 2 * NAL + NB;                 // per group-1 wave per prologue slice
@@ -910,13 +913,14 @@ void nt_pp_kernel(const NtArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave >> 2, wj = wave & 3, wi = grp;
+  const int grp = wave >> 2, v = wave & 3, wi = grp;
+  // Column block of the wave's 128 x 64 sub-tile: group 1's wave v takes block v (the B block it
+  // also moves, so it refills only a block whose last reader in this phase pair is itself), group
+  // 0's takes block 3 - v. The two waves that share a SIMD (v and v + 4) thus cover blocks 3 - v
+  // and v. Every assignment gives the same bits; this one evens out the SIMDs' MFMA counts on
+  // diagonal tiles.
+  const int wj = grp == 0 ? 3 - v : v;
 
-  // the decode is the same for every lane; readfirstlane states it, so the buffer descriptors
-  // and offsets built from it stay scalar whatever the compiler's uniformity analysis proves
-  const TilePos tp = decode_tile(a, blockIdx.x, gridDim.x);
-  const int l = __builtin_amdgcn_readfirstlane(tp.l);
-  const int bi = __builtin_amdgcn_readfirstlane(tp.bi), bj = __builtin_amdgcn_readfirstlane(tp.bj);
   const int i0 = bi * 256, j0 = bj * 256;
   const uint16_t* __restrict__ Ab = a.A + (long long)l * a.sA + (long long)i0 * a.lda;
   const uint16_t* __restrict__ Bb =
@@ -927,7 +931,6 @@ void nt_pp_kernel(const NtArgs a) {
 
   // lane l of a DMA instruction writes LDS slot l % CPR of row l / CPR of its RPI-row group: it
   // fetches the global chunk the swizzle places there
-  const int v = wave & 3;
   const int lrow = lane / T::CPR, lsl = lane % T::CPR;
   // The swizzle of a row (and of a k-major row) repeats every 16 rows, so instructions q and
   // q + 2 of a part differ by 16 rows: two per-lane offsets per operand, the rest of the
@@ -990,6 +993,8 @@ void nt_pp_kernel(const NtArgs a) {
 #pragma unroll
   for (int y = 0; y < 4; ++y) kboff[y] = BKM ? wj * KBLK + kmajor64_lane_off(lane, 16 * y) : 0;
   bf16x8_t af[KS][8], bfr[KS][4];
+  // the fragments of slot `slot` that the blocks x - y <= LIM use: A block x for x <= LIM + 3,
+  // B block y for y >= -LIM
   auto mem_phase = [&](int slot) {
     const char* sa = smem + slot * T::STAGE;
     const char* sb = sa + T::A_BYTES;
@@ -998,11 +1003,13 @@ void nt_pp_kernel(const NtArgs a) {
       const int kc = ks * 4 + kq;
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
+        if (x > LIM + 3) continue;
         const int row = arow0 + x * 16;
         af[ks][x] = *reinterpret_cast<const bf16x8_t*>(sa + row * T::ROWB + (T::slot(kc, row) << 4));
       }
 #pragma unroll
       for (int y = 0; y < 4; ++y) {
+        if (y < -LIM) continue;
         if constexpr (BKM) {
           bfr[ks][y] = read_kmajor(sb + kboff[y] + ks * 32 * 128, 128);
         } else {
@@ -1011,6 +1018,15 @@ void nt_pp_kernel(const NtArgs a) {
         }
       }
     }
+  };
+  auto compute_phase = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int x = 0; x < 8; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y)
+          if (x - y <= LIM) acc[x][y] = mfma_16x16x32<E>(bfr[ks][y], af[ks][x], acc[x][y]);
   };
 
   const int KT = a.K / BK;
@@ -1053,13 +1069,7 @@ void nt_pp_kernel(const NtArgs a) {
       }
     }
     phase_barrier();
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int x = 0; x < 8; ++x)
-#pragma unroll
-        for (int y = 0; y < 4; ++y)
-          acc[x][y] = mfma_16x16x32<E>(bfr[ks][y], af[ks][x], acc[x][y]);
+    compute_phase();
     if (RA && grp == 0) wait_vmcnt<0>();             // slice kt + 1's A rows have landed
     // Last slice: group 1 stops at the barrier before its MFMAs (|2KT), which is also the one
     // after group 0's; no wave reads the ring after it, so group 0's epilogue overlaps group 1's
@@ -1083,9 +1093,50 @@ void nt_pp_kernel(const NtArgs a) {
 #undef DMUON_PP_AHI
 #undef DMUON_PP_B
   wait_vmcnt<0>();
+  // a diagonal-tile wave whose values all lie below the diagonal has nothing to store
+  if constexpr (LIM >= -3)
+    nt_epilogue<T, MODE, E>(a, smem, Acc16<8, 4>{acc, lane}, l, bi, bj, i0, j0, lane, wave, wi,
+                            wj);
+}
 
-  nt_epilogue<T, MODE, E>(a, smem, Acc16<8, 4>{acc, lane}, l, bi, bj, i0, j0, lane, wave, wi,
-                          wj);
+template <int BK, int S, int MODE, int E, bool BKM>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void nt_pp_kernel(const NtArgs a) {
+  using T = Tile<256, 256, BK, S, 2, 4>;
+  __shared__ __attribute__((aligned(16))) char smem[T::LDS_BYTES];
+  static_assert(T::LDS_BYTES <= 160 * 1024, "LDS budget");
+  // the decode is the same for every lane; readfirstlane states it, so the buffer descriptors
+  // and offsets built from it stay scalar whatever the compiler's uniformity analysis proves
+  const TilePos tp = decode_tile(a, blockIdx.x, gridDim.x);
+  const int l = __builtin_amdgcn_readfirstlane(tp.l);
+  const int bi = __builtin_amdgcn_readfirstlane(tp.bi), bj = __builtin_amdgcn_readfirstlane(tp.bj);
+  // Which copy of the schedule this wave runs (one call site each: pp_tile is inlined wherever
+  // it is called). 0: every block; on a diagonal tile of an exactly symmetric product, block
+  // (x, y) of a wave (tile rows 128 wi + 16 x, columns 64 wj + 16 y) lies strictly below the
+  // diagonal when 8 wi + x > 4 wj + y and its values are dropped: with c = 4 wj - 8 wi a wave
+  // keeps the blocks with x - y <= c -- all (c >= 7: copy 0), none (c <= -4: 1), x <= y
+  // (c = 0: 2) or x <= y + 4 (c = 4: 3). With group 0 in reversed column order (pp_tile) that
+  // is 32 + 0, 32 + 0, 26 + 10 and 10 + 26 of the 64 MFMAs per slice on the four SIMDs (10, 26,
+  // 42 and 58 in natural order). s_barrier counts waves, not program counters, and every copy
+  // passes the same barriers.
+  // NtArgs::diag_skip chooses how much of that is used: DIAG_SKIP_WAVES only copies 0 and 1.
+  int copy = 0;
+  if constexpr (MODE == EPI_SYM) {
+    if (a.sym_exact && a.tri && bi == bj && a.diag_skip != DIAG_SKIP_NONE) {
+      const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+      const int grp = wave >> 2, v = wave & 3;
+      const int c = 4 * (grp == 0 ? 3 - v : v) - 8 * grp;
+      copy = c <= -4 ? 1 : (c >= 7 || a.diag_skip != DIAG_SKIP_BLOCKS) ? 0 : c == 0 ? 2 : 3;
+    }
+  }
+  if constexpr (MODE == EPI_SYM) {
+    if (copy == 1) pp_tile<BK, S, MODE, E, BKM, -8>(a, smem, l, bi, bj);
+    else if (copy == 2) pp_tile<BK, S, MODE, E, BKM, 0>(a, smem, l, bi, bj);
+    else if (copy == 3) pp_tile<BK, S, MODE, E, BKM, 4>(a, smem, l, bi, bj);
+    else pp_tile<BK, S, MODE, E, BKM, 7>(a, smem, l, bi, bj);
+  } else {
+    pp_tile<BK, S, MODE, E, BKM, 7>(a, smem, l, bi, bj);
+  }
 }
 
 // Compute units of the current device, queried once per device (0 if the query fails).

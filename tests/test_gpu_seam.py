@@ -340,7 +340,8 @@ def test_standalone_ns_on_two_streams_uses_one_workspace_each(gpu):
     """gram_newton_schulz / direct_newton_schulz issued on two streams, interleaved without
     waiting: each stream gets its own NS workspace, and every result equals the same call made
     alone on the default stream."""
-    from dmuon_amd.optim import newton_schulz as nsm
+    import importlib
+    nsm = importlib.import_module("dmuon_amd.optim.newton_schulz")
     Gs = [torch.randn(512, 1536, generator=torch.Generator().manual_seed(70 + i)).to(gpu)
           for i in range(6)]
     ref = [nsm.gram_newton_schulz(g) if i % 3 else nsm.direct_newton_schulz(g)
