@@ -56,14 +56,19 @@ int64_t align256(int64_t b) { return round_up(b, 256); }
 constexpr int kDiagSkipPoly = DIAG_SKIP_BLOCKS;
 constexpr int kDiagSkipGram = DIAG_SKIP_NONE;
 
+// Gram backend: the two Q X products read X itself as their k-major B operand (transposing LDS
+// reads) instead of a transposed copy, so the staging writes one fp16 copy of ns_in (12 B per
+// element instead of 14) and the restart Q X writes X alone, into the second X buffer.
+constexpr bool kGramKmajorQX = true;
+
 // Power-of-two scale of the fp16 NS operand X, both backends (entries of the normalised X are at
 // most 1; the scale keeps the typical ~1/sqrt(mn) entries out of the fp16 subnormal range)
 constexpr float kNsKx = 4096.f;
 
 struct Workspace {
   uint16_t *X, *XT0, *XT1, *Am, *Pm;
-  // Gram backend only: the accumulated polynomial Q and its transpose (ping-pong), P R
-  uint16_t *Q0, *Q1, *Q0T, *Q1T, *Wm;
+  // Gram backend only: the two slots of the accumulated polynomial Q (or its transpose), P R
+  uint16_t *Q0, *Q1, *Wm;
   float *partials, *scale, *scale_sq;
   // correction of a copy staged with an estimated scale (1 when staged exactly), and the
   // per-matrix "stage again" flags
@@ -85,16 +90,16 @@ Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch, int
   const int64_t L = batch;
   const int64_t xs = (int64_t)m_pad * n_pad * 2;
   const int64_t as = (int64_t)m_pad * m_pad * 2;
+  // direct: X and its transposed copy in turn (XT0, XT1); Gram: X and the second X buffer a
+  // restart writes (XT0), plus the two Q slots and P R
   w.X = reinterpret_cast<uint16_t*>(take(L * xs));
   w.XT0 = reinterpret_cast<uint16_t*>(take(L * xs));
-  w.XT1 = reinterpret_cast<uint16_t*>(take(L * xs));
+  if (!gram) w.XT1 = reinterpret_cast<uint16_t*>(take(L * xs));
   w.Am = reinterpret_cast<uint16_t*>(take(L * as));
   w.Pm = reinterpret_cast<uint16_t*>(take(L * as));
   if (gram) {
     w.Q0 = reinterpret_cast<uint16_t*>(take(L * as));
     w.Q1 = reinterpret_cast<uint16_t*>(take(L * as));
-    w.Q0T = reinterpret_cast<uint16_t*>(take(L * as));
-    w.Q1T = reinterpret_cast<uint16_t*>(take(L * as));
     w.Wm = reinterpret_cast<uint16_t*>(take(L * as));
   }
   w.nparts = pre_blocks_per_mat(Rp, Cp);
@@ -249,13 +254,17 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
   // per-matrix correction (ratio for X, ratio_sq for X X^T; 1 after an exact staging). A
   // restart rewrites X exactly scaled.
   bool x_staged = true;
+  // with kGramKmajorQX: the current X and the buffer a restart writes the next one into (the
+  // transposed-copy region XT0 holds m_pad x n_pad values as well)
+  uint16_t* x_cur = w.X;
+  uint16_t* x_nxt = w.XT0;
   // R = alpha X X^T
   auto gram_of_x = [&](uint16_t* R, float alpha) -> int {
     NtArgs s{};
     s.alpha_dev = x_staged ? w.ratio_sq : nullptr;
     s.elt = ELT_F16;
-    s.A = w.X; s.lda = n_pad; s.sA = xs;
-    s.B = w.X; s.ldb = n_pad; s.sB = xs;
+    s.A = x_cur; s.lda = n_pad; s.sA = xs;
+    s.B = x_cur; s.ldb = n_pad; s.sB = xs;
     s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch;
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
     s.sym_exact = 1; s.diag_skip = kDiagSkipGram;
@@ -271,18 +280,31 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     g.alpha_dev = x_staged ? w.ratio : nullptr;
     g.elt = ELT_F16;
     g.A = Q; g.lda = m_pad; g.sA = as;
-    g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
+    if (kGramKmajorQX) {
+      g.B = x_cur; g.ldb = n_pad; g.sB = xs; g.b_kmajor = 1;
+    } else {
+      g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
+    }
     g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch;
     g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.beta = 0.f;
     if (!last) {
       g.alpha = 1.f;
       g.mode = EPI_NS;
-      g.D = w.X; g.ldd = n_pad; g.sD = xs;
-      g.DT = xt_nxt; g.lddt = m_pad; g.sDT = xs;
+      if (kGramKmajorQX) {
+        // X itself is the B operand, so the new X goes to the other buffer
+        g.D = x_nxt; g.ldd = n_pad; g.sD = xs;
+      } else {
+        g.D = w.X; g.ldd = n_pad; g.sD = xs;
+        g.DT = xt_nxt; g.lddt = m_pad; g.sDT = xs;
+      }
       if (timed(PC_GEMM, gemm_flops, 0.0, stream, who, [&] { return launch_nt(g, tile, stream); }))
         return 1;
-      uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
+      if (kGramKmajorQX) {
+        uint16_t* t = x_cur; x_cur = x_nxt; x_nxt = t;
+      } else {
+        uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
+      }
       x_staged = false;
       return 0;
     }
@@ -296,17 +318,15 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
                  [&] { return launch_nt(g, tile, stream); });
   };
   // Q <- P Q = Z Q + a Q as a full product (Q is a product of polynomials that no longer
-  // commute once rounded; its factor order must match R's). Z is symmetric, so the same update
-  // also runs transposed, Q^T <- Q^T Z + a Q^T, reading Q^T as its A operand and addend and
-  // writing Q^T alone. A segment's updates (between a (re)start and the Q X that consumes Q)
-  // therefore run transposed and write only Q^T, except the last two: the second-to-last writes
-  // Q^T and, as its transposed output, Q (the last one reads both), and the last runs as
-  // Z Q + a Q and writes Q, the row form Q X reads. A Q that is still P itself is symmetric: one
-  // buffer serves as both forms.
-  uint16_t* qbuf[2] = {w.Q0, w.Q1};          // row form of each slot's Q (when written)
-  const uint16_t* qtbuf[2] = {w.Q0, w.Q1};   // its transpose
-  enum { Q_TRANS = 0, Q_TRANS_BOTH = 1, Q_ROW = 2 };
-  auto q_update = [&](const uint16_t* Zm, int from, float a_, int form) -> int {
+  // commute once rounded; its factor order must match R's). Z is symmetric, so the update runs
+  // transposed, Q^T <- Q^T Z + a Q^T: Q^T is its A operand and its addend (the K loop takes the
+  // addend's slices last), and the output is Q^T -- except for the last update before the Q X
+  // that consumes Q, which writes only its transposed output, the row form Q that Q X reads.
+  // A Q that is still P itself (after a start or restart) is symmetric and serves as either
+  // form. Two slots, used in turn.
+  uint16_t* qslot[2] = {w.Q0, w.Q1};
+  uint16_t* qbuf[2] = {w.Q0, w.Q1};          // the row form of a slot's Q, once it has one
+  auto q_update = [&](const uint16_t* Zm, int from, float a_, bool last) -> int {
     const int to = 1 - from;
     NtArgs g{};
     g.elt = ELT_F16;
@@ -315,17 +335,11 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     g.mode = EPI_NS; g.alpha = 1.f; g.beta = a_;
     g.lda = g.ldb = g.ldc = g.ldd = g.lddt = m_pad;
     g.sA = g.sB = g.sC = g.sD = g.sDT = as;
-    if (form == Q_ROW) {
-      g.A = Zm; g.B = qtbuf[from]; g.C = qbuf[from];
-      g.D = qbuf[to];
-    } else {
-      uint16_t* qt_to = to ? w.Q1T : w.Q0T;
-      g.A = qtbuf[from]; g.B = Zm; g.C = qtbuf[from];
-      g.c_in = C_IS_A;                         // the addend is the A panel's last slices
-      g.D = qt_to;
-      if (form == Q_TRANS_BOTH) g.DT = qbuf[to];
-      qtbuf[to] = qt_to;
-    }
+    g.A = qslot[from]; g.B = Zm; g.C = qslot[from];
+    g.c_in = C_IS_A;                           // the addend is the A panel's last slices
+    if (last) g.DT = qslot[to];                // Q, the row form
+    else g.D = qslot[to];                      // Q^T
+    qbuf[to] = qslot[to];
     return timed(PC_POLY, full_sq_flops, 0.0, stream, who,
                  [&] { return launch_nt(g, tile, stream); });
   };
@@ -355,21 +369,19 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     const float zr2 = cc / (rs * rs), zr1 = cb / rs;
     if (qs < 0 && !evolve) {
       // Q = Z + a I in one product (Z itself is not needed); symmetric, its own transpose
-      if (sq(R, R, R, qbuf[0], zr2, zr1, ca, true)) return 1;
-      qtbuf[0] = qbuf[0];
+      if (sq(R, R, R, qslot[0], zr2, zr1, ca, true)) return 1;
+      qbuf[0] = qslot[0];
       qs = 0;
       continue;
     }
     if (qs < 0) {
       // Z = c R^2 + b R, and Q = Z + a I written by the same epilogue
-      if (sq(R, R, R, Z, zr2, zr1, 0.f, true, qbuf[0], ca)) return 1;
-      qtbuf[0] = qbuf[0];
+      if (sq(R, R, R, Z, zr2, zr1, 0.f, true, qslot[0], ca)) return 1;
+      qbuf[0] = qslot[0];
       qs = 0;
     } else {
       if (sq(R, R, R, Z, zr2, zr1, 0.f, true)) return 1;   // Z = c R^2 + b R
-      const int left = updates_left(it);
-      const int form = left == 1 ? Q_ROW : left == 2 ? Q_TRANS_BOTH : Q_TRANS;
-      if (q_update(Z, qs, ca, form)) return 1;              // Q <- Z Q + a Q
+      if (q_update(Z, qs, ca, updates_left(it) == 1)) return 1;   // Q <- Z Q + a Q
       qs = 1 - qs;
     }
     if (evolve) {
@@ -462,6 +474,12 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     q.nesterov = nesterov;
     q.kx = kNsKx;
     q.scale = w.scale + l0;
+    // the Gram backend's Q X products read X k-major (kGramKmajorQX): only X is staged, by the
+    // direct write for a wide orientation, by the transposed one for a tall orientation
+    if (gram && kGramKmajorQX) {
+      q.skip_y = tall_ ? 1 : 0;
+      q.skip_yt = tall_ ? 0 : 1;
+    }
     return q;
   };
   const double Ld = batch, md = m, nd = n, elems = (double)rows * cols * batch;

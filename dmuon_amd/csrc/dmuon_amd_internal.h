@@ -85,6 +85,8 @@ struct PreArgs {
   const float* scale; float kx;           // PRE_F16: per-matrix 1/(||ns_in|| + eps), power of 2
   float* const* est_ptrs;                 // PRE_EST: per-matrix scale estimate (device float)
   const int* restage;                     // PRE_F16: optional per-matrix "copy needed" flags
+  // copies not written (the consumer reads the other one): skip_y -- Y, skip_yt -- YT
+  int skip_y, skip_yt;
 };
 hipError_t launch_pre(const PreArgs& a, hipStream_t stream);
 int pre_blocks_per_mat(int Rp, int Cp);

@@ -186,7 +186,7 @@ __device__ __forceinline__ float pre_tile(const PreArgs& a, int l, int r0, int c
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       o[e] = ST == PRE_BF16 ? f2bf(ns[e]) : f2h(__fmul_rn(ns[e], sc));
-    if (row < a.Rp) {
+    if (row < a.Rp && !a.skip_y) {
       uint2 p;
       p.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
       p.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
@@ -195,7 +195,7 @@ __device__ __forceinline__ float pre_tile(const PreArgs& a, int l, int r0, int c
 #pragma unroll
     for (int e = 0; e < 4; ++e) tileT[4 * tc + e][rl] = o[e];
   }
-  if (copy) {   // block-uniform
+  if (copy && !a.skip_yt) {   // block-uniform
     __syncthreads();
     // transposed write: row cl of YT gets 64 consecutive source rows (128 B)
     const int cl = tid >> 2, seg = tid & 3;

@@ -342,7 +342,10 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
     // that the global stores are whole 128-byte row segments (8 B x 16 lanes for a D row,
     // 16 B x 8 lanes for a 64-value D^T row) instead of scattered 2-byte stores.
     static_assert(Acc::SLABS % 2 == 0, "transposed rows pair the slabs");
-    uint16_t* Db = a.D + (long long)l * a.sD;
+    // EPI_NS may write D^T alone (D == nullptr): the last Q update of a Gram segment, which
+    // runs transposed and produces the row form the Q X product reads
+    const bool row_out = MODE == EPI_SYM || a.D != nullptr;
+    uint16_t* Db = row_out ? a.D + (long long)l * a.sD : nullptr;
     uint16_t* DTb = nullptr;
     long long ldt = 0;
     // diagonal tile of a result that must be exactly symmetric: each value computed for (i, j)
@@ -412,9 +415,10 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
       for (int q = 0; q < NQ; ++q) {
         o2[q].x = pack2_elt<E>(r[q][0], r[q][1]);
         o2[q].y = pack2_elt<E>(r[q][2], r[q][3]);
-        *reinterpret_cast<u32x2_t*>(reg + acc.row(q) * T::EPN + acc.col(q) * 2) = o2[q];
+        if (row_out)
+          *reinterpret_cast<u32x2_t*>(reg + acc.row(q) * T::EPN + acc.col(q) * 2) = o2[q];
       }
-      {
+      if (row_out) {
         // the slab as whole 16-byte row chunks (8 lanes per 64-value row), all of its LDS reads
         // ahead of the stores
         static_assert(T::EPN % 16 == 0, "16-byte slab rows");
@@ -1162,6 +1166,9 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   if (a.K <= 0 || a.K % 64 != 0) return hipErrorInvalidValue;
   // the second output relies on the exactly symmetric diagonal-tile path for its diagonal
   if (a.D2 && !(a.mode == EPI_SYM && a.tri && a.sym_exact)) return hipErrorInvalidValue;
+  // an output to write: D for a symmetric product, D or D^T for an NS step
+  if ((a.mode == EPI_SYM && !a.D) || (a.mode == EPI_NS && !a.D && !a.DT))
+    return hipErrorInvalidValue;
   // k-major B: whole-panel buffer range and slice offsets in 32 bits, rows of whole tiles
   if (a.b_kmajor && ((long long)a.K * a.ldb * 2 >= (1LL << 31) || a.ldb < a.N))
     return hipErrorInvalidValue;

@@ -108,7 +108,10 @@ def test_plan(rows, cols, batch, tile, m_pad, n_pad):
     assert ws >= batch * (3 * x + 2 * a)
     tg, mpg, npg, wsg = _C.plan(rows, cols, batch, backend=_C.NS_GRAM)
     assert (tg, mpg, npg) == (tile, m_pad, n_pad)
-    assert wsg >= ws + batch * 3 * a       # R, P and two Q buffers plus R P
+    # direct: X, two transposed copies, A, P; Gram: X and a second X buffer (its Q X products
+    # read X itself), R, Z, two Q slots and P R
+    assert wsg >= batch * (2 * x + 5 * a) and wsg < batch * (2 * x + 6 * a)
+    assert wsg == ws - batch * x + batch * 3 * a or abs(wsg - (ws - batch * x + batch * 3 * a)) < 4096
 
 
 def test_plan_rejects_bad_arguments():
