@@ -396,6 +396,29 @@ def nt_roofline(prof: dict, prof_steps: int) -> dict:
             "launches_per_step": mf_launch // prof_steps}
 
 
+def run_config(torch, dmuon, dev, name: str, ns) -> dict:
+    """The GPU leg of BASELINE config `name` (c1: the literal fp32 plumbing config with Keller's
+    direct NS; c2-c4 with the NS form `ns`)."""
+    if name == "c1":
+        keller = dmuon.NewtonSchulz("direct", coefficients=KELLER)
+        return dict(config_leg(torch, dmuon, dev, [(1024, 1024)], keller, 10, 1, 10,
+                               dtype=torch.float32),
+                    workload="one fp32 1024x1024 weight (its own master), fp32 gradient, zero "
+                             "momentum; lr 0.02, mu 0.95 Nesterov, wd 0.1, 5 direct Keller NS "
+                             "steps; median of 10 steps after the first")
+    if name == "c2":
+        return dict(config_leg(torch, dmuon, dev, [(4096, 4096)], ns, 100, 3, 20,
+                               momentum_init=True),
+                    workload="one bf16 4096x4096 matrix, momentum ~N(0, 0.02^2), 100 timed steps")
+    if name == "c3":
+        return {f"{s[0]}x{s[1]}": config_leg(torch, dmuon, dev, [s], ns, 20, 3, 30 + i)
+                for i, s in enumerate(C3_SHAPES)}
+    if name == "c4":
+        return dict(config_leg(torch, dmuon, dev, C4_SHAPES, ns, 20, 3, 40),
+                    workload="64 x (1408x2048) + 64 x (2048x1408) bf16 expert matrices")
+    raise ValueError(name)
+
+
 def copy_leg(torch, dev, _C, gib: int = 4, reps: int = 5) -> dict:
     """A device-to-device copy of `gib` GiB, read + write bytes over the time: torch's
     Tensor.copy_ and the library's streaming copy (dmuon_stream_copy: one 16-byte chunk per
@@ -461,6 +484,9 @@ def main():
                          "in a second pass")
     ap.add_argument("--overlap-staging", action="store_true",
                     help="Muon(overlap_staging=True): stage the next chunk on a second stream")
+    ap.add_argument("--config-only", choices=("c1", "c2", "c3", "c4"), default=None,
+                    help="only run that BASELINE config leg on the GPU (its own matrices) and "
+                         "print its JSON line (for profiling one config)")
     ap.add_argument("--library-compare", action="store_true",
                     help="only time the NT MFMA kernel against torch's library GEMM "
                          "(hipBLASLt) on one NT-form bf16 product and print that JSON line")
@@ -482,6 +508,12 @@ def main():
     torch.cuda.set_device(dev)
     if args.library_compare:
         print(json.dumps(library_compare(torch, dev, _C)), flush=True)
+        return
+    if args.config_only:
+        ns = (dmuon.NewtonSchulz("gram") if args.ns == "gram" else
+              dmuon.NewtonSchulz("direct", coefficients=KELLER))
+        print(json.dumps({args.config_only: run_config(torch, dmuon, dev, args.config_only,
+                                                       ns)}), flush=True)
         return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)   # 1 GiB
@@ -613,23 +645,8 @@ def main():
 
     configs = None
     if not args.no_configs:
-        keller = dmuon.NewtonSchulz("direct", coefficients=KELLER)
-        configs = {"c1": dict(config_leg(torch, dmuon, dev, [(1024, 1024)], keller, 10, 1, 10,
-                                         dtype=torch.float32),
-                              workload="one fp32 1024x1024 weight (its own master), fp32 "
-                                       "gradient, zero momentum; lr 0.02, mu 0.95 Nesterov, "
-                                       "wd 0.1, 5 direct Keller NS steps; median of 10 steps "
-                                       "after the first")}
-        configs["c2"] = dict(config_leg(torch, dmuon, dev, [(4096, 4096)], ns, 100, 3, 20,
-                                        momentum_init=True),
-                             workload="one bf16 4096x4096 matrix, momentum ~N(0, 0.02^2), "
-                                      "100 timed steps")
-        configs["c3"] = {}
-        for i, shape in enumerate(C3_SHAPES):
-            configs["c3"][f"{shape[0]}x{shape[1]}"] = config_leg(torch, dmuon, dev, [shape], ns,
-                                                                 20, 3, 30 + i)
-        configs["c4"] = dict(config_leg(torch, dmuon, dev, C4_SHAPES, ns, 20, 3, 40),
-                             workload="64 x (1408x2048) + 64 x (2048x1408) bf16 expert matrices")
+        configs = {name: run_config(torch, dmuon, dev, name, ns)
+                   for name in ("c1", "c2", "c3", "c4")}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget, args.ns)
     if configs is not None and not args.no_cpu_baseline:
