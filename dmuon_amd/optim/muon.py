@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import logging
 import math
+import os
 from collections import OrderedDict
 from typing import Optional, Union
 
@@ -121,6 +122,15 @@ class Muon(torch.optim.Optimizer):
         if comm_ctx is None:
             raise ValueError(
                 "Model has no _dedicated_comm_ctx. Call dmuon.dedicate_params() first.")
+        graph_env = os.environ.get("DMUON_NS_CUDA_GRAPH")
+        if graph_env is not None:
+            # the reference's per-shape NS graph cache (ns_graph.py:38-47) has no counterpart:
+            # say so instead of ignoring the switch silently
+            logger.warning(
+                "DMUON_NS_CUDA_GRAPH=%s has no effect in dmuon_amd: each bucket's whole Newton-"
+                "Schulz runs as one C call that enqueues its kernel launches (no per-NS Python "
+                "launch sequence to capture). To remove the host launch cost, capture "
+                "Muon.step itself with torch.cuda.graph after one eager step.", graph_env)
         self.model = model
         self._comm_ctx = comm_ctx
         self._ns = ns_backend

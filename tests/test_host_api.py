@@ -233,3 +233,22 @@ def test_pointer_table_cache(monkeypatch):
     assert c is not b and len(made) == 4
     assert any(t is b for t in opt._captured_tables.values())
     assert not any(t is c or t is a for t in opt._captured_tables.values())
+
+
+def test_ns_graph_switch_is_reported_not_ignored(monkeypatch, caplog):
+    """The reference's DMUON_NS_CUDA_GRAPH (ns_graph.py:38-47) switches its per-shape NS graph
+    cache; this build has no such cache (a group's NS is one C call), so setting the variable
+    logs that it has no effect, naming what to capture instead."""
+    m = _model()
+    dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2)
+    dmuon.replicate(m)
+    monkeypatch.setenv("DMUON_NS_CUDA_GRAPH", "0")
+    with caplog.at_level(logging.WARNING):
+        dmuon.Muon(m)
+    assert "DMUON_NS_CUDA_GRAPH=0 has no effect" in caplog.text
+    assert "torch.cuda.graph" in caplog.text
+    caplog.clear()
+    monkeypatch.delenv("DMUON_NS_CUDA_GRAPH")
+    with caplog.at_level(logging.WARNING):
+        dmuon.Muon(m)
+    assert "DMUON_NS_CUDA_GRAPH" not in caplog.text
