@@ -15,10 +15,13 @@
 // sqrt and division are the correctly rounded ones. For fp32 storage R is the identity.
 //
 // Work split: the tensors are concatenated into one index space (offsets = prefix sums of
-// their sizes); block b takes a contiguous range of it, finds its first tensor by binary
-// search and walks the tensors the range overlaps. Inside a tensor, 8-element vectors
-// (16-byte loads/stores of bf16, two of fp32) cover the aligned middle; ragged ends and
-// tensors whose base pointers are not 16-byte aligned take the per-element path.
+// their sizes); block b takes the contiguous range [4096 b, 4096 (b + 1)) of it, finds its
+// first tensor by binary search and walks the tensors the range overlaps. Small ranges over a
+// grid of the whole index space keep the addresses that the resident blocks touch close
+// together; with a few long ranges per block (8192 blocks over 1.05 G elements) the same
+// kernel moved 4.5 TB/s instead of 5.4 on MI355X. Inside a tensor, 8-element vectors (16-byte
+// loads/stores of bf16, two of fp32) cover the aligned middle; ragged ends and tensors whose
+// base pointers are not 16-byte aligned take the per-element path.
 #include "dmuon_amd_internal.h"
 
 namespace dmuon {
@@ -199,12 +202,12 @@ __global__ __launch_bounds__(256) void adamw_kernel(const AdamWArgs a) {
 
 hipError_t launch_adamw(AdamWArgs a, hipStream_t stream) {
   if (a.total <= 0 || a.n <= 0) return hipSuccess;
-  long long blocks = (a.total + 16383) / 16384;
-  if (blocks > 8192) blocks = 8192;
-  long long per = (a.total + blocks - 1) / blocks;
-  per = (per + 7) & ~7LL;
+  // 4096 elements per block (a multiple of the 8-element vector), more when the grid would
+  // exceed 2^31 blocks
+  long long per = 4096;
+  if ((a.total + per - 1) / per > 0x7fffffffLL) per = ((a.total + 0x7ffffffeLL) / 0x7fffffffLL + 7) & ~7LL;
   a.per_block = per;
-  blocks = (a.total + per - 1) / per;
+  const long long blocks = (a.total + per - 1) / per;
   const dim3 grid((unsigned)blocks), block(256);
   if (a.p_dtype == DT_F32 && a.g_dtype == DT_F32)
     hipLaunchKernelGGL((adamw_kernel<DT_F32, DT_F32>), grid, block, 0, stream, a);

@@ -141,8 +141,9 @@ struct ClipArgs {
   long long n_jobs, chunk;
   float* local_sq;                        // sumsq: per-segment accumulators (added to)
   const float* coefs;                     // scale: per-segment coefficients
+  long long piece;                        // scale: elements per block (set by launch_clip_scale)
 };
 hipError_t launch_clip_sumsq(const ClipArgs& a, hipStream_t stream);
-hipError_t launch_clip_scale(const ClipArgs& a, hipStream_t stream);
+hipError_t launch_clip_scale(ClipArgs a, hipStream_t stream);
 
 }  // namespace dmuon

@@ -231,7 +231,7 @@ def test_kernels_match_oracle_reference_buckets(gpu):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("chunk", [1, 1000, 4097, 65536])
+@pytest.mark.parametrize("chunk", [1, 1000, 4097, 20001, 65536])
 def test_kernels_ragged_chunks_and_unaligned(gpu, chunk):
     _check_against_oracle(_mixed_buckets(gpu), gpu, 2.0, chunk_size=chunk, unaligned=True)
 
