@@ -225,6 +225,9 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
              const char* who) {
   const long long xs = (long long)m_pad * n_pad, as = (long long)m_pad * m_pad;
   const double full_sq_flops = 2.0 * batch * (double)m * m * m;
+  // K loop lengths: the operands are zero past m (n), so the products multiply only m (n)
+  // rounded up to the 64-wide slice, not the tile-padded m_pad (n_pad)
+  const int km = (int)round_up(m, 64), kn = (int)round_up(n, 64);
   auto is_restart = [&](int it) {
     for (int r = 0; r < n_restarts; ++r)
       if (restarts[r] == it) return true;
@@ -238,7 +241,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     s.elt = ELT_F16;
     s.A = A; s.lda = m_pad; s.sA = as;
     s.B = B; s.ldb = m_pad; s.sB = as;
-    s.M = m_pad; s.N = m_pad; s.K = m_pad; s.L = batch;
+    s.M = m_pad; s.N = m_pad; s.K = m_pad; s.L = batch; s.k_loop = km;
     s.mt = s.nt = m_pad / tile;
     s.tiles_per_mat = tri ? tri_tiles(m_pad, tile) : s.mt * s.nt; s.tri = tri ? 1 : 0;
     s.sym_exact = 1; s.diag_skip = kDiagSkipPoly;
@@ -265,7 +268,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     s.elt = ELT_F16;
     s.A = x_cur; s.lda = n_pad; s.sA = xs;
     s.B = x_cur; s.ldb = n_pad; s.sB = xs;
-    s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch;
+    s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch; s.k_loop = kn;
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
     s.sym_exact = 1; s.diag_skip = kDiagSkipGram;
     s.mode = EPI_SYM; s.alpha = alpha;
@@ -285,7 +288,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     } else {
       g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
     }
-    g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch;
+    g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch; g.k_loop = km;
     g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.beta = 0.f;
     if (!last) {
@@ -330,7 +333,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     const int to = 1 - from;
     NtArgs g{};
     g.elt = ELT_F16;
-    g.M = m_pad; g.N = m_pad; g.K = m_pad; g.L = batch;
+    g.M = m_pad; g.N = m_pad; g.K = m_pad; g.L = batch; g.k_loop = km;
     g.mt = g.nt = m_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.mode = EPI_NS; g.alpha = 1.f; g.beta = a_;
     g.lda = g.ldb = g.ldc = g.ldd = g.lddt = m_pad;
@@ -537,6 +540,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   // kNsKx throughout; the first A (eigenvalues ~1/m) carries kr until its polynomial.
   int kr = 1;
   while (kr * 2 <= m && kr < 4096) kr *= 2;
+  const int km = (int)round_up(m, 64), kn = (int)round_up(n, 64);   // K loops (zero past m, n)
   for (int it = 0; it < T; ++it) {
     const float ca = coeffs[3 * it], cb = coeffs[3 * it + 1], cc = coeffs[3 * it + 2];
     const float rs = it == 0 ? (float)kr : 1.f;   // the stored A is rs * (X X^T)
@@ -545,7 +549,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     s.elt = ELT_F16;
     s.A = w.X; s.lda = n_pad; s.sA = xs;
     s.B = w.X; s.ldb = n_pad; s.sB = xs;
-    s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch;
+    s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch; s.k_loop = kn;
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
     s.sym_exact = 1; s.diag_skip = kDiagSkipGram;
     s.mode = EPI_SYM; s.alpha = rs / (kNsKx * kNsKx); s.beta = 0.f; s.diag = 0.f;
@@ -558,7 +562,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     q.elt = ELT_F16;
     q.A = w.Am; q.lda = m_pad; q.sA = as;
     q.B = w.Am; q.ldb = m_pad; q.sB = as;
-    q.M = m_pad; q.N = m_pad; q.K = m_pad; q.L = batch;
+    q.M = m_pad; q.N = m_pad; q.K = m_pad; q.L = batch; q.k_loop = km;
     q.mt = q.nt = m_pad / tile; q.tiles_per_mat = s.tiles_per_mat; q.tri = 1;
     q.sym_exact = 1; q.diag_skip = kDiagSkipPoly;
     q.mode = EPI_SYM; q.alpha = cc / (rs * rs); q.beta = cb / rs; q.diag = 0.f;
@@ -572,7 +576,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     g.elt = ELT_F16;
     g.A = w.Pm; g.lda = m_pad; g.sA = as;
     g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
-    g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch;
+    g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch; g.k_loop = km;
     g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.alpha = it + 1 < T ? 1.f : 1.f / kNsKx; g.beta = ca;
     g.alpha_dev = it == 0 ? w.ratio : nullptr;

@@ -24,6 +24,10 @@ struct NtArgs {
   const uint16_t* A; long long lda, sA;   // elt [L][M][K], row stride lda, batch stride sA
   const uint16_t* B; long long ldb, sB;   // elt [L][N][K]
   int M, N, K, L;                         // multiples of the tile sizes (host pads)
+  // K elements the loop multiplies (0: K), a multiple of 64: the operands are zero-padded
+  // past it, so the slices beyond add nothing (an m x m product padded to a tile multiple
+  // loops over m rounded up to 64 only)
+  int k_loop;
   int mt, nt, tiles_per_mat, tri;         // tile grid; tri: upper-triangle tiles of an MxM result
   int mode;
   float alpha, beta, diag;

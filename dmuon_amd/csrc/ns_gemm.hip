@@ -259,11 +259,11 @@ struct Occupancy {
 
 // First K slice of the tile's loop (see NtArgs::c_in): the slices that hold the tile's addend
 // values -- columns j0.. of A (C is A) or rows i0.. of B (C is B), read in the 256-aligned block
-// that contains them -- come last.
+// that contains them -- come last (a block that ends past the loop's KT slices starts it at 0).
 __device__ __forceinline__ int first_slice(const NtArgs& a, int i0, int j0, int BK, int KT) {
   if (a.c_in == C_NONE) return 0;
   const int blk = (a.c_in == C_IS_A ? j0 : i0) / 256 + 1;
-  return (blk * 256 / BK) % KT;
+  return min(blk * 256 / BK, KT) % KT;
 }
 
 // Logical tile of this block: matrix l of the batch, tile row bi, tile column bj.
@@ -792,7 +792,7 @@ void nt_mfma_kernel(const NtArgs a) {
 #pragma unroll
     for (int y = 0; y < BJ; ++y) acc[x][y] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int KT = a.K / BK;
+  const int KT = (a.k_loop > 0 ? a.k_loop : a.K) / BK;
   const int kt0 = __builtin_amdgcn_readfirstlane(first_slice(a, i0, j0, BK, KT));
   auto rot = [&](int t) { return t + kt0 >= KT ? t + kt0 - KT : t + kt0; };
   constexpr int KS = BK / 32;                     // MFMA substeps per slice
@@ -1033,7 +1033,7 @@ __device__ __forceinline__ void pp_tile(const NtArgs& a, char* smem, int l, int 
           if (x - y <= LIM) acc[x][y] = mfma_16x16x32<E>(bfr[ks][y], af[ks][x], acc[x][y]);
   };
 
-  const int KT = a.K / BK;
+  const int KT = (a.k_loop > 0 ? a.k_loop : a.K) / BK;
   const int kt0 = __builtin_amdgcn_readfirstlane(first_slice(a, i0, j0, BK, KT));
   auto rot = [&](int t) { return t + kt0 >= KT ? t + kt0 - KT : t + kt0; };
   if (grp == 1) {
@@ -1183,6 +1183,7 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
       !(a.C == a.B && a.K == a.M && a.M == a.N && a.ldc == a.ldb && (a.L <= 1 || a.sC == a.sB)))
     return hipErrorInvalidValue;
   if (a.c_in != C_NONE && a.c_in != C_IS_A && a.c_in != C_IS_B) return hipErrorInvalidValue;
+  if (a.k_loop < 0 || a.k_loop > a.K || a.k_loop % 64 != 0) return hipErrorInvalidValue;
   dim3 grid((unsigned)nb);
 #define DMUON_NT3(TILE, BK, S, WM, WN, E, KM)                                                  \
   do {                                                                                         \

@@ -57,6 +57,16 @@ int main() {
   a = square(buf, 512, 512, 512);
   a.c_in = 7;
   expect_refused("unknown c_in code", a);
+  // the K loop may stop short of K only at a slice boundary inside the operands
+  a = square(buf, 512, 512, 512);
+  a.k_loop = 576;
+  expect_refused("k_loop=576 > K=512", a);
+  a = square(buf, 512, 512, 512);
+  a.k_loop = 480;
+  expect_refused("k_loop=480 not a multiple of 64", a);
+  a = square(buf, 512, 512, 512);
+  a.k_loop = -64;
+  expect_refused("k_loop < 0", a);
   if (bad) {
     printf("%d case(s) not refused\n", bad);
     return 1;

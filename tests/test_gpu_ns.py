@@ -315,14 +315,17 @@ def test_rank_deficient_special_cases(gpu, backend):
 
 @pytest.mark.parametrize("backend", ["gram", "direct"])
 @pytest.mark.parametrize("shape,L", [((256, 768), 1), ((512, 512), 2), ((1024, 3072), 1),
-                                     ((768, 256), 3), ((1024, 1024), 1)])
+                                     ((768, 256), 3), ((1024, 1024), 1), ((384, 640), 2),
+                                     ((640, 384), 1), ((1408, 2048), 1)])
 def test_tile_sizes_give_the_same_bits(gpu, shape, L, backend):
-    """With m a multiple of 256 the 256-tile ping-pong kernel and the 128-tile kernels give the
-    same bits. On the diagonal tiles of the exactly symmetric products (X X^T, the R / Z / W
-    polynomials) the ping-pong kernel computes only the 16x16 blocks on or above the diagonal,
-    group 0 takes its columns in reversed order and two waves do no MFMA work at all; the
-    128-tile kernels compute every block. Equal bits show the skipped blocks are exactly the
-    dropped ones."""
+    """The 256-tile ping-pong kernel and the 128-tile kernels give the same bits. On the
+    diagonal tiles of the exactly symmetric products (X X^T, the R / Z / W polynomials) the
+    ping-pong kernel computes only the 16x16 blocks on or above the diagonal, group 0 takes its
+    columns in reversed order and two waves do no MFMA work at all; the 128-tile kernels compute
+    every block. Equal bits show the skipped blocks are exactly the dropped ones. For an m that
+    is not a multiple of 256 the two tile sizes pad the matrices differently (384 -> 512 or 384,
+    1408 -> 1536 or 1408); the K loops run over m (n) rounded up to 64 either way, so every value
+    is summed in the same order."""
     coeffs = o.POLAR_EXPRESS if backend == "gram" else o.KELLER
     Gs = [_g(shape, seed=31 * i + shape[0]).to(gpu) for i in range(L)]
     u128 = newton_schulz_batched(Gs, coeffs, tile=128, backend=backend, restart_iterations=[2])
