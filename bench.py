@@ -286,6 +286,63 @@ def library_compare(torch, dev, _C, reps: int = 10, rounds: int = 3) -> dict:
     return out
 
 
+def tile_cost(torch, dev, _C, reps: int = 5, rounds: int = 3) -> dict:
+    """Fixed cost per tile of the 256-tile triangle products: dmuon_syrk (fp16, upper-triangle
+    tiles, lower triangle written as the mirror) over 64 matrices of 4096 x 4096 outputs (8704
+    tiles = 34 waves on 256 CUs) at K = 64 .. 4096, without and with an addend C. Time per tile
+    wave is linear in K; the intercept of a least-squares line is the per-tile cost that does
+    not scale with K (block start, first slices' latency, epilogue), the slope the main loop."""
+    L, M, ks = 64, 4096, (64, 256, 1024, 2048, 4096)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    waves = L * (M // 256) * (M // 256 + 1) / 2 / cus
+    g = torch.Generator(device=dev).manual_seed(0)
+    A = (torch.randn(L * M * max(ks), device=dev, generator=g) * 0.02).to(torch.float16)
+    C = (torch.randn(L, M, M, device=dev, generator=g) * 0.02).to(torch.float16)
+    D = torch.empty(L, M, M, device=dev, dtype=torch.float16)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def call(K, addend):
+        _C.call("dmuon_syrk", _C.DTYPE_F16, A.data_ptr(), K, M * K, None, 0, 0,
+                C.data_ptr() if addend else None, M, M * M, D.data_ptr(), M, M * M, M, K, L,
+                1.0, 0.5 if addend else 0.0, 0.0, None, 256, None, 0, stream)
+
+    out = {"metric": "NT triangle product: fixed cost per tile wave", "matrices": L,
+           "M": M, "tiles": int(L * (M // 256) * (M // 256 + 1) // 2), "cus": cus,
+           "tile_waves": round(waves, 2), "dtype": "fp16",
+           "timing": f"median of {rounds} rounds of {reps} calls per point"}
+    for addend in (False, True):
+        us = {}
+        for K in ks:
+            for _ in range(2):
+                call(K, addend)
+            torch.cuda.synchronize()
+            t = []
+            with quiet_gc():
+                for _ in range(rounds):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(reps):
+                        call(K, addend)
+                    e1.record()
+                    torch.cuda.synchronize()
+                    t.append(e0.elapsed_time(e1) / reps * 1e3)
+            us[K] = sorted(t)[len(t) // 2]
+        per_wave = {K: v / waves for K, v in us.items()}
+        n = len(ks)
+        mk = sum(ks) / n
+        mt = sum(per_wave.values()) / n
+        slope = (sum((k - mk) * (per_wave[k] - mt) for k in ks)
+                 / sum((k - mk) ** 2 for k in ks))
+        fixed = mt - slope * mk
+        out["with_addend" if addend else "mirror_only"] = {
+            "us_per_launch": {str(k): round(v, 1) for k, v in us.items()},
+            "us_per_tile_wave": {str(k): round(v, 2) for k, v in per_wave.items()},
+            "fixed_us_per_tile_wave": round(fixed, 2),
+            "us_per_tile_wave_per_1024_k": round(slope * 1024, 2),
+            "fixed_fraction_at_k": {str(k): round(fixed / per_wave[k], 3) for k in ks}}
+    return out
+
+
 @contextlib.contextmanager
 def quiet_gc():
     """Python's cyclic garbage collector off inside a timed region (after one full collection):
@@ -487,6 +544,9 @@ def main():
     ap.add_argument("--config-only", choices=("c1", "c2", "c3", "c4"), default=None,
                     help="only run that BASELINE config leg on the GPU (its own matrices) and "
                          "print its JSON line (for profiling one config)")
+    ap.add_argument("--tile-cost", action="store_true",
+                    help="only measure the triangle products' fixed cost per tile wave (a K "
+                         "sweep of dmuon_syrk) and print that JSON line")
     ap.add_argument("--library-compare", action="store_true",
                     help="only time the NT MFMA kernel against torch's library GEMM "
                          "(hipBLASLt) on one NT-form bf16 product and print that JSON line")
@@ -508,6 +568,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.library_compare:
         print(json.dumps(library_compare(torch, dev, _C)), flush=True)
+        return
+    if args.tile_cost:
+        print(json.dumps(tile_cost(torch, dev, _C)), flush=True)
         return
     if args.config_only:
         ns = (dmuon.NewtonSchulz("gram") if args.ns == "gram" else
