@@ -53,11 +53,16 @@ __device__ __forceinline__ void st1(void* p, long long i, float x) {
   else static_cast<float*>(p)[i] = x;
 }
 
-// 8 consecutive elements starting at element i (i % 8 == 0, base 16-byte aligned)
+// 8 consecutive elements starting at element i (i % 8 == 0, base 16-byte aligned). Every
+// stream is read and written once per step, so all vector accesses are non-temporal: on MI355X
+// the c5 AdamW bucket (1.05 G bf16 elements) took 2.59 ms this way against 2.75 with ordinary
+// loads and stores (non-temporal loads or stores alone: 2.81 and 2.73 ms; the gradient's loads
+// alone 2.69).
 template <int D>
 __device__ __forceinline__ void ld8(const void* p, long long i, float* x) {
   if constexpr (D == DT_BF16) {
-    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + i);
+    const u32x4_t w = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(p) + i));
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       x[2 * k] = bf2f(w[k] & 0xffff);
@@ -65,7 +70,7 @@ __device__ __forceinline__ void ld8(const void* p, long long i, float* x) {
     }
   } else {
     const u32x4_t* q = reinterpret_cast<const u32x4_t*>(static_cast<const float*>(p) + i);
-    const u32x4_t w0 = q[0], w1 = q[1];
+    const u32x4_t w0 = __builtin_nontemporal_load(q), w1 = __builtin_nontemporal_load(q + 1);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       x[k] = __uint_as_float(w0[k]);
@@ -80,13 +85,13 @@ __device__ __forceinline__ void st8(void* p, long long i, const float* x) {
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       w[k] = (unsigned)f2bf(x[2 * k]) | ((unsigned)f2bf(x[2 * k + 1]) << 16);
-    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p) + i) = w;
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(p) + i));
   } else {
     u32x4_t* q = reinterpret_cast<u32x4_t*>(static_cast<float*>(p) + i);
-    q[0] = u32x4_t{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
-                   __float_as_uint(x[3])};
-    q[1] = u32x4_t{__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]),
-                   __float_as_uint(x[7])};
+    __builtin_nontemporal_store(u32x4_t{__float_as_uint(x[0]), __float_as_uint(x[1]),
+                                        __float_as_uint(x[2]), __float_as_uint(x[3])}, q);
+    __builtin_nontemporal_store(u32x4_t{__float_as_uint(x[4]), __float_as_uint(x[5]),
+                                        __float_as_uint(x[6]), __float_as_uint(x[7])}, q + 1);
   }
 }
 
