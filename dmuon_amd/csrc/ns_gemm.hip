@@ -324,14 +324,28 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
   static_assert(Acc::SLABS * 32 == T::WTM && NQ * 4 * 64 == 32 * T::WTN, "accumulator layout");
   const int iw = i0 + wi * T::WTM, jw = j0 + wj * T::WTN;
   const uint16_t* Cb = a.C ? a.C + (long long)l * a.sC : nullptr;
-  // addend C (X for the NS step, A for the polynomial), one 32-row slab at a time, the next
-  // slab's loads in flight while the current one is processed: group q of slab x is 4 values at
-  // row iw + 32x + row(q), columns jw + col(q) .. +3
+  // addend C in the accumulator layout (the final step's epilogue), one 32-row slab at a time:
+  // group q of slab x is 4 values at row iw + 32x + row(q), columns jw + col(q) .. +3
   auto load_c = [&](int x, u32x2_t* dst) {
     const uint16_t* crow = Cb + (long long)(iw + 32 * x) * a.ldc + jw;
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
       dst[q] = *reinterpret_cast<const u32x2_t*>(crow + (long long)acc.row(q) * a.ldc + acc.col(q));
+  };
+  // the same slab read row by row, whole 128-byte lines per instruction (WTN / 4 lanes per row,
+  // 4 values each): group q of slab x is row iw + 32x + CRI q + lane / CLR, columns
+  // jw + 4 (lane % CLR) .. +3. The SYM / NS epilogues pass these through the wave's LDS slab to
+  // the accumulator layout: the accumulator-layout loads above touch 16 lines per instruction
+  // for 32 bytes each, which made the addend read cost twice as long per tile (measured on a
+  // 34-wave triangle product: ~190 us per launch against ~90)
+  constexpr int CLR = T::WTN / 4, CRI = 64 / CLR;
+  static_assert(CRI * NQ == 32, "coalesced addend groups cover the slab");
+  auto load_c_rows = [&](int x, u32x2_t* dst) {
+    const uint16_t* crow =
+        Cb + (long long)(iw + 32 * x + lane / CLR) * a.ldc + jw + 4 * (lane % CLR);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      dst[q] = *reinterpret_cast<const u32x2_t*>(crow + (long long)(CRI * q) * a.ldc);
   };
   float s = a.alpha;
   if (a.alpha_dev) s *= a.alpha_dev[l];
@@ -369,10 +383,23 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
       if (a.D2) D2b = a.D2 + (long long)l * a.sD;
     }
     u32x2_t cbuf[2][NQ];
-    if (Cb) load_c(0, cbuf[0]);
+    if (Cb) load_c_rows(0, cbuf[0]);
 #pragma unroll
     for (int x = 0; x < Acc::SLABS; ++x) {
-      if (Cb && x + 1 < Acc::SLABS) load_c(x + 1, cbuf[(x + 1) & 1]);
+      if (Cb) {
+        // slab x's addend rows into the wave's slab area, read back in accumulator layout (one
+        // wave's LDS accesses complete in order, so neither needs a barrier; the previous
+        // slab's reads of this area were issued before)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          *reinterpret_cast<u32x2_t*>(reg + (CRI * q + lane / CLR) * T::EPN +
+                                      8 * (lane % CLR)) = cbuf[x & 1][q];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          cbuf[x & 1][q] = *reinterpret_cast<const u32x2_t*>(reg + acc.row(q) * T::EPN +
+                                                               acc.col(q) * 2);
+      }
+      if (Cb && x + 1 < Acc::SLABS) load_c_rows(x + 1, cbuf[(x + 1) & 1]);
       // r = s v + beta c (SYM; + diag where i == j) or s (v + beta c) (NS), rounded to E. The
       // tests that do not depend on the element -- an addend at all, a slab that meets the
       // diagonal -- are taken once per slab; without C the addend term is the constant
