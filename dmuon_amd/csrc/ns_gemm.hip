@@ -324,20 +324,13 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
   static_assert(Acc::SLABS * 32 == T::WTM && NQ * 4 * 64 == 32 * T::WTN, "accumulator layout");
   const int iw = i0 + wi * T::WTM, jw = j0 + wj * T::WTN;
   const uint16_t* Cb = a.C ? a.C + (long long)l * a.sC : nullptr;
-  // addend C in the accumulator layout (the final step's epilogue), one 32-row slab at a time:
-  // group q of slab x is 4 values at row iw + 32x + row(q), columns jw + col(q) .. +3
-  auto load_c = [&](int x, u32x2_t* dst) {
-    const uint16_t* crow = Cb + (long long)(iw + 32 * x) * a.ldc + jw;
-#pragma unroll
-    for (int q = 0; q < NQ; ++q)
-      dst[q] = *reinterpret_cast<const u32x2_t*>(crow + (long long)acc.row(q) * a.ldc + acc.col(q));
-  };
-  // the same slab read row by row, whole 128-byte lines per instruction (WTN / 4 lanes per row,
-  // 4 values each): group q of slab x is row iw + 32x + CRI q + lane / CLR, columns
-  // jw + 4 (lane % CLR) .. +3. The SYM / NS epilogues pass these through the wave's LDS slab to
-  // the accumulator layout: the accumulator-layout loads above touch 16 lines per instruction
-  // for 32 bytes each, which made the addend read cost twice as long per tile (measured on a
-  // 34-wave triangle product: ~190 us per launch against ~90)
+  // addend C (X for the NS step, A for the polynomial), one 32-row slab at a time, read row by
+  // row in whole 128-byte lines per instruction (WTN / 4 lanes per row, 4 values each): group q
+  // of slab x is row iw + 32x + CRI q + lane / CLR, columns jw + 4 (lane % CLR) .. +3. The
+  // epilogues pass it through the wave's LDS slab to the accumulator layout: loading it in that
+  // layout directly touches 16 lines per instruction for 32 bytes each, which made the addend
+  // read cost twice as long per tile (measured on a 34-wave triangle product: ~190 us per
+  // launch against ~90)
   constexpr int CLR = T::WTN / 4, CRI = 64 / CLR;
   static_assert(CRI * NQ == 32, "coalesced addend groups cover the slab");
   auto load_c_rows = [&](int x, u32x2_t* dst) {
@@ -560,7 +553,19 @@ __device__ __forceinline__ void nt_epilogue(const NtArgs& a, char* smem, const A
 #pragma unroll
     for (int x = 0; x < Acc::SLABS; ++x) {
       u32x2_t cfin[NQ];
-      if (Cb) load_c(x, cfin);
+      if (Cb) {
+        // the addend's rows as whole lines, through the slab area into the accumulator layout
+        // (all of them read back before the fp32 values below overwrite the area)
+        load_c_rows(x, cfin);
+        char* reg = smem + wave * T::EPI_REGION;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          *reinterpret_cast<u32x2_t*>(reg + (CRI * q + lane / CLR) * T::EPN +
+                                      8 * (lane % CLR)) = cfin[q];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          cfin[q] = *reinterpret_cast<const u32x2_t*>(reg + acc.row(q) * T::EPN + acc.col(q) * 2);
+      }
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         float cv[4] = {0.f, 0.f, 0.f, 0.f};
