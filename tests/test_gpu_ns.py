@@ -316,7 +316,7 @@ def test_rank_deficient_special_cases(gpu, backend):
 @pytest.mark.parametrize("backend", ["gram", "direct"])
 @pytest.mark.parametrize("shape,L", [((256, 768), 1), ((512, 512), 2), ((1024, 3072), 1),
                                      ((768, 256), 3), ((1024, 1024), 1), ((384, 640), 2),
-                                     ((640, 384), 1), ((1408, 2048), 1)])
+                                     ((640, 384), 1), ((1408, 2048), 1), ((1100, 1900), 2)])
 def test_tile_sizes_give_the_same_bits(gpu, shape, L, backend):
     """The 256-tile ping-pong kernel and the 128-tile kernels give the same bits. On the
     diagonal tiles of the exactly symmetric products (X X^T, the R / Z / W polynomials) the
@@ -324,8 +324,8 @@ def test_tile_sizes_give_the_same_bits(gpu, shape, L, backend):
     columns in reversed order and two waves do no MFMA work at all; the 128-tile kernels compute
     every block. Equal bits show the skipped blocks are exactly the dropped ones. For an m that
     is not a multiple of 256 the two tile sizes pad the matrices differently (384 -> 512 or 384,
-    1408 -> 1536 or 1408); the K loops run over m (n) rounded up to 64 either way, so every value
-    is summed in the same order."""
+    1408 -> 1536 or 1408, 1100 x 1900 -> 1280 x 2048 or 1152 x 1920); the K loops run over m (n)
+    rounded up to 64 either way (1152, 1920), so every value is summed in the same order."""
     coeffs = o.POLAR_EXPRESS if backend == "gram" else o.KELLER
     Gs = [_g(shape, seed=31 * i + shape[0]).to(gpu) for i in range(L)]
     u128 = newton_schulz_batched(Gs, coeffs, tile=128, backend=backend, restart_iterations=[2])
