@@ -189,6 +189,60 @@ def test_zero_and_non_contiguous_gradients(gpu, backend):
             assert torch.equal(x, y)
 
 
+class _MatsBias(nn.Module):
+    def __init__(self, device):
+        super().__init__()
+        gen = torch.Generator().manual_seed(21)
+        self.ws = nn.ParameterList(
+            [nn.Parameter((torch.randn(256, 640, generator=gen) * 0.02).to(device)) for _ in range(3)])
+        self.bias = nn.Parameter((torch.randn(640, generator=gen) * 0.02).to(device))
+
+
+@pytest.mark.parametrize("backend", ["gram", "direct"])
+def test_params_without_gradients_are_skipped(gpu, backend):
+    """A dedicated matrix or an AdamW-routed parameter whose gradient is None in a step is left
+    exactly as it was -- weight, momentum buffer, AdamW moments and step count -- as the
+    reference's per-parameter loops skip it (muon.py:1639, :1848); the matrices that do have a
+    gradient get the same bits as in the step where every matrix has one (a group of two
+    against a group of three)."""
+    runs = []
+    for skip in (True, False):
+        m = _MatsBias(gpu)
+        dmuon.dedicate_params(m, None, lambda n, p: p.dim() == 2)
+        dmuon.replicate(m)
+        opt = dmuon.Muon(m, lr=0.02, momentum=0.95, weight_decay=0.1, adamw_lr=1e-3,
+                         ns_backend=backend)
+        ps = list(m.ws)
+        gen = torch.Generator().manual_seed(9)
+        for step in range(2):
+            for q in ps:
+                q.grad = (torch.randn(256, 640, generator=gen) * 0.02).to(gpu)
+            m.bias.grad = (torch.randn(640, generator=gen) * 0.02).to(gpu)
+            if step == 1 and skip:
+                ps[1].grad = None
+                m.bias.grad = None
+                dps = dmuon.get_owned_params(m)
+                before = (ps[1].detach().clone(),
+                          opt.state[id(dps[1])]["momentum_buffer"].detach().clone(),
+                          m.bias.detach().clone(),
+                          opt.state[m.bias]["exp_avg"].detach().clone(),
+                          opt.state[m.bias]["exp_avg_sq"].detach().clone(),
+                          opt.state[m.bias]["step"])
+            opt.step()
+        torch.cuda.synchronize()
+        if skip:
+            dps = dmuon.get_owned_params(m)
+            after = (ps[1].detach(), opt.state[id(dps[1])]["momentum_buffer"].detach(),
+                     m.bias.detach(), opt.state[m.bias]["exp_avg"].detach(),
+                     opt.state[m.bias]["exp_avg_sq"].detach(), opt.state[m.bias]["step"])
+            for x, y in zip(before[:5], after[:5]):
+                assert torch.equal(x, y)
+            assert before[5] == after[5] == 1
+        runs.append([ps[0].detach().clone(), ps[2].detach().clone()])
+    for x, y in zip(runs[0], runs[1]):
+        assert torch.equal(x, y)
+
+
 @pytest.mark.parametrize("shapes", [
     [(256, 4096), (4096, 256), (1024, 3584), (3584, 1024), (512, 2048)],   # c3 aspect ratios / 4
     [(176, 256)] * 8 + [(256, 176)] * 8,                                    # c4 MoE batch / 8
