@@ -69,6 +69,48 @@ def test_gram_call_sequence_fp16(gpu, m, n):
     _check_close(Rn, _mm(RZ, Z.t()) + a * RZ.float(), rel=2e-2, fro_tol=2e-2)
 
 
+@pytest.mark.parametrize("M", [128, 256])
+@pytest.mark.parametrize("scale", [1e-4, 0.01, 1.0, 10.0])
+def test_input_magnitudes_stay_finite(gpu, M, scale):
+    """The reference's SYRK stability cases (tests/unit/test_syrk_stress.py:300-346): fp16
+    operands of K = 512 at scales 1e-4 .. 10 (A A^T up to ~5e4, inside fp16's range) give no NaN
+    or Inf, with and without C, alpha and beta; and the values match torch fp32 on the same
+    16-bit inputs -- at scale 1e-4 the products (~1e-7 .. 5e-6) are fp16 subnormals, where the
+    bound is two subnormal steps (2^-24 each) from the fp32 result rounded to fp16."""
+    g = torch.Generator().manual_seed(42)
+    A = (torch.randn(M, 512, generator=g) * scale).to(torch.float16).to(gpu)
+    C = torch.randn(M, M, generator=g) * scale
+    C = ((C + C.t()) / 2).to(torch.float16).to(gpu)
+    out = torch.empty(M, M, dtype=torch.float16, device=gpu)
+    syrk_or_cublas(A, out)
+    out2 = torch.empty_like(out)
+    syrk_or_cublas(A, out2, C=C, alpha=0.5, beta=0.3)
+    for o_, ref in ((out, _mm(A, A.t())), (out2, 0.5 * _mm(A, A.t()) + 0.3 * C.float())):
+        assert torch.isfinite(o_).all()
+        if scale >= 0.01:
+            _check_close(o_, ref)
+        else:
+            assert (o_.float() - ref.half().float()).abs().max().item() <= 2 * 2.0 ** -24
+
+
+def test_diag_add_zero_is_bit_identical_to_none(gpu):
+    """diag_add in {0, 1, -3.5} adds that multiple of I to the symmetric product, and 0 gives
+    the same bits as no diagonal term (the reference's tests/unit/test_syrk.py:99-136)."""
+    X = _x(256, 640, 3, gpu)
+    R = torch.empty(256, 256, dtype=torch.float16, device=gpu)
+    syrk_or_cublas(X, R)
+    base = torch.empty_like(R)
+    syrk_or_cublas(R, base, C=R, alpha=0.7, beta=-0.2)
+    for d in (0.0, 1.0, -3.5):
+        out = torch.empty_like(R)
+        syrk_or_cublas(R, out, C=R, alpha=0.7, beta=-0.2, diag_add=d)
+        if d == 0.0:
+            assert torch.equal(out, base)
+        else:
+            _check_close(out, 0.7 * _mm(R, R.t()) - 0.2 * R.float() +
+                         d * torch.eye(256, device=gpu))
+
+
 def test_padded_path_equals_in_place_path(gpu):
     """The same numbers through the in-place path (aligned) and the padded path (a base 2
     bytes off, or K not a multiple of 64 completed by zero columns) give the same bits."""
