@@ -9,6 +9,8 @@ Small sizes: against the CPU oracle on identical seeded inputs --
 Full BASELINE sizes: size-independent properties -- transpose equivariance, scale invariance,
 bit-exact determinism, and the closed-form spectrum (singular values of U equal f(sigma(X))).
 """
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -271,6 +273,66 @@ def test_moe_batch_gram_full_size(gpu):
         single = newton_schulz_batched([mats[37]], o.POLAR_EXPRESS, tile=tile, backend="gram",
                                        restart_iterations=[2])[0]
         assert torch.equal(single, outs[37])
+
+
+def _spectrum(kind, m, rng):
+    """Singular values of the kinds the reference's precision suite samples
+    (tests/precision/matrix_zoo.py:23-86): well-conditioned uniform, a Gaussian m x 2m matrix's
+    (Marchenko-Pastur), power law i^-a, exponential decay exp(-b i / m), and a bulk with a 10%
+    tail scaled by 1e-3; each normalised to a largest value of 1."""
+    if kind == "uniform":
+        lo, hi = 0.25 + 0.1 * rng.random(), 0.9 + 0.1 * rng.random()
+        s = np.linspace(hi, lo, m) + 0.1 * (hi - lo) * (rng.random(m) - 0.5)
+        s = np.maximum(s, 0.05)
+    elif kind == "marchenko_pastur":
+        s = np.linalg.svd(rng.standard_normal((m, 2 * m)), compute_uv=False)
+    elif kind == "power_law":
+        s = np.arange(1, m + 1, dtype=np.float64) ** -(0.3 + 0.4 * rng.random())
+    elif kind == "exponential":
+        s = np.exp(-(2.0 + 6.0 * rng.random()) * np.arange(m) / m)
+    else:
+        s = rng.random(m)
+        s[-max(1, m // 10):] *= 1e-3
+    s = np.sort(s)[::-1]
+    return s / s.max()
+
+
+@pytest.mark.parametrize("backend", ["gram", "direct"])
+@pytest.mark.parametrize("kind", ["uniform", "marchenko_pastur", "power_law", "exponential",
+                                  "heavy_tail"])
+def test_spectrum_kinds_vs_closed_form(gpu, kind, backend):
+    """G = U diag(s) V^T with random orthogonal U, V and s from each kind of spectrum, wide and
+    tall: the device NS's distance to the exact output of the same polynomial (U f(S) V^T) is
+    no larger than the reference fp16 pipeline's own, and the two are within the 2e-2 gate of
+    each other -- or, for the ill-conditioned kinds, where the reference's fp16 Gram pipeline
+    itself lands 1-2% from the exact output (exponential: 1.4-1.6%), within 2.5 times that
+    distance (the two pipelines round X and the products differently, so they err in different
+    directions)."""
+    coeffs = o.POLAR_EXPRESS if backend == "gram" else o.KELLER
+    ref_fn = ((lambda g: o.gram_ns(g, coeffs, [2], dtype="fp16")) if backend == "gram"
+              else (lambda g: o.direct_ns(g, coeffs, dtype="fp16")))
+    rng = np.random.default_rng(zlib.crc32(kind.encode()))
+    m, n = 384, 1152
+    out = []
+    for tall in (False, True):
+        s = _spectrum(kind, m, rng)
+        Uo, _ = np.linalg.qr(rng.standard_normal((m, m)))
+        Vo, _ = np.linalg.qr(rng.standard_normal((n, m)))
+        G = (Uo * (0.02 * s)[None, :]) @ Vo.T
+        if tall:
+            G = G.T.copy()
+        Gt = torch.from_numpy(G).float()
+        U = newton_schulz_batched([Gt.to(gpu)], coeffs, backend=backend,
+                                  restart_iterations=[2])[0].cpu().double().numpy()
+        assert np.isfinite(U).all()
+        cf = o.closed_form_ns(Gt.double().numpy(), coeffs)
+        ref = ref_fn(Gt.numpy())
+        e_ref, e_cf, e_cf_ref = o.rel_fro(U, ref), o.rel_fro(U, cf), o.rel_fro(ref, cf)
+        out.append(f"{'tall' if tall else 'wide'}: vs reference fp16 {e_ref:.2e}, vs exact "
+                   f"{e_cf:.2e} (reference fp16 {e_cf_ref:.2e})")
+        assert e_ref < max(BF16_TOL, 2.5 * e_cf_ref), (tall, e_ref, e_cf_ref)
+        assert e_cf <= 1.25 * e_cf_ref + 1e-3, (tall, e_cf, e_cf_ref)
+    print(f"{kind} {backend}: " + "; ".join(out))
 
 
 @pytest.mark.parametrize("backend", ["gram", "direct"])
