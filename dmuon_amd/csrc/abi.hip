@@ -245,6 +245,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     s.mt = s.nt = m_pad / tile;
     s.tiles_per_mat = tri ? tri_tiles(m_pad, tile) : s.mt * s.nt; s.tri = tri ? 1 : 0;
     s.sym_exact = 1; s.diag_skip = kDiagSkipPoly;
+    s.m_live = tri && km < m_pad ? km : 0;      // the rows and columns past m are never read
     s.mode = EPI_SYM; s.alpha = alpha; s.beta = C ? beta : 0.f; s.diag = diag;
     s.C = C; s.ldc = m_pad; s.sC = as;
     s.c_in = (C && C == A) ? C_IS_A : C_NONE;   // C's tile is the A panel's last slices
@@ -271,6 +272,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch; s.k_loop = kn;
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
     s.sym_exact = 1; s.diag_skip = kDiagSkipGram;
+    s.m_live = km < m_pad ? km : 0;
     s.mode = EPI_SYM; s.alpha = alpha;
     s.D = R; s.ldd = m_pad; s.sD = as;
     return timed(PC_SYRK, syrk_flops, 0.0, stream, who, [&] { return launch_nt(s, tile, stream); });
@@ -552,6 +554,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch; s.k_loop = kn;
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
     s.sym_exact = 1; s.diag_skip = kDiagSkipGram;
+    s.m_live = km < m_pad ? km : 0;
     s.mode = EPI_SYM; s.alpha = rs / (kNsKx * kNsKx); s.beta = 0.f; s.diag = 0.f;
     s.alpha_dev = it == 0 ? w.ratio_sq : nullptr;   // the staged X's scale correction
     s.D = w.Am; s.ldd = m_pad; s.sD = as;
@@ -565,6 +568,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     q.M = m_pad; q.N = m_pad; q.K = m_pad; q.L = batch; q.k_loop = km;
     q.mt = q.nt = m_pad / tile; q.tiles_per_mat = s.tiles_per_mat; q.tri = 1;
     q.sym_exact = 1; q.diag_skip = kDiagSkipPoly;
+    q.m_live = km < m_pad ? km : 0;
     q.mode = EPI_SYM; q.alpha = cc / (rs * rs); q.beta = cb / rs; q.diag = 0.f;
     q.C = w.Am; q.ldc = m_pad; q.sC = as;
     q.c_in = C_IS_A;

@@ -333,7 +333,7 @@ def test_launch_nt_refuses_mismatched_addend_alias(tmp_path):
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     print(run.stdout)
     assert run.returncode == 0, run.stdout + run.stderr
-    assert run.stdout.count("refused") >= 11 and "NOT REFUSED" not in run.stdout
+    assert run.stdout.count("refused") >= 14 and "NOT REFUSED" not in run.stdout
 
 
 def test_binding_refuses_a_library_of_another_abi_version():
