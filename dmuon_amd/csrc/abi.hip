@@ -245,7 +245,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     s.mt = s.nt = m_pad / tile;
     s.tiles_per_mat = tri ? tri_tiles(m_pad, tile) : s.mt * s.nt; s.tri = tri ? 1 : 0;
     s.sym_exact = 1; s.diag_skip = kDiagSkipPoly;
-    s.m_live = tri && km < m_pad ? km : 0;      // the rows and columns past m are never read
+    s.live_rows = s.live_cols = km < m_pad ? km : 0;   // rows and columns past m: never read
     s.mode = EPI_SYM; s.alpha = alpha; s.beta = C ? beta : 0.f; s.diag = diag;
     s.C = C; s.ldc = m_pad; s.sC = as;
     s.c_in = (C && C == A) ? C_IS_A : C_NONE;   // C's tile is the A panel's last slices
@@ -272,7 +272,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch; s.k_loop = kn;
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
     s.sym_exact = 1; s.diag_skip = kDiagSkipGram;
-    s.m_live = km < m_pad ? km : 0;
+    s.live_rows = s.live_cols = km < m_pad ? km : 0;
     s.mode = EPI_SYM; s.alpha = alpha;
     s.D = R; s.ldd = m_pad; s.sD = as;
     return timed(PC_SYRK, syrk_flops, 0.0, stream, who, [&] { return launch_nt(s, tile, stream); });
@@ -291,6 +291,8 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
       g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
     }
     g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch; g.k_loop = km;
+    g.live_rows = km < m_pad ? km : 0;
+    g.live_cols = kn < n_pad ? kn : 0;
     g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.beta = 0.f;
     if (!last) {
@@ -336,6 +338,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     NtArgs g{};
     g.elt = ELT_F16;
     g.M = m_pad; g.N = m_pad; g.K = m_pad; g.L = batch; g.k_loop = km;
+    g.live_rows = g.live_cols = km < m_pad ? km : 0;
     g.mt = g.nt = m_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.mode = EPI_NS; g.alpha = 1.f; g.beta = a_;
     g.lda = g.ldb = g.ldc = g.ldd = g.lddt = m_pad;
@@ -554,7 +557,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch; s.k_loop = kn;
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
     s.sym_exact = 1; s.diag_skip = kDiagSkipGram;
-    s.m_live = km < m_pad ? km : 0;
+    s.live_rows = s.live_cols = km < m_pad ? km : 0;
     s.mode = EPI_SYM; s.alpha = rs / (kNsKx * kNsKx); s.beta = 0.f; s.diag = 0.f;
     s.alpha_dev = it == 0 ? w.ratio_sq : nullptr;   // the staged X's scale correction
     s.D = w.Am; s.ldd = m_pad; s.sD = as;
@@ -568,7 +571,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     q.M = m_pad; q.N = m_pad; q.K = m_pad; q.L = batch; q.k_loop = km;
     q.mt = q.nt = m_pad / tile; q.tiles_per_mat = s.tiles_per_mat; q.tri = 1;
     q.sym_exact = 1; q.diag_skip = kDiagSkipPoly;
-    q.m_live = km < m_pad ? km : 0;
+    q.live_rows = q.live_cols = km < m_pad ? km : 0;
     q.mode = EPI_SYM; q.alpha = cc / (rs * rs); q.beta = cb / rs; q.diag = 0.f;
     q.C = w.Am; q.ldc = m_pad; q.sC = as;
     q.c_in = C_IS_A;
@@ -581,6 +584,8 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     g.A = w.Pm; g.lda = m_pad; g.sA = as;
     g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
     g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch; g.k_loop = km;
+    g.live_rows = km < m_pad ? km : 0;
+    g.live_cols = kn < n_pad ? kn : 0;
     g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.alpha = it + 1 < T ? 1.f : 1.f / kNsKx; g.beta = ca;
     g.alpha_dev = it == 0 ? w.ratio : nullptr;

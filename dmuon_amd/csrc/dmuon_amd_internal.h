@@ -60,10 +60,11 @@ struct NtArgs {
   // DIAG_SKIP_WAVES skips the two waves that hold no kept value; DIAG_SKIP_BLOCKS also skips the
   // 16x16 blocks strictly below the diagonal in the waves that straddle it. Same bits each way.
   int diag_skip;
-  // EPI_SYM + tri, 256-tiles: rows and columns from m_live on are padding that no later product
-  // reads (every K loop stops before it; 0: none). A wave whose 128 x 64 sub-tile lies wholly
-  // in it does no MFMA work and stores nothing; the padding then holds whatever it held.
-  int m_live;
+  // 256-tiles: output rows from live_rows on and columns from live_cols on are padding that no
+  // later product reads (every K loop stops before it; 0: none). A wave whose 128 x 64
+  // sub-tile lies wholly in it does no MFMA work and stores nothing; the padding then holds
+  // whatever it held.
+  int live_rows, live_cols;
 };
 enum { DIAG_SKIP_NONE = 0, DIAG_SKIP_WAVES = 1, DIAG_SKIP_BLOCKS = 2 };
 enum { C_NONE = 0, C_IS_A = 1, C_IS_B = 2 };

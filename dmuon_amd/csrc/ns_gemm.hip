@@ -1156,27 +1156,23 @@ void nt_pp_kernel(const NtArgs a) {
   // 42 and 58 in natural order). s_barrier counts waves, not program counters, and every copy
   // passes the same barriers.
   // NtArgs::diag_skip chooses how much of that is used: DIAG_SKIP_WAVES only copies 0 and 1.
-  // NtArgs::m_live: a wave whose rows or columns all lie in the unread padding takes copy 1 too.
-  int copy = 0;
+  // NtArgs::live_rows / live_cols: a wave whose rows or columns all lie in the unread padding
+  // takes copy 1 too, in every mode.
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int grp = wave >> 2, v = wave & 3;
+  int copy = (a.live_rows > 0 && bi * 256 + 128 * grp >= a.live_rows) ||
+                     (a.live_cols > 0 && bj * 256 + 64 * (grp == 0 ? 3 - v : v) >= a.live_cols)
+                 ? 1 : 0;
   if constexpr (MODE == EPI_SYM) {
-    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const int grp = wave >> 2, v = wave & 3;
-    if (a.m_live > 0 && (bi * 256 + 128 * grp >= a.m_live ||
-                         bj * 256 + 64 * (grp == 0 ? 3 - v : v) >= a.m_live)) {
-      copy = 1;
-    } else if (a.sym_exact && a.tri && bi == bj && a.diag_skip != DIAG_SKIP_NONE) {
+    if (copy == 0 && a.sym_exact && a.tri && bi == bj && a.diag_skip != DIAG_SKIP_NONE) {
       const int c = 4 * (grp == 0 ? 3 - v : v) - 8 * grp;
       copy = c <= -4 ? 1 : (c >= 7 || a.diag_skip != DIAG_SKIP_BLOCKS) ? 0 : c == 0 ? 2 : 3;
     }
   }
-  if constexpr (MODE == EPI_SYM) {
-    if (copy == 1) pp_tile<BK, S, MODE, E, BKM, -8>(a, smem, l, bi, bj);
-    else if (copy == 2) pp_tile<BK, S, MODE, E, BKM, 0>(a, smem, l, bi, bj);
-    else if (copy == 3) pp_tile<BK, S, MODE, E, BKM, 4>(a, smem, l, bi, bj);
-    else pp_tile<BK, S, MODE, E, BKM, 7>(a, smem, l, bi, bj);
-  } else {
-    pp_tile<BK, S, MODE, E, BKM, 7>(a, smem, l, bi, bj);
-  }
+  if (copy == 1) pp_tile<BK, S, MODE, E, BKM, -8>(a, smem, l, bi, bj);
+  else if (MODE == EPI_SYM && copy == 2) pp_tile<BK, S, MODE, E, BKM, 0>(a, smem, l, bi, bj);
+  else if (MODE == EPI_SYM && copy == 3) pp_tile<BK, S, MODE, E, BKM, 4>(a, smem, l, bi, bj);
+  else pp_tile<BK, S, MODE, E, BKM, 7>(a, smem, l, bi, bj);
 }
 
 // Compute units of the current device, queried once per device (0 if the query fails).
@@ -1220,7 +1216,8 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
     return hipErrorInvalidValue;
   if (a.c_in != C_NONE && a.c_in != C_IS_A && a.c_in != C_IS_B) return hipErrorInvalidValue;
   if (a.k_loop < 0 || a.k_loop > a.K || a.k_loop % 64 != 0) return hipErrorInvalidValue;
-  if (a.m_live < 0 || a.m_live % 64 != 0 || (a.m_live && !(a.mode == EPI_SYM && a.tri)))
+  if (a.live_rows < 0 || a.live_rows % 64 != 0 || a.live_cols < 0 || a.live_cols % 64 != 0 ||
+      (a.tri && a.live_rows != a.live_cols))
     return hipErrorInvalidValue;
   dim3 grid((unsigned)nb);
 #define DMUON_NT3(TILE, BK, S, WM, WN, E, KM)                                                  \

@@ -67,19 +67,18 @@ int main() {
   a = square(buf, 512, 512, 512);
   a.k_loop = -64;
   expect_refused("k_loop < 0", a);
-  // unread padding is declared only for a triangle of a symmetric product, at a slice boundary
+  // unread padding starts at a slice boundary, at the same place for both sides of a triangle
+  a = square(buf, 512, 512, 512);
+  a.live_rows = 448 + 32;
+  expect_refused("live_rows not a multiple of 64", a);
+  a = square(buf, 512, 512, 512);
+  a.live_cols = -64;
+  expect_refused("live_cols < 0", a);
   a = square(buf, 512, 512, 512);
   a.tri = 1;
-  a.m_live = 448 + 32;
-  expect_refused("m_live not a multiple of 64", a);
-  a = square(buf, 512, 512, 512);
-  a.m_live = 448;
-  expect_refused("m_live on a full (non-triangle) product", a);
-  a = square(buf, 512, 512, 512);
-  a.mode = dmuon::EPI_NS;
-  a.tri = 1;
-  a.m_live = 448;
-  expect_refused("m_live on an NS-step product", a);
+  a.live_rows = 448;
+  a.live_cols = 384;
+  expect_refused("triangle with live_rows != live_cols", a);
   if (bad) {
     printf("%d case(s) not refused\n", bad);
     return 1;
