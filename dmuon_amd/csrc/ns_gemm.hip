@@ -1169,10 +1169,15 @@ void nt_pp_kernel(const NtArgs a) {
       copy = c <= -4 ? 1 : (c >= 7 || a.diag_skip != DIAG_SKIP_BLOCKS) ? 0 : c == 0 ? 2 : 3;
     }
   }
-  if (copy == 1) pp_tile<BK, S, MODE, E, BKM, -8>(a, smem, l, bi, bj);
-  else if (MODE == EPI_SYM && copy == 2) pp_tile<BK, S, MODE, E, BKM, 0>(a, smem, l, bi, bj);
-  else if (MODE == EPI_SYM && copy == 3) pp_tile<BK, S, MODE, E, BKM, 4>(a, smem, l, bi, bj);
-  else pp_tile<BK, S, MODE, E, BKM, 7>(a, smem, l, bi, bj);
+  if (copy == 1) {
+    pp_tile<BK, S, MODE, E, BKM, -8>(a, smem, l, bi, bj);
+  } else if constexpr (MODE == EPI_SYM) {
+    if (copy == 2) pp_tile<BK, S, MODE, E, BKM, 0>(a, smem, l, bi, bj);
+    else if (copy == 3) pp_tile<BK, S, MODE, E, BKM, 4>(a, smem, l, bi, bj);
+    else pp_tile<BK, S, MODE, E, BKM, 7>(a, smem, l, bi, bj);
+  } else {
+    pp_tile<BK, S, MODE, E, BKM, 7>(a, smem, l, bi, bj);
+  }
 }
 
 // Compute units of the current device, queried once per device (0 if the query fails).
