@@ -60,6 +60,15 @@ constexpr int kDiagSkipGram = DIAG_SKIP_NONE;
 // reads) instead of a transposed copy, so the staging writes one fp16 copy of ns_in (12 B per
 // element instead of 14) and the restart Q X writes X alone, into the second X buffer.
 constexpr bool kGramKmajorQX = true;
+// Direct backend, the same for its P X products: X ping-pongs between two buffers (P X reads the
+// current X as its B operand, so the new X cannot overwrite it) and no transposed copy is kept.
+constexpr bool kDirectKmajorPX = true;
+
+// X is read k-major only while its whole m_pad x n_pad panel fits the 32-bit buffer range of the
+// kernel's operand loads (m_pad * n_pad * 2 < 2^31 bytes); larger shapes keep the transposed copy.
+bool x_kmajor(int gram, int64_t m_pad, int64_t n_pad) {
+  return (gram ? kGramKmajorQX : kDirectKmajorPX) && m_pad * n_pad * 2 < (1LL << 31);
+}
 
 // Power-of-two scale of the fp16 NS operand X, both backends (entries of the normalised X are at
 // most 1; the scale keeps the typical ~1/sqrt(mn) entries out of the fp16 subnormal range)
@@ -90,11 +99,12 @@ Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch, int
   const int64_t L = batch;
   const int64_t xs = (int64_t)m_pad * n_pad * 2;
   const int64_t as = (int64_t)m_pad * m_pad * 2;
-  // direct: X and its transposed copy in turn (XT0, XT1); Gram: X and the second X buffer a
-  // restart writes (XT0), plus the two Q slots and P R
+  // X and the second X buffer (XT0) that the products reading X k-major write the next X into;
+  // without k-major reads, X and its transposed copy in turn (XT0, XT1). Gram adds the two Q
+  // slots and P R.
   w.X = reinterpret_cast<uint16_t*>(take(L * xs));
   w.XT0 = reinterpret_cast<uint16_t*>(take(L * xs));
-  if (!gram) w.XT1 = reinterpret_cast<uint16_t*>(take(L * xs));
+  if (!x_kmajor(gram, m_pad, n_pad)) w.XT1 = reinterpret_cast<uint16_t*>(take(L * xs));
   w.Am = reinterpret_cast<uint16_t*>(take(L * as));
   w.Pm = reinterpret_cast<uint16_t*>(take(L * as));
   if (gram) {
@@ -228,6 +238,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
   // K loop lengths: the operands are zero past m (n), so the products multiply only m (n)
   // rounded up to the 64-wide slice, not the tile-padded m_pad (n_pad)
   const int km = (int)round_up(m, 64), kn = (int)round_up(n, 64);
+  const bool kmaj = x_kmajor(1, m_pad, n_pad);
   auto is_restart = [&](int it) {
     for (int r = 0; r < n_restarts; ++r)
       if (restarts[r] == it) return true;
@@ -258,7 +269,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
   // per-matrix correction (ratio for X, ratio_sq for X X^T; 1 after an exact staging). A
   // restart rewrites X exactly scaled.
   bool x_staged = true;
-  // with kGramKmajorQX: the current X and the buffer a restart writes the next one into (the
+  // with k-major Q X reads: the current X and the buffer a restart writes the next one into (the
   // transposed-copy region XT0 holds m_pad x n_pad values as well)
   uint16_t* x_cur = w.X;
   uint16_t* x_nxt = w.XT0;
@@ -285,7 +296,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     g.alpha_dev = x_staged ? w.ratio : nullptr;
     g.elt = ELT_F16;
     g.A = Q; g.lda = m_pad; g.sA = as;
-    if (kGramKmajorQX) {
+    if (kmaj) {
       g.B = x_cur; g.ldb = n_pad; g.sB = xs; g.b_kmajor = 1;
     } else {
       g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
@@ -298,7 +309,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     if (!last) {
       g.alpha = 1.f;
       g.mode = EPI_NS;
-      if (kGramKmajorQX) {
+      if (kmaj) {
         // X itself is the B operand, so the new X goes to the other buffer
         g.D = x_nxt; g.ldd = n_pad; g.sD = xs;
       } else {
@@ -307,7 +318,7 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
       }
       if (timed(PC_GEMM, gemm_flops, 0.0, stream, who, [&] { return launch_nt(g, tile, stream); }))
         return 1;
-      if (kGramKmajorQX) {
+      if (kmaj) {
         uint16_t* t = x_cur; x_cur = x_nxt; x_nxt = t;
       } else {
         uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
@@ -482,9 +493,9 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     q.nesterov = nesterov;
     q.kx = kNsKx;
     q.scale = w.scale + l0;
-    // the Gram backend's Q X products read X k-major (kGramKmajorQX): only X is staged, by the
+    // products that read X k-major (Gram's Q X, direct's P X) need only X: it is staged by the
     // direct write for a wide orientation, by the transposed one for a tall orientation
-    if (gram && kGramKmajorQX) {
+    if (x_kmajor(gram, m_pad, n_pad)) {
       q.skip_y = tall_ ? 1 : 0;
       q.skip_yt = tall_ ? 0 : 1;
     }
@@ -546,14 +557,18 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   int kr = 1;
   while (kr * 2 <= m && kr < 4096) kr *= 2;
   const int km = (int)round_up(m, 64), kn = (int)round_up(n, 64);   // K loops (zero past m, n)
+  // with k-major P X reads: the current X and the buffer the next one is written to
+  const bool kmaj = x_kmajor(0, m_pad, n_pad);
+  uint16_t* x_cur = w.X;
+  uint16_t* x_nxt = w.XT0;
   for (int it = 0; it < T; ++it) {
     const float ca = coeffs[3 * it], cb = coeffs[3 * it + 1], cc = coeffs[3 * it + 2];
     const float rs = it == 0 ? (float)kr : 1.f;   // the stored A is rs * (X X^T)
     // A = X X^T of the normalised X (the stored X is kNsKx * X)
     NtArgs s{};
     s.elt = ELT_F16;
-    s.A = w.X; s.lda = n_pad; s.sA = xs;
-    s.B = w.X; s.ldb = n_pad; s.sB = xs;
+    s.A = x_cur; s.lda = n_pad; s.sA = xs;
+    s.B = x_cur; s.ldb = n_pad; s.sB = xs;
     s.M = m_pad; s.N = m_pad; s.K = n_pad; s.L = batch; s.k_loop = kn;
     s.mt = s.nt = m_pad / tile; s.tiles_per_mat = tri_tiles(m_pad, tile); s.tri = 1;
     s.sym_exact = 1; s.diag_skip = kDiagSkipGram;
@@ -582,21 +597,34 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     NtArgs g{};
     g.elt = ELT_F16;
     g.A = w.Pm; g.lda = m_pad; g.sA = as;
-    g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
+    if (kmaj) {
+      g.B = x_cur; g.ldb = n_pad; g.sB = xs; g.b_kmajor = 1;
+    } else {
+      g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
+    }
     g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch; g.k_loop = km;
     g.live_rows = km < m_pad ? km : 0;
     g.live_cols = kn < n_pad ? kn : 0;
     g.mt = m_pad / tile; g.nt = n_pad / tile; g.tiles_per_mat = g.mt * g.nt; g.tri = 0;
     g.alpha = it + 1 < T ? 1.f : 1.f / kNsKx; g.beta = ca;
     g.alpha_dev = it == 0 ? w.ratio : nullptr;
-    g.C = w.X; g.ldc = n_pad; g.sC = xs;
+    g.C = x_cur; g.ldc = n_pad; g.sC = xs;
     if (it + 1 < T) {
       g.mode = EPI_NS;
-      g.D = w.X; g.ldd = n_pad; g.sD = xs;
-      g.DT = xt_nxt; g.lddt = m_pad; g.sDT = xs;
+      if (kmaj) {
+        // X itself is the B operand, so the new X goes to the other buffer
+        g.D = x_nxt; g.ldd = n_pad; g.sD = xs;
+      } else {
+        g.D = w.X; g.ldd = n_pad; g.sD = xs;
+        g.DT = xt_nxt; g.lddt = m_pad; g.sDT = xs;
+      }
       if (timed(PC_GEMM, gemm_flops, 0.0, stream, who, [&] { return launch_nt(g, tile, stream); }))
         return 1;
-      uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
+      if (kmaj) {
+        uint16_t* t = x_cur; x_cur = x_nxt; x_nxt = t;
+      } else {
+        uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
+      }
     } else {
       g.mode = EPI_FINAL;
       g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;

@@ -105,13 +105,28 @@ def test_plan(rows, cols, batch, tile, m_pad, n_pad):
     assert (t, mp, np_) == (tile, m_pad, n_pad)
     x = mp * np_ * 2
     a = mp * mp * 2
-    assert ws >= batch * (3 * x + 2 * a)
+    # direct: X and a second X buffer (its P X products read X itself), A, P; Gram: the two X
+    # buffers (for Q X), R, Z, two Q slots and P R
+    assert ws >= batch * (2 * x + 2 * a) and ws < batch * (2 * x + 3 * a)
     tg, mpg, npg, wsg = _C.plan(rows, cols, batch, backend=_C.NS_GRAM)
     assert (tg, mpg, npg) == (tile, m_pad, n_pad)
-    # direct: X, two transposed copies, A, P; Gram: X and a second X buffer (its Q X products
-    # read X itself), R, Z, two Q slots and P R
     assert wsg >= batch * (2 * x + 5 * a) and wsg < batch * (2 * x + 6 * a)
-    assert wsg == ws - batch * x + batch * 3 * a or abs(wsg - (ws - batch * x + batch * 3 * a)) < 4096
+    assert abs(wsg - (ws + batch * 3 * a)) < 4096
+
+
+def test_plan_keeps_transposed_copies_past_the_kmajor_range():
+    # X is read k-major only while m_pad * n_pad * 2 < 2^31 bytes; a larger X keeps two
+    # transposed copies beside it (three X-sized buffers) in both backends
+    for rows, cols in [(32768, 32768), (16384, 65536)]:
+        for backend in (_C.NS_DIRECT, _C.NS_GRAM):
+            t, mp, np_, ws = _C.plan(rows, cols, 1, backend=backend)
+            x, a = mp * np_ * 2, mp * mp * 2
+            assert x >= 1 << 31
+            n_a = 2 if backend == _C.NS_DIRECT else 5
+            assert 3 * x + n_a * a <= ws < 3 * x + n_a * a + (1 << 22)
+    t, mp, np_, ws = _C.plan(15872, 65536, 1)      # just inside: two X buffers
+    x, a = mp * np_ * 2, mp * mp * 2
+    assert x < 1 << 31 and 2 * x + 2 * a <= ws < 2 * x + 2 * a + (1 << 22)
 
 
 def test_plan_rejects_bad_arguments():
