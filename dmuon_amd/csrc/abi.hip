@@ -56,26 +56,20 @@ int64_t align256(int64_t b) { return round_up(b, 256); }
 constexpr int kDiagSkipPoly = DIAG_SKIP_BLOCKS;
 constexpr int kDiagSkipGram = DIAG_SKIP_NONE;
 
-// Gram backend: the two Q X products read X itself as their k-major B operand (transposing LDS
-// reads) instead of a transposed copy, so the staging writes one fp16 copy of ns_in (12 B per
-// element instead of 14) and the restart Q X writes X alone, into the second X buffer.
-constexpr bool kGramKmajorQX = true;
-// Direct backend, the same for its P X products: X ping-pongs between two buffers (P X reads the
-// current X as its B operand, so the new X cannot overwrite it) and no transposed copy is kept.
-constexpr bool kDirectKmajorPX = true;
-
-// X is read k-major only while its whole m_pad x n_pad panel fits the 32-bit buffer range of the
-// kernel's operand loads (m_pad * n_pad * 2 < 2^31 bytes); larger shapes keep the transposed copy.
-bool x_kmajor(int gram, int64_t m_pad, int64_t n_pad) {
-  return (gram ? kGramKmajorQX : kDirectKmajorPX) && m_pad * n_pad * 2 < (1LL << 31);
-}
+// The products X' = P X (direct) and Q X (Gram) read X itself as their k-major B operand
+// (transposing LDS reads) instead of a transposed copy: the staging writes one fp16 copy of
+// ns_in (12 B per element, not 14), and X ping-pongs between two buffers (such a product reads
+// the current X across the whole K range, so the new X cannot overwrite it). The k-major loads
+// address a matrix's whole X through one 32-bit buffer range, so m_pad * n_pad * 2 < 2^31
+// bytes: 2^30 fp16 values per padded matrix, which plan() enforces.
+constexpr int64_t kMaxXBytes = int64_t(1) << 31;
 
 // Power-of-two scale of the fp16 NS operand X, both backends (entries of the normalised X are at
 // most 1; the scale keeps the typical ~1/sqrt(mn) entries out of the fp16 subnormal range)
 constexpr float kNsKx = 4096.f;
 
 struct Workspace {
-  uint16_t *X, *XT0, *XT1, *Am, *Pm;
+  uint16_t *X, *X2, *Am, *Pm;
   // Gram backend only: the two slots of the accumulated polynomial Q (or its transpose), P R
   uint16_t *Q0, *Q1, *Wm;
   float *partials, *scale, *scale_sq;
@@ -99,12 +93,10 @@ Workspace carve(char* base, int m_pad, int n_pad, int Rp, int Cp, int batch, int
   const int64_t L = batch;
   const int64_t xs = (int64_t)m_pad * n_pad * 2;
   const int64_t as = (int64_t)m_pad * m_pad * 2;
-  // X and the second X buffer (XT0) that the products reading X k-major write the next X into;
-  // without k-major reads, X and its transposed copy in turn (XT0, XT1). Gram adds the two Q
-  // slots and P R.
+  // X and the second X buffer the NS products write the next X into, both backends; Gram adds
+  // the two Q slots and P R
   w.X = reinterpret_cast<uint16_t*>(take(L * xs));
-  w.XT0 = reinterpret_cast<uint16_t*>(take(L * xs));
-  if (!x_kmajor(gram, m_pad, n_pad)) w.XT1 = reinterpret_cast<uint16_t*>(take(L * xs));
+  w.X2 = reinterpret_cast<uint16_t*>(take(L * xs));
   w.Am = reinterpret_cast<uint16_t*>(take(L * as));
   w.Pm = reinterpret_cast<uint16_t*>(take(L * as));
   if (gram) {
@@ -201,6 +193,9 @@ int plan(int rows, int cols, int batch, int tile_req, int num_cus, int gram, int
   int t = tile_req;
   if (t == 0) t = auto_tile(m, n, batch, num_cus);
   const int mp = (int)round_up(m, t), np = (int)round_up(n, t);
+  if ((int64_t)mp * np * 2 >= kMaxXBytes)
+    return fail("dmuon_ns_plan: a %d x %d matrix pads to %d x %d, %lld fp16 values; the NS "
+                "kernels take at most 2^30 per matrix", rows, cols, mp, np, (long long)mp * np);
   const bool tall = rows > cols;
   const int Rp = tall ? np : mp, Cp = tall ? mp : np;
   Workspace w = carve(nullptr, mp, np, Rp, Cp, batch, gram);
@@ -238,7 +233,6 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
   // K loop lengths: the operands are zero past m (n), so the products multiply only m (n)
   // rounded up to the 64-wide slice, not the tile-padded m_pad (n_pad)
   const int km = (int)round_up(m, 64), kn = (int)round_up(n, 64);
-  const bool kmaj = x_kmajor(1, m_pad, n_pad);
   auto is_restart = [&](int it) {
     for (int r = 0; r < n_restarts; ++r)
       if (restarts[r] == it) return true;
@@ -269,10 +263,9 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
   // per-matrix correction (ratio for X, ratio_sq for X X^T; 1 after an exact staging). A
   // restart rewrites X exactly scaled.
   bool x_staged = true;
-  // with k-major Q X reads: the current X and the buffer a restart writes the next one into (the
-  // transposed-copy region XT0 holds m_pad x n_pad values as well)
+  // the current X and the buffer a restart writes the next one into
   uint16_t* x_cur = w.X;
-  uint16_t* x_nxt = w.XT0;
+  uint16_t* x_nxt = w.X2;
   // R = alpha X X^T
   auto gram_of_x = [&](uint16_t* R, float alpha) -> int {
     NtArgs s{};
@@ -288,19 +281,13 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     s.D = R; s.ldd = m_pad; s.sD = as;
     return timed(PC_SYRK, syrk_flops, 0.0, stream, who, [&] { return launch_nt(s, tile, stream); });
   };
-  uint16_t* xt_cur = w.XT0;
-  uint16_t* xt_nxt = w.XT1;
   // X <- Q X (an NS restart), or the final U = Q X / KX with the Muon update in the epilogue
   auto qx = [&](const uint16_t* Q, bool last) -> int {
     NtArgs g{};
     g.alpha_dev = x_staged ? w.ratio : nullptr;
     g.elt = ELT_F16;
     g.A = Q; g.lda = m_pad; g.sA = as;
-    if (kmaj) {
-      g.B = x_cur; g.ldb = n_pad; g.sB = xs; g.b_kmajor = 1;
-    } else {
-      g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
-    }
+    g.B = x_cur; g.ldb = n_pad; g.sB = xs; g.b_kmajor = 1;
     g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch; g.k_loop = km;
     g.live_rows = km < m_pad ? km : 0;
     g.live_cols = kn < n_pad ? kn : 0;
@@ -309,20 +296,10 @@ int run_gram(const Workspace& w, int m, int n, int m_pad, int n_pad, int tile, i
     if (!last) {
       g.alpha = 1.f;
       g.mode = EPI_NS;
-      if (kmaj) {
-        // X itself is the B operand, so the new X goes to the other buffer
-        g.D = x_nxt; g.ldd = n_pad; g.sD = xs;
-      } else {
-        g.D = w.X; g.ldd = n_pad; g.sD = xs;
-        g.DT = xt_nxt; g.lddt = m_pad; g.sDT = xs;
-      }
+      g.D = x_nxt; g.ldd = n_pad; g.sD = xs;   // X is the B operand: the new X goes elsewhere
       if (timed(PC_GEMM, gemm_flops, 0.0, stream, who, [&] { return launch_nt(g, tile, stream); }))
         return 1;
-      if (kmaj) {
-        uint16_t* t = x_cur; x_cur = x_nxt; x_nxt = t;
-      } else {
-        uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
-      }
+      uint16_t* t = x_cur; x_cur = x_nxt; x_nxt = t;
       x_staged = false;
       return 0;
     }
@@ -476,10 +453,10 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     q.g_dtype = g_dtype;
     q.buf_ptrs = buf_ptrs ? buf_ptrs + l0 : nullptr;
     q.est_ptrs = est_ptrs ? est_ptrs + l0 : nullptr;
-    q.Y = (tall_ ? w.XT0 : w.X) + l0 * xs;
+    q.Y = w.X + l0 * xs;
     q.ldy = tall_ ? m_pad : n_pad;
     q.sY = xs;
-    q.YT = (tall_ ? w.X : w.XT0) + l0 * xs;
+    q.YT = w.X + l0 * xs;
     q.ldyt = tall_ ? n_pad : m_pad;
     q.sYT = xs;
     q.partials = w.partials + (long long)l0 * w.nparts;
@@ -493,12 +470,10 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     q.nesterov = nesterov;
     q.kx = kNsKx;
     q.scale = w.scale + l0;
-    // products that read X k-major (Gram's Q X, direct's P X) need only X: it is staged by the
-    // direct write for a wide orientation, by the transposed one for a tall orientation
-    if (x_kmajor(gram, m_pad, n_pad)) {
-      q.skip_y = tall_ ? 1 : 0;
-      q.skip_yt = tall_ ? 0 : 1;
-    }
+    // the NS products read X k-major, so only X is staged: by the direct write for a wide
+    // orientation, by the transposed one for a tall orientation
+    q.skip_y = tall_ ? 1 : 0;
+    q.skip_yt = tall_ ? 0 : 1;
     return q;
   };
   const double Ld = batch, md = m, nd = n, elems = (double)rows * cols * batch;
@@ -545,8 +520,6 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   const double obytes = out_ptrs ? elems * (out_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0) : 0.0;
   const double pbytes = pub_ptrs ? elems * (pub_dtype == DMUON_DTYPE_F32 ? 4.0 : 2.0) : 0.0;
 
-  uint16_t* xt_cur = w.XT0;
-  uint16_t* xt_nxt = w.XT1;
   if (gram)
     return run_gram(w, m, n, m_pad, n_pad, tile, batch, tall, n_flip, coeffs, T, restarts,
                     n_restarts,
@@ -557,10 +530,9 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   int kr = 1;
   while (kr * 2 <= m && kr < 4096) kr *= 2;
   const int km = (int)round_up(m, 64), kn = (int)round_up(n, 64);   // K loops (zero past m, n)
-  // with k-major P X reads: the current X and the buffer the next one is written to
-  const bool kmaj = x_kmajor(0, m_pad, n_pad);
+  // the current X and the buffer the next one is written to
   uint16_t* x_cur = w.X;
-  uint16_t* x_nxt = w.XT0;
+  uint16_t* x_nxt = w.X2;
   for (int it = 0; it < T; ++it) {
     const float ca = coeffs[3 * it], cb = coeffs[3 * it + 1], cc = coeffs[3 * it + 2];
     const float rs = it == 0 ? (float)kr : 1.f;   // the stored A is rs * (X X^T)
@@ -597,11 +569,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     NtArgs g{};
     g.elt = ELT_F16;
     g.A = w.Pm; g.lda = m_pad; g.sA = as;
-    if (kmaj) {
-      g.B = x_cur; g.ldb = n_pad; g.sB = xs; g.b_kmajor = 1;
-    } else {
-      g.B = xt_cur; g.ldb = m_pad; g.sB = xs;
-    }
+    g.B = x_cur; g.ldb = n_pad; g.sB = xs; g.b_kmajor = 1;
     g.M = m_pad; g.N = n_pad; g.K = m_pad; g.L = batch; g.k_loop = km;
     g.live_rows = km < m_pad ? km : 0;
     g.live_cols = kn < n_pad ? kn : 0;
@@ -611,20 +579,10 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
     g.C = x_cur; g.ldc = n_pad; g.sC = xs;
     if (it + 1 < T) {
       g.mode = EPI_NS;
-      if (kmaj) {
-        // X itself is the B operand, so the new X goes to the other buffer
-        g.D = x_nxt; g.ldd = n_pad; g.sD = xs;
-      } else {
-        g.D = w.X; g.ldd = n_pad; g.sD = xs;
-        g.DT = xt_nxt; g.lddt = m_pad; g.sDT = xs;
-      }
+      g.D = x_nxt; g.ldd = n_pad; g.sD = xs;   // X is the B operand: the new X goes elsewhere
       if (timed(PC_GEMM, gemm_flops, 0.0, stream, who, [&] { return launch_nt(g, tile, stream); }))
         return 1;
-      if (kmaj) {
-        uint16_t* t = x_cur; x_cur = x_nxt; x_nxt = t;
-      } else {
-        uint16_t* t = xt_cur; xt_cur = xt_nxt; xt_nxt = t;
-      }
+      uint16_t* t = x_cur; x_cur = x_nxt; x_nxt = t;
     } else {
       g.mode = EPI_FINAL;
       g.out_ptrs = out_ptrs; g.out_dtype = out_dtype;

@@ -217,8 +217,11 @@ int dmuon_muon_update(void* const* w_ptrs, int w_dtype, const void* const* u_ptr
 /*
  * Planning for a group of `batch` same-shape rows x cols matrices: NS dims m = min, n = max,
  * chosen output tile (tile_req 0 = automatic, else 128 or 256), padded m_pad / n_pad and the
- * workspace bytes dmuon_muon_step_group / dmuon_newton_schulz_group need for `backend`
- * (DMUON_NS_GRAM needs five more m_pad x m_pad fp16 matrices per group member). Host-only.
+ * workspace bytes dmuon_muon_step_group / dmuon_newton_schulz_group need for `backend` (per
+ * group member two m_pad x n_pad fp16 matrices, X and the next X, and two m_pad x m_pad ones
+ * for DMUON_NS_DIRECT, five for DMUON_NS_GRAM). A padded matrix holds at most 2^30 values
+ * (m_pad * n_pad; the NS products read X k-major through 32-bit offsets): larger shapes are
+ * refused with an error. Host-only.
  */
 int dmuon_ns_plan(int rows, int cols, int batch, int tile_req, int num_cus, int backend,
                   int* tile, int* m_pad, int* n_pad, int64_t* workspace_bytes);

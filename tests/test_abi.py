@@ -114,17 +114,14 @@ def test_plan(rows, cols, batch, tile, m_pad, n_pad):
     assert abs(wsg - (ws + batch * 3 * a)) < 4096
 
 
-def test_plan_keeps_transposed_copies_past_the_kmajor_range():
-    # X is read k-major only while m_pad * n_pad * 2 < 2^31 bytes; a larger X keeps two
-    # transposed copies beside it (three X-sized buffers) in both backends
-    for rows, cols in [(32768, 32768), (16384, 65536)]:
+def test_plan_refuses_matrices_past_the_kmajor_range():
+    # the NS products read X k-major through 32-bit offsets: a padded matrix holds at most 2^30
+    # values, and a larger one is refused by the planner (before any workspace or launch)
+    for rows, cols in [(32768, 32768), (16384, 65536), (65536, 16384)]:
         for backend in (_C.NS_DIRECT, _C.NS_GRAM):
-            t, mp, np_, ws = _C.plan(rows, cols, 1, backend=backend)
-            x, a = mp * np_ * 2, mp * mp * 2
-            assert x >= 1 << 31
-            n_a = 2 if backend == _C.NS_DIRECT else 5
-            assert 3 * x + n_a * a <= ws < 3 * x + n_a * a + (1 << 22)
-    t, mp, np_, ws = _C.plan(15872, 65536, 1)      # just inside: two X buffers
+            with pytest.raises(RuntimeError, match="2\\^30"):
+                _C.plan(rows, cols, 1, backend=backend)
+    t, mp, np_, ws = _C.plan(15872, 65536, 1)      # just inside: 2^30 - 2^23 values
     x, a = mp * np_ * 2, mp * mp * 2
     assert x < 1 << 31 and 2 * x + 2 * a <= ws < 2 * x + 2 * a + (1 << 22)
 
