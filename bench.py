@@ -635,12 +635,11 @@ def main():
     pre = prof["pre"]
     pre_gbs = pre["bytes"] / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
     # what the staging actually moves per element: gradient (2 B) and momentum (4 + 4 B), and
-    # the fp16 NS operand -- one copy (2 B) for the Gram form, whose Q X products read X itself,
-    # X and its transpose (4 B) for the direct form -- in one pass with the kept scale (Muon's
-    # default); two passes re-read the gradient and the new momentum (6 B more)
+    # one fp16 copy of the NS operand (2 B; both NS forms read X itself, k-major) -- in one pass
+    # with the kept scale (Muon's default); two passes re-read the gradient and the new
+    # momentum (6 B more)
     single_pass = opt._single_pass
-    copies = 2.0 if ns.backend == "gram" else 4.0
-    actual_per_elem = 10.0 + copies + (0.0 if single_pass else 6.0)
+    actual_per_elem = 12.0 + (0.0 if single_pass else 6.0)
     pre_actual = n_elems * actual_per_elem * prof_steps
     pre_actual_gbs = pre_actual / (pre["ms"] * 1e-3) / 1e9 if pre["ms"] > 0 else None
     adam = prof["adamw"]
@@ -788,8 +787,7 @@ def main():
         "roofline_elementwise": {
             "kernel": ("muon_pre_kernel: momentum + Nesterov + norm partials + fp16 staging of "
                        "ns_in with the kept scale in one pass (a second pass only for matrices "
-                       "whose scale moved by more than 4x); one fp16 copy for the Gram form, "
-                       "the copy and its transpose for the direct form" if single_pass else
+                       "whose scale moved by more than 4x); one fp16 copy of ns_in" if single_pass else
                        "muon_pre_kernel: momentum + Nesterov + norm partials, then fp16 "
                        "staging of ns_in / ||ns_in|| (two passes)"),
             "bound": "hbm", "achieved": None if pre_gbs is None else round(pre_gbs, 1),
