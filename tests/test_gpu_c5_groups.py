@@ -3,7 +3,9 @@ matrix set): Muon.step over the q/o bucket (64 x 4096^2, one chunk) and over the
 (32 down 4096 x 14336 and 64 gate/up 14336 x 4096 of 32 layers: three 32-matrix chunks, the
 first with n_transposed = 0, the other two with every member stored transposed), two optimizer
 steps with the defaults bench.py times -- Gram NS (Polar-Express, restart at 2), single-pass
-staging, bf16 masters updated in place, lr 0.02, momentum 0.95 Nesterov, weight decay 0.1.
+staging, bf16 masters updated in place, lr 0.02, momentum 0.95 Nesterov, weight decay 0.1 --
+and the same buckets with the direct NS backend and Keller's coefficients (bench.py's
+c5_direct leg).
 
 Checked per chunk, against the reference's per-parameter loop (muon.py:1638-1747):
   * every momentum buffer after step 2 equals buf.mul_(mu).add_(grad) of step 1's buffer,
@@ -61,30 +63,42 @@ def _table(ts, dev):
     return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=dev)
 
 
-def _single_step(g, buf, est, w, rows, cols, n_t, tile, dev):
+# (library backend code, coefficients, restarts) per NS form
+_FORMS = {
+    "gram": (_C.NS_GRAM, dmuon.POLAR_EXPRESS_COEFFICIENTS, [2]),
+    "direct": (_C.NS_DIRECT, o.KELLER, []),
+}
+
+
+def _single_step(g, buf, est, w, rows, cols, n_t, tile, dev, form="gram"):
     """One step of one matrix through dmuon_muon_step_group (batch 1) on copies of its state;
     returns the new (momentum buffer, kept scale, weight)."""
+    backend, coeffs, restarts = _FORMS[form]
     buf, est, w = buf.clone(), est.clone(), w.clone()
     gp, bp, ep, wp = (_table([t], dev) for t in (g, buf, est, w))
-    coeff, T = _coeff_array(dmuon.POLAR_EXPRESS_COEFFICIENTS)
-    rst, n_rst = _C.restart_array([2])
-    _, _, _, nbytes = _C.plan(rows, cols, 1, tile, 0, _C.NS_GRAM)
+    coeff, T = _coeff_array(coeffs)
+    rst, n_rst = _C.restart_array(restarts)
+    _, _, _, nbytes = _C.plan(rows, cols, 1, tile, 0, backend)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     w_code = _C.DTYPE_F32 if w.dtype == torch.float32 else _C.DTYPE_BF16
     _C.call("dmuon_muon_step_group", gp.data_ptr(), _C.DTYPE_BF16, bp.data_ptr(), ep.data_ptr(),
             wp.data_ptr(), w_code, None, 0, rows, cols, 1, n_t, LR, MU, WD, 1, 0, coeff, T,
-            _C.NS_GRAM, rst, n_rst, EPS, ws.data_ptr(), ws.numel(), tile,
+            backend, rst, n_rst, EPS, ws.data_ptr(), ws.numel(), tile,
             torch.cuda.current_stream(dev).cuda_stream)
     return buf, est, w
 
 
-def _run_bucket(gpu, shapes, expect_chunks):
+def _run_bucket(gpu, shapes, expect_chunks, form="gram"):
+    backend, coeffs, _ = _FORMS[form]
     model = _Bucket(shapes, gpu)
     dmuon.dedicate_params(model, None, lambda n, p: p.dim() == 2,
                           param_policy={"defaults": {"master_dtype": torch.bfloat16}})
     dmuon.replicate(model)
-    opt = dmuon.Muon(model, lr=LR, momentum=MU, weight_decay=WD)
-    assert opt._ns.backend == "gram" and opt._single_pass
+    # Muon's default NS is the Gram form; the direct form is passed as bench.py passes it
+    kw = {} if form == "gram" else {
+        "ns_backend": dmuon.NewtonSchulz("direct", coefficients=o.KELLER)}
+    opt = dmuon.Muon(model, lr=LR, momentum=MU, weight_decay=WD, **kw)
+    assert opt._ns.backend == form and opt._single_pass
     ps = list(model.parameters())
     dps = dmuon.get_owned_params(model)
     muon_group = next(g for g in opt.param_groups if g.get("use_muon"))
@@ -95,13 +109,13 @@ def _run_bucket(gpu, shapes, expect_chunks):
     # and its chunks, as Muon._buckets / _chunk_sizes form them
     order = sorted(range(len(ps)), key=lambda i: ps[i].shape[0] > ps[i].shape[1])
     num_cus = torch.cuda.get_device_properties(gpu).multi_processor_count
-    sizes = opt._chunk_sizes(m, n, len(ps), num_cus, _C.NS_GRAM)
+    sizes = opt._chunk_sizes(m, n, len(ps), num_cus, backend)
     assert sizes == expect_chunks, sizes
     chunks, s0 = [], 0
     for size in sizes:
         members = order[s0:s0 + size]
         s0 += size
-        tile = _C.plan(m, n, size, 0, num_cus, _C.NS_GRAM)[0]
+        tile = _C.plan(m, n, size, 0, num_cus, backend)[0]
         chunks.append((members, tile))
 
     _set_grads(ps, 1, gpu)
@@ -134,7 +148,7 @@ def _run_bucket(gpu, shapes, expect_chunks):
             i = members[pos]
             w1, buf1, est1 = sampled[i]
             n_t = 1 if ps[i].shape[0] != m else 0
-            buf, est, w = _single_step(g2s[i], buf1, est1, w1, m, n, n_t, tile, gpu)
+            buf, est, w = _single_step(g2s[i], buf1, est1, w1, m, n, n_t, tile, gpu, form)
             st = opt.state[id(dps[i])]
             assert torch.equal(ps[i].detach(), w), (c, pos, "weight")
             assert torch.equal(st["momentum_buffer"], buf), (c, pos, "momentum")
@@ -146,11 +160,11 @@ def _run_bucket(gpu, shapes, expect_chunks):
             w1, buf1, est1 = sampled[i]
             n_t = 1 if ps[i].shape[0] != m else 0
             zero = torch.zeros(ps[i].shape, dtype=torch.float32, device=gpu)
-            buf, _, w = _single_step(g2s[i], buf1, est1, zero, m, n, n_t, tile, gpu)
+            buf, _, w = _single_step(g2s[i], buf1, est1, zero, m, n, n_t, tile, gpu, form)
             lrs = float(torch.tensor(LR * 0.2 * math.sqrt(n), dtype=torch.float32))
             u = w.double() / -lrs
             ns_in = g2s[i].double() + MU * buf.double()         # grad.add(buf, alpha=mu)
-            ref = _closed_form_gpu(ns_in, o.POLAR_EXPRESS, EPS)
+            ref = _closed_form_gpu(ns_in, coeffs, EPS)
             err = ((u - ref).norm() / ref.norm()).item()
             print(f"chunk {c} member {pos} {tuple(ps[i].shape)}: NS vs exact {err:.2e}",
                   flush=True)
@@ -158,15 +172,17 @@ def _run_bucket(gpu, shapes, expect_chunks):
     return [len(mb) for mb, _ in chunks]
 
 
-def test_c5_qo_bucket_one_chunk_of_64(gpu):
+@pytest.mark.parametrize("form", ["gram", "direct"])
+def test_c5_qo_bucket_one_chunk_of_64(gpu, form):
     """q and o of 32 layers: 64 x 4096^2 in one chunk (n_transposed 0)."""
-    _run_bucket(gpu, [(4096, 4096)] * (2 * LAYERS), [64])
+    _run_bucket(gpu, [(4096, 4096)] * (2 * LAYERS), [64], form)
 
 
-def test_c5_mlp_bucket_mixed_orientation_chunks(gpu):
+@pytest.mark.parametrize("form", ["gram", "direct"])
+def test_c5_mlp_bucket_mixed_orientation_chunks(gpu, form):
     """gate, up, down of 32 layers in model order: the bucket is the 32 downs (4096 x 14336)
     followed by the 64 gates / ups (14336 x 4096), split into chunks of 32, 32, 32."""
     shapes = []
     for _ in range(LAYERS):
         shapes += [(14336, 4096), (14336, 4096), (4096, 14336)]
-    _run_bucket(gpu, shapes, [32, 32, 32])
+    _run_bucket(gpu, shapes, [32, 32, 32], form)
