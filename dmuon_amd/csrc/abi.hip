@@ -482,7 +482,7 @@ int run_group(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, float* c
   // algorithmic bytes (what one ideal pass moves): gradient read, fp32 momentum read (not on
   // the first step) and write, one 2-byte copy of the normalised ns_in. The second pass's
   // re-read of the gradient and the new momentum (fp16 cannot hold an un-normalised gradient,
-  // so the copy waits for the norm) and its transposed copy are overhead, not counted.
+  // so the copy waits for the norm) is overhead, not counted.
   // With est_ptrs (a per-matrix scale kept from the previous step) the first pass also writes
   // the fp16 copy as fp16(kx * est * ns_in); the norm finalize then keeps that copy when
   // r = scale / est is within [1/4, 4] (the first products multiply by r or r^2, and every copy
