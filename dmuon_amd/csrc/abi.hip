@@ -14,10 +14,12 @@
 using namespace dmuon;
 
 // Scratch of dmuon_muon_step_group_noalloc: one static device array, of which the loader gives
-// every GPU the library runs on its own copy, held until the process ends. Host code never uses
-// the array's name as an address (on the host it is a stand-in symbol): the device address of
-// the current GPU's copy comes from hipGetSymbolAddress on the first call on that GPU and is
-// kept per device (scratch_of_current_device).
+// every GPU its own copy, held until the process ends. This file holds no kernels, so its code
+// object -- the array with it -- is loaded onto a GPU by the first hipGetSymbolAddress there,
+// not by the kernels of the other entry points. Host code never uses the array's name as an
+// address (on the host it is a stand-in symbol): the device address of the current GPU's copy
+// comes from hipGetSymbolAddress on the first call on that GPU and is kept per device
+// (scratch_of_current_device).
 static __device__ __align__(256) char scratch[DMUON_NOALLOC_SCRATCH_BYTES];
 
 namespace {

@@ -290,18 +290,20 @@ int dmuon_muon_apply_group(void* const* w_ptrs, int w_dtype, void* const* pub_pt
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
  * reference (its step allocates through torch). The arguments are dmuon_muon_step_group's minus
  * the workspace: the scratch is one static device array of DMUON_NOALLOC_SCRATCH_BYTES per GPU
- * (each GPU the library runs on holds it until the process ends), and a group whose planned
- * workspace (dmuon_ns_plan) exceeds it is rejected with an error before any launch. The call
+ * (512 MiB: any single Muon matrix of Llama-3-8B in either NS form; a GPU holds it from the first
+ * resolution of its address, below, until the process ends -- the library's other entry points
+ * do not load it), and a group whose planned workspace (dmuon_ns_plan) exceeds it is rejected
+ * with an error before any launch. The call
  * allocates nothing: no hipMalloc / hipFree, no library allocation, no profiler events. Every
  * call on one GPU shares that GPU's array and leaves its contents behind; a step needs none of
  * them (it writes every scratch byte it reads), but calls that overlap on one GPU (two streams,
  * two threads) race. `stream` must belong to the current device. Results equal
  * dmuon_muon_step_group's bit for bit. The scratch address of each GPU is resolved once, by
- * dmuon_noalloc_init or the first call on that GPU; that first resolution may load the library's
- * code object, so a caller that captures the step must make it happen before capturing (a first
- * call on a capturing stream is refused with an error).
+ * dmuon_noalloc_init or the first call on that GPU; that first resolution loads the code object
+ * that holds the array (reserving the array on that GPU), so a caller that captures the step must
+ * make it happen before capturing (a first call on a capturing stream is refused with an error).
  */
-#define DMUON_NOALLOC_SCRATCH_BYTES (256LL << 20)
+#define DMUON_NOALLOC_SCRATCH_BYTES (512LL << 20)
 int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs,
                                   float* const* est_ptrs, void* const* w_ptrs, int w_dtype,
                                   void* const* pub_ptrs, int pub_dtype, int rows, int cols,
@@ -314,7 +316,8 @@ int dmuon_muon_step_group_noalloc(void* const* g_ptrs, int g_dtype, float* const
  * reference; for the same callers, those that cannot allocate): resolves the device address of
  * this GPU's scratch array outside any capture and returns it (*scratch_out, may be NULL) with
  * its size in bytes (*scratch_bytes, may be NULL). Call it once per device before capturing the
- * allocation-free step. Allocates no device memory of its own. */
+ * allocation-free step. Allocates no device memory besides the array itself, which the loader
+ * reserves on this GPU with its code object at the first resolution. */
 int dmuon_noalloc_init(void** scratch_out, int64_t* scratch_bytes);
 
 /* direct_newton_schulz / gram_newton_schulz (by `backend`, as above) for `batch` matrices of one

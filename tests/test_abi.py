@@ -280,8 +280,10 @@ def test_noalloc_step_refuses_groups_beyond_its_scratch_without_gpu():
     coeff = (ctypes.c_float * 15)(*([3.4445, -4.7750, 2.0315] * 5))
     rst = (ctypes.c_int * 1)(2)
     p = ctypes.c_void_p(4096)
-    assert _C.plan(4096, 14336, 1, backend=_C.NS_GRAM)[3] > limit
-    msg = _err(lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 4096, 14336, 1, 0,
+    # one 4096 x 14336 matrix fits, two do not
+    assert _C.plan(4096, 14336, 1, backend=_C.NS_GRAM)[3] <= limit
+    assert _C.plan(4096, 14336, 2, backend=_C.NS_GRAM)[3] > limit
+    msg = _err(lib.dmuon_muon_step_group_noalloc(p, 1, p, None, p, 1, None, 0, 4096, 14336, 2, 0,
                                                  0.02, 0.95, 0.1, 1, 1, coeff, 5, 1, rst, 1,
                                                  1e-7, 0, None))
     assert "scratch" in msg and str(limit) in msg

@@ -5,8 +5,13 @@ row whose second is smaller than the first (the scratch keeps the first call's c
 every call both scratch areas are filled with 0xFF bytes (NaN in fp16 and fp32), so a read of a
 scratch byte the step did not write first shows up as a NaN or a mismatch. The step is also
 captured into a graph (after dmuon_noalloc_init) and replayed against eager workspace calls.
-The refusal of a group larger than the scratch is checked on the CPU (tests/test_abi.py)."""
+The refusal of a group larger than the scratch is checked on the CPU (tests/test_abi.py). A
+fresh process shows that the scratch is reserved on a GPU by dmuon_noalloc_init, not by loading
+the library and running its other kernels."""
 import ctypes
+import os
+import subprocess
+import sys
 
 import pytest
 import torch
@@ -116,9 +121,53 @@ def _run_both(grp, rows, cols, first, backend, coeffs, dev):
     return other
 
 
+_RESERVATION_PROBE = r'''
+import ctypes, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+from dmuon_amd import _C
+from dmuon_amd.optim import syrk_dispatch as sd
+dev = torch.device("cuda:0")
+x = torch.randn(1024, 1024, device=dev).to(torch.float16)
+d = torch.empty(1024, 1024, device=dev, dtype=torch.float16)
+def free():
+    torch.cuda.synchronize()
+    return torch.cuda.mem_get_info(dev)[0]
+f0 = free()
+sd.syrk_or_cublas(x, d, alpha=1.0, beta=0.0)   # loads the library and runs its SYRK kernel
+f1 = free()
+p, n = ctypes.c_void_p(), ctypes.c_int64()
+assert _C.lib().dmuon_noalloc_init(ctypes.byref(p), ctypes.byref(n)) == 0
+f2 = free()
+print(f0 - f1, f1 - f2, n.value)
+'''
+
+
+def test_scratch_is_reserved_by_noalloc_init_only(gpu):
+    """In a fresh process: device free memory is unchanged (within 64 MiB) by loading the library
+    and running a kernel, and drops by at least the scratch size at dmuon_noalloc_init -- the
+    array's code object holds no kernels and is loaded by the address resolution."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("fresh process: library load, one SYRK, dmuon_noalloc_init", flush=True)
+    out = subprocess.run([sys.executable, "-c", _RESERVATION_PROBE, root], capture_output=True,
+                         text=True, timeout=240, cwd=root)
+    assert out.returncode == 0, out.stderr[-2000:]
+    kernels, init, nbytes = (int(v) for v in out.stdout.split()[-3:])
+    print(f"free memory: -{kernels >> 20} MiB for load + kernel, -{init >> 20} MiB at init "
+          f"(scratch {nbytes >> 20} MiB)", flush=True)
+    assert nbytes == 512 << 20
+    assert kernels < 64 << 20
+    assert init >= nbytes
+
+
 def test_noalloc_matches_workspace_entry_point(gpu):
     pe = dmuon.POLAR_EXPRESS_COEFFICIENTS
     keller = dmuon.KELLER_COEFFICIENTS
+    # call 0: one Llama-3-8B MLP matrix (14336 x 4096, staged transposed), Gram NS: its
+    # 384 MiB workspace reaches past the first half of the scratch
+    mlp = _Group(14336, 4096, 1, torch.bfloat16, False, 4, gpu)
+    _run_both(mlp, 14336, 4096, 1, _C.NS_GRAM, pe, gpu)
+    del mlp
     big = _Group(512, 1536, 3, torch.bfloat16, False, 1, gpu)
     # call 1: a 3 x 512 x 1536 group, Gram NS, first step (exact staging)
     big = _run_both(big, 512, 1536, 1, _C.NS_GRAM, pe, gpu)
