@@ -782,9 +782,11 @@ void nt_mfma_kernel(const NtArgs a) {
   for (int q = 0; q < T::B_INST; ++q) {
     if constexpr (BKM) {
       // k-major: instruction q fills k-rows (NW q + w) KRPK.. of the slice; lane l writes slot
-      // l % KCPR of its row, i.e. fetches the chunk kswz places there
+      // l % KCPR of its row, i.e. fetches the chunk the swizzle places there (64-wide tiles:
+      // 128-byte k-rows, the ping-pong kernel's block layout)
       const int kr = (T::NW * q + wave) * KRPK + lane / KCPR, sl = lane % KCPR;
-      offb[q] = (unsigned)(kr * a.ldb + 8 * (sl ^ kswz(kr))) * 2u;
+      const int sw = BN == 64 ? kswz64(kr) : kswz(kr);
+      offb[q] = (unsigned)(kr * a.ldb + 8 * (sl ^ sw)) * 2u;
     } else {
       const int r = (T::NW * q + wave) * T::RPI + lrow;
       offb[q] = (unsigned)(r * a.ldb + T::slot(lsl, r) * 8) * 2u;
@@ -834,7 +836,10 @@ void nt_mfma_kernel(const NtArgs a) {
   const int kq = lane >> 4;
   int kboff[BJ];                                  // k-major B: this lane's read offsets
 #pragma unroll
-  for (int y = 0; y < BJ; ++y) kboff[y] = BKM ? kmajor_lane_off(lane, wj * T::WTN + 16 * y, KROWB) : 0;
+  for (int y = 0; y < BJ; ++y)
+    kboff[y] = !BKM ? 0
+               : BN == 64 ? kmajor64_lane_off(lane, wj * T::WTN + 16 * y)
+                          : kmajor_lane_off(lane, wj * T::WTN + 16 * y, KROWB);
 
   // lane l reads row (l % 16) of each 16-row block at the 16-byte chunk 4 ks + l / 16
   auto load_frags = [&](const char* sa, const char* sb, int ks, bf16x8_t* af, bf16x8_t* bfr) {
@@ -1283,12 +1288,12 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
       return launch_nt(s, 256, stream);
     }
   }
-  if (tile == 128 && !a.b_kmajor) {
+  if (tile == 128) {
     // The same products on 64x64 tiles (2 waves of 64x32, a seven-slot ring of 16 KiB slots,
     // one block per CU) when those still fit one wave of blocks on the device: four times the
     // CUs on a launch that waits on load latency. Every value keeps its K order -- the slice
     // rotation depends only on the 256-aligned block of the tile's columns -- so the bits match
-    // the 128-tile kernel's.
+    // the 128-tile kernel's. A k-major B is one 64-value block of 128-byte k-rows per slice.
     NtArgs s = a;
     s.mt = 2 * a.mt;
     s.nt = 2 * a.nt;
@@ -1296,21 +1301,27 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
     const long long nb64 = (long long)s.tiles_per_mat * a.L;
     if (nb64 <= cus) {
       dim3 g64((unsigned)nb64), b64(128);
-#define DMUON_NT64(E)                                                                          \
+#define DMUON_NT64K(E, KM)                                                                     \
   do {                                                                                         \
     if (s.mode == EPI_SYM)                                                                     \
-      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_SYM, E, false>), g64, b64, 0, \
+      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_SYM, E, KM>), g64, b64, 0,    \
                          stream, s);                                                           \
     else if (s.mode == EPI_NS)                                                                 \
-      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_NS, E, false>), g64, b64, 0,  \
+      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_NS, E, KM>), g64, b64, 0,     \
                          stream, s);                                                           \
     else                                                                                       \
-      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_FINAL, E, false>), g64, b64,  \
-                         0, stream, s);                                                        \
+      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_FINAL, E, KM>), g64, b64, 0,  \
+                         stream, s);                                                           \
+  } while (0)
+#define DMUON_NT64(E)                                                                          \
+  do {                                                                                         \
+    if (s.b_kmajor) DMUON_NT64K(E, true);                                                      \
+    else DMUON_NT64K(E, false);                                                                \
   } while (0)
       if (a.elt == ELT_F16) DMUON_NT64(ELT_F16);
       else DMUON_NT64(ELT_BF16);
 #undef DMUON_NT64
+#undef DMUON_NT64K
       return hipGetLastError();
     }
   }

@@ -210,7 +210,8 @@ def test_small_launch_variants_same_bits(gpu, dtype):
     """One 1024 x 1024 product replicated in batches sized so that launch_nt runs it on each
     of its kernels for a 128-tile plan -- 64-tiles, 128-tiles with a four-slot ring, 128-tiles
     two per CU, 256-tiles -- for the triangle product with its addend (Z = c R R^T + b R, C = R),
-    the full NS product (X' = s (P X + beta X) with X'^T) and the fused final weight update:
+    the full NS product (X' = s (P X + beta X) with X'^T) and the fused final weight update, the
+    NS products both from a transposed copy of X and from X itself (the k-major B operand):
     every variant must give the same bits for every matrix of every batch."""
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
     m = 1024
@@ -251,9 +252,21 @@ def test_small_launch_variants_same_bits(gpu, dtype):
         _C.call("dmuon_ns_gemm_final", code, Pb.data_ptr(), m, m * m, XTb.data_ptr(), m, m * m,
                 Xb.data_ptr(), m, m * m, m, m, L, 0.25, 1.5, None, m - 3, m - 5, 0, None, 0,
                 wp.data_ptr(), _C.DTYPE_F32, None, 0, 0.998, 0.01, 128, stream)
+        # the same products reading X itself (XT = NULL: k-major B)
+        Xk, XTk = torch.empty_like(Xb), torch.empty_like(Xb)
+        _C.call("dmuon_ns_gemm", code, Pb.data_ptr(), m, m * m, None, 0, 0,
+                Xb.data_ptr(), m, m * m, Xk.data_ptr(), m, m * m, XTk.data_ptr(), m, m * m, m,
+                m, L, 0.5, a, None, 128, stream)
+        Wk = [W0.clone() for _ in range(L)]
+        wpk = torch.tensor([w.data_ptr() for w in Wk], dtype=torch.int64, device=gpu)
+        _C.call("dmuon_ns_gemm_final", code, Pb.data_ptr(), m, m * m, None, 0, 0,
+                Xb.data_ptr(), m, m * m, m, m, L, 0.25, 1.5, None, m - 3, m - 5, 0, None, 0,
+                wpk.data_ptr(), _C.DTYPE_F32, None, 0, 0.998, 0.01, 128, stream)
         torch.cuda.synchronize()
         assert all(torch.equal(Xo[i], Xo[0]) and torch.equal(W[i], W[0]) for i in range(L)), v
         assert torch.equal(XTo[0], Xo[0].t()), v
+        assert all(torch.equal(Xk[i], Xo[0]) and torch.equal(Wk[i], W[0]) for i in range(L)), v
+        assert torch.equal(XTk[0], XTo[0]), v
         xs[v], ws[v] = Xo[0].clone(), W[0].clone()
     assert all(torch.equal(x, xs["64"]) for x in xs.values()), {v: L for v, L in full.items()}
     assert all(torch.equal(w, ws["64"]) for w in ws.values())
