@@ -1,12 +1,16 @@
 // Bandwidth-bound kernels of the Muon step on gfx950.
 //
 //  pre      buf <- mu*buf + g (first step: buf <- g); ns_in = g + mu*buf (Nesterov) or buf;
-//           writes bf16(ns_in) twice -- in the gradient's own layout and transposed (LDS-tiled
-//           64x64 transpose) -- into zero-padded NS operands, plus per-block partial sums of
-//           ns_in^2 for the Frobenius norm. One pass: 2 (g) + 4 + 4 (buf) + 2 + 2 (copies) B/elt.
-//           The fp16 NS stages in two passes instead: PRE_NORM (momentum + partials), then,
+//           writes a 16-bit copy of ns_in into a zero-padded NS operand -- in the gradient's
+//           own layout (Y) and/or transposed through a 64x64 LDS tile (YT); the callers' skip
+//           flags choose, and the Muon step writes only the m x n orientation the products read
+//           -- plus per-block partial sums of ns_in^2 for the Frobenius norm.
+//           PRE_EST (the Muon step's default) is one pass, 2 (g) + 4 + 4 (buf) + 2 (copy) B/elt:
+//           the copy is fp16(kx * est * ns_in) with the parameter's kept scale est, used when
+//           the new norm confirms it. Otherwise two passes: PRE_NORM (momentum + partials), then,
 //           once the norm is known, PRE_F16 recomputes ns_in and writes fp16(kx * ns_in / norm)
-//           (fp16 cannot hold an un-normalised gradient safely). 2+4+4, then 2+4+2+2 B/elt.
+//           (fp16 cannot hold an un-normalised gradient safely): 2+4+4, then 2+4+2 B/elt.
+//           PRE_BF16 writes bf16(ns_in) (the stand-alone staging entry point).
 //  finalize scale = 1/(||ns_in||_F + eps) per matrix, fixed-order (deterministic) reduction.
 //  update   W <- W*(1 - lr*wd) - lr*scale*U   for callers holding a materialised U.
 #include <algorithm>
