@@ -189,7 +189,7 @@ def _blas_threads():
 
 def cpu_config(shapes, ns: str, dtype: str, rounds: int, seed: int, scale: float = 1.0,
                sample: str = "") -> dict:
-    """One BASELINE config on the host: the oracle's Muon step (momentum
+    """One BASELINE config on the host (the per-config CPU baseline): the oracle's Muon step (momentum
     from a zero buffer, Nesterov, the NS of `ns` -- "direct" with Keller's coefficients or
     "gram" with Polar-Express and a restart at 2 --, weight decay 0.1 and the update) over
     `shapes`, with every tensor op rounded to `dtype` ("fp16": the reference's literal
@@ -554,8 +554,8 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures the single-GPU owner path only: "
-                          "run bench.py with --gpus 1 (multi-GPU sharding is described in "
-                          "DESIGN.md, not benchmarked)"}))
+                          "run bench.py with --gpus 1 (multi-GPU sharding is designed, not "
+                          "benchmarked)"}))
         sys.exit(2)
 
     import torch
@@ -606,7 +606,7 @@ def main():
     n_elems = sum(p.numel() for p in mats)
     rest_elems = sum(p.numel() for n, p in model.named_parameters() if not n.startswith("mats."))
     flops = sum(ns_useful_flops(*p.shape, 5, ns.backend, ns.restart_iterations) for p in mats)
-    # BASELINE.md's own count of useful NS FLOPs (the direct form: T*[m(m+1)n + m(m+1)m + 2m^2n],
+    # the baseline's own count of useful NS FLOPs (the direct form: T*[m(m+1)n + m(m+1)m + 2m^2n],
     # 471.81 TF for c5), whatever form the step computes
     flops_baseline = sum(ns_useful_flops(*p.shape, 5, "direct") for p in mats)
 
@@ -678,8 +678,8 @@ def main():
     del opt
     torch.cuda.empty_cache()
 
-    # ---- the same c5 step with 5 direct Keller NS steps (the north star's "X <- P X" form and
-    # BASELINE.md's FLOP model, 471.81 useful TFLOP, with its 50%-of-peak line) ---------------
+    # ---- the same c5 step with 5 direct Keller NS steps (the "X <- P X" form the baseline's FLOP
+    # model counts, 471.81 useful TFLOP, with its 50%-of-peak line) ---------------------------
     c5_direct = None
     if not args.no_configs and args.ns == "gram" and args.layers == N_LAYERS:
         opt_d = dmuon.Muon(model, lr=0.02, momentum=0.95, weight_decay=0.1, adamw_lr=1e-3,
@@ -712,7 +712,7 @@ def main():
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_budget, args.ns)
     if configs is not None and not args.no_cpu_baseline:
-        # c1 the reference's literal fp16 pipeline, median of 10; c2-c4
+        # per-config CPU baselines: c1 the reference's literal fp16 pipeline, median of 10; c2-c4
         # its fp32-compute variant (fp16 GEMMs are impractically slow on the host), median of 3,
         # the NS form of the GPU legs; c4 on a sample of its experts
         configs["c1"] = with_cpu(configs["c1"], cpu_config([(1024, 1024)], "direct", "fp16", 10,
@@ -773,7 +773,7 @@ def main():
         "ns_frac_mfma_peak_step": round(flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "ns_baseline_flop_model": {
             "useful_tflop_per_step": round(flops_baseline / 1e12, 2),
-            "definition": "BASELINE.md section 2: T*[m(m+1)n + m(m+1)m + 2m^2n] per matrix",
+            "definition": "useful NS FLOPs of the direct form: T*[m(m+1)n + m(m+1)m + 2m^2n] per matrix",
             "tflops": round(flops_baseline / (ms_per_step * 1e-3) / 1e12, 1),
             "frac": round(flops_baseline / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
             "ms_at_50pct_peak": round(flops_baseline / (0.5 * MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3, 1)},

@@ -56,8 +56,9 @@ def _ctypes_class(t):
 
 
 def test_binding_argument_types_match_the_header():
-    """_C.py's argtypes and the INTEGRATION.md ctypes stubs take each declared parameter with
-    its width: a wrong count or a 32/64-bit mix-up would pass garbage through ctypes."""
+    """_C.py's argtypes and the ctypes stubs of the integration guide take each declared
+    parameter with its width: a wrong count or a 32/64-bit mix-up would pass garbage through
+    ctypes."""
     hdr = _header_params()
     assert set(hdr) == set(_C.EXPORTED_SYMBOLS)
     for name, (_, argtypes) in _C._SIGNATURES.items():
