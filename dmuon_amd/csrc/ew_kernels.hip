@@ -2,9 +2,12 @@
 //
 //  pre      buf <- mu*buf + g (first step: buf <- g); ns_in = g + mu*buf (Nesterov) or buf;
 //           writes a 16-bit copy of ns_in into a zero-padded NS operand -- in the gradient's
-//           own layout (Y) and/or transposed through a 64x64 LDS tile (YT); the callers' skip
-//           flags choose, and the Muon step writes only the m x n orientation the products read
-//           -- plus per-block partial sums of ns_in^2 for the Frobenius norm.
+//           own layout (Y) and/or transposed through LDS (YT); the callers' skip flags choose,
+//           and the Muon step writes only the m x n orientation the products read -- plus
+//           partial sums of ns_in^2 for the Frobenius norm. Unpadded matrices with one copy run
+//           on kernels whose wave instructions each move one contiguous run (a wide matrix as a
+//           flat array, a tall one in 64 x 256 tiles); padded ones, or both copies, on 64x64
+//           tiles.
 //           PRE_EST (the Muon step's default) is one pass, 2 (g) + 4 + 4 (buf) + 2 (copy) B/elt:
 //           the copy is fp16(kx * est * ns_in) with the parameter's kept scale est, used when
 //           the new norm confirms it. Otherwise two passes: PRE_NORM (momentum + partials), then,
@@ -53,8 +56,9 @@ typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4_copy_t __attribute__((ext_vector_type(4)));
 // The gradient and the momentum buffer are streamed once per pass: non-temporal loads (and the
 // buffer's non-temporal store) keep them from displacing cache lines the NS kernels reuse
-// (measured 26.6 -> 24.8 ms per c5 step over both passes). The NS operands X, X^T stay normal
-// stores: the products read them next (non-temporal there measured 7% slower).
+// (measured 26.6 -> 24.8 ms per c5 step over both passes). The 64x64-tile kernel stores the NS
+// operands X, X^T normally; the contiguous-run kernels store X non-temporal (+3% on their own,
+// the products reading X only after the whole batch is staged).
 // The pointers come from device pointer tables, so the compiler cannot tell they are global
 // memory and would emit flat accesses (which also count against lgkmcnt); cast to the global
 // address space.
@@ -214,20 +218,186 @@ __device__ __forceinline__ float pre_tile(const PreArgs& a, int l, int r0, int c
   return ss;
 }
 
+// Partial sums of ns_in^2: one per 1024 elements' unit of work of whichever staging kernel ran
+// (a wave of a 64x64 tile, a 1024-element block of a wide matrix, four rows of a tall one's 64 x
+// 256 tile), (Rp / 32) * (Cp / 32) per matrix, summed in a fixed order by the norm finalize.
 template <int ST>
 __global__ __launch_bounds__(256) void muon_pre_kernel(const PreArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t tileT[kTile][kTile + kPad];
-  __shared__ float red[4];
   const int tid = threadIdx.x;
   float ss = pre_tile<ST>(a, blockIdx.z, blockIdx.y * kTile, blockIdx.x * kTile, tileT);
   if constexpr (ST == PRE_F16) return;
   ss = wave_sum(ss);
-  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  if ((tid & 63) == 0) {
+    const long long blk = (long long)blockIdx.z * gridDim.x * gridDim.y +
+                          blockIdx.y * gridDim.x + blockIdx.x;
+    a.partials[blk * 4 + (tid >> 6)] = ss;
+  }
+}
+
+// The per-element arithmetic of every staging kernel (the reference's order of roundings):
+// buf.mul_(mu).add_(g) (two roundings; the first step takes g), then grad.add(buf, alpha=mu)
+// (one fused rounding) for Nesterov. PRE_F16 recomputes ns_in from the momentum already written.
+template <int ST>
+__device__ __forceinline__ void pre_elem(const PreArgs& a, bool has_buf, float g, float b,
+                                         float& nb, float& ns) {
+  if (has_buf) {
+    if constexpr (ST == PRE_F16) nb = b;
+    else nb = a.first_step ? g : __fadd_rn(__fmul_rn(b, a.mu), g);
+    ns = a.nesterov ? __builtin_fmaf(a.mu, nb, g) : nb;
+  } else {
+    nb = g;
+    ns = g;
+  }
+}
+
+template <int ST>
+__device__ __forceinline__ uint16_t pre_out(float ns, float sc) {
+  return ST == PRE_BF16 ? f2bf(ns) : f2h(__fmul_rn(ns, sc));
+}
+
+// Four consecutive gradient values (and momentum values) at flat index i, one vector load each.
+__device__ __forceinline__ void pre_load4(const PreArgs& a, const void* g, const float* buf,
+                                          bool read_buf, long long i, float (&gv)[4],
+                                          float (&bv)[4]) {
+  if (a.g_dtype == DT_F32) {
+    const f32x4_t t = ldg_nt(reinterpret_cast<const f32x4_t*>(static_cast<const float*>(g) + i));
+    gv[0] = t.x; gv[1] = t.y; gv[2] = t.z; gv[3] = t.w;
+  } else {
+    const u32x2_t t =
+        ldg_nt(reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(g) + i));
+    gv[0] = bf2f(t.x & 0xffff); gv[1] = bf2f(t.x >> 16);
+    gv[2] = bf2f(t.y & 0xffff); gv[3] = bf2f(t.y >> 16);
+  }
+  if (read_buf) {
+    const f32x4_t b = ldg_nt(reinterpret_cast<const f32x4_t*>(buf + i));
+    bv[0] = b.x; bv[1] = b.y; bv[2] = b.z; bv[3] = b.w;
+  } else {
+    bv[0] = bv[1] = bv[2] = bv[3] = 0.f;
+  }
+}
+
+// Copy scale of this launch for matrix l (1 for PRE_BF16 / PRE_NORM), and whether it writes one
+// (PRE_EST without a usable estimate writes momentum and partials only).
+template <int ST>
+__device__ __forceinline__ float pre_scale(const PreArgs& a, int l, bool& copy) {
+  float sc = 1.f;
+  if constexpr (ST == PRE_F16) sc = a.scale[l] * a.kx;
+  if constexpr (ST == PRE_EST) sc = *a.est_ptrs[l] * a.kx;
+  copy = ST != PRE_NORM && (ST != PRE_EST || sc > 0.f);
+  return sc;
+}
+
+// The contiguous-run kernels store the NS copy non-temporal (see above).
+constexpr bool kCopyNT = true;
+template <class V>
+__device__ __forceinline__ void st_copy(V* p, V v) {
+  if constexpr (kCopyNT) stg_nt(p, v);
+  else *(__attribute__((address_space(1))) V*)p = v;
+}
+
+// Wide orientation without padding (Rp == rows, Cp == cols, Y in the gradient's own layout, no
+// transposed copy): the matrix is one flat array, four consecutive elements per thread and 1024
+// per block over a grid of the whole matrix, so every wave instruction moves one contiguous run
+// (1 KiB of momentum, 512 B of gradient and copy). Measured on a 64 x 4096^2 batch: 79% of 8 TB/s
+// against 67% for the 64x64 tiles (whose wave instructions cover four 256-byte row pieces), and
+// 58-70% for 8 elements per thread or several pieces per block. The copy is stored non-temporal:
+// the products read it only after the whole batch is staged.
+template <int ST>
+__global__ __launch_bounds__(256) void muon_pre_wide_kernel(const PreArgs a) {
+  const int l = blockIdx.y;
+  const long long i = (long long)blockIdx.x * 1024 + 4 * threadIdx.x;
+  const void* g = a.g_ptrs[l];
+  float* buf = a.buf_ptrs ? a.buf_ptrs[l] : nullptr;
+  const bool read_buf = buf && (ST == PRE_F16 || !a.first_step);
+  bool copy;
+  const float sc = pre_scale<ST>(a, l, copy);
+  float gv[4], bv[4], nb[4], ns[4];
+  pre_load4(a, g, buf, read_buf, i, gv, bv);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    pre_elem<ST>(a, buf != nullptr, gv[e], bv[e], nb[e], ns[e]);
+    ss += ns[e] * ns[e];
+  }
+  if (ST != PRE_F16 && buf)
+    stg_nt(reinterpret_cast<f32x4_t*>(buf + i), f32x4_t{nb[0], nb[1], nb[2], nb[3]});
+  if (copy) {
+    u32x2_t p;
+    p.x = (uint32_t)pre_out<ST>(ns[0], sc) | ((uint32_t)pre_out<ST>(ns[1], sc) << 16);
+    p.y = (uint32_t)pre_out<ST>(ns[2], sc) | ((uint32_t)pre_out<ST>(ns[3], sc) << 16);
+    st_copy(reinterpret_cast<u32x2_t*>(a.Y + (long long)l * a.sY + i), p);
+  }
+  if constexpr (ST == PRE_F16) return;
+  __shared__ float red[4];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
-  if (tid == 0) {
-    const int nparts = gridDim.x * gridDim.y;
-    a.partials[(long long)blockIdx.z * nparts + blockIdx.y * gridDim.x + blockIdx.x] =
-        (red[0] + red[1]) + (red[2] + red[3]);
+  if (threadIdx.x == 0)
+    a.partials[(long long)l * gridDim.x + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Tall orientation without padding (rows % 64 == 0, cols % 256 == 0; only the transposed copy
+// YT, the NS operand X = ns_in^T): 64 x 256 tiles of the gradient, wave w taking rows w, w + 4,
+// ... with four consecutive columns per lane (each wave instruction one contiguous row run, as
+// in the wide kernel), eight rows' loads in flight; the copy goes through LDS and leaves as X rows
+// of 64 values (128-byte runs). Measured on a 32 x 14336x4096 batch: 76% of 8 TB/s against 65%
+// for the 64x64 tiles (128 x 256 tiles: 74%, four rows in flight: 75%).
+template <int ST>
+__global__ __launch_bounds__(256) void muon_pre_tall_kernel(const PreArgs a) {
+  constexpr int TR = 64, TC = 256, RB = 8;
+  __shared__ __attribute__((aligned(16))) uint16_t tt[TC][TR + kPad];
+  const int l = blockIdx.z;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const long long r0 = (long long)blockIdx.y * TR, c0 = (long long)blockIdx.x * TC;
+  const int c = 4 * lane;
+  const void* g = a.g_ptrs[l];
+  float* buf = a.buf_ptrs ? a.buf_ptrs[l] : nullptr;
+  const bool read_buf = buf && (ST == PRE_F16 || !a.first_step);
+  bool copy;
+  const float sc = pre_scale<ST>(a, l, copy);
+  float ss[TR / 16] = {0.f, 0.f, 0.f, 0.f};   // one per four rows of this wave
+#pragma unroll
+  for (int rb = 0; rb < TR / 4; rb += RB) {
+    float gv[RB][4], bv[RB][4];
+#pragma unroll
+    for (int q = 0; q < RB; ++q)
+      pre_load4(a, g, buf, read_buf, (r0 + w + 4 * (rb + q)) * a.cols + c0 + c, gv[q], bv[q]);
+#pragma unroll
+    for (int q = 0; q < RB; ++q) {
+      const int rl = w + 4 * (rb + q);
+      float nb[4], ns[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pre_elem<ST>(a, buf != nullptr, gv[q][e], bv[q][e], nb[e], ns[e]);
+        ss[(rb + q) / 4] += ns[e] * ns[e];
+      }
+      if (ST != PRE_F16 && buf)
+        stg_nt(reinterpret_cast<f32x4_t*>(buf + (r0 + rl) * a.cols + c0 + c),
+               f32x4_t{nb[0], nb[1], nb[2], nb[3]});
+      if (copy) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tt[c + e][rl] = pre_out<ST>(ns[e], sc);
+      }
+    }
+  }
+  if (copy) {   // block-uniform
+    __syncthreads();
+    // X rows c0 + cr, 64 values (eight 16-byte pieces) each, 32 rows per pass
+    uint16_t* X = a.YT + (long long)l * a.sYT;
+#pragma unroll
+    for (int pass = 0; pass < TC / 32; ++pass) {
+      const int cr = pass * 32 + (threadIdx.x >> 3), pc = threadIdx.x & 7;
+      const u32x4_copy_t v = *reinterpret_cast<const u32x4_copy_t*>(&tt[cr][pc * 8]);
+      st_copy(reinterpret_cast<u32x4_copy_t*>(X + (c0 + cr) * a.ldyt + r0 + pc * 8), v);
+    }
+  }
+  if constexpr (ST == PRE_F16) return;
+  const long long blk = (long long)l * gridDim.x * gridDim.y + blockIdx.y * gridDim.x + blockIdx.x;
+#pragma unroll
+  for (int j = 0; j < TR / 16; ++j) {
+    const float s = wave_sum(ss[j]);
+    if (lane == 0) a.partials[blk * 16 + w * 4 + j] = s;
   }
 }
 
@@ -246,19 +416,40 @@ __global__ __launch_bounds__(256) void muon_restage_kernel(const PreArgs a) {
   }
 }
 
-__global__ __launch_bounds__(256) void norm_finalize_kernel(const float* partials, int nparts,
-                                                            float eps, float* scale,
-                                                            float* scale_sq) {
-  __shared__ double red[256];
-  const int l = blockIdx.x;
+// Sum of matrix l's partials in fp64, in a fixed order (the same bits on every call): thread t
+// adds groups of four consecutive partials t, t + 1024, ..., then a tree over the 1024 threads.
+// One block per matrix; 1024 threads with four loads per step keep ~57K partials of a
+// 4096 x 14336 matrix from being a long chain of dependent load latencies. Result in red[0].
+constexpr int kFinThreads = 1024;
+__device__ __forceinline__ void sum_partials(const float* partials, int nparts, int l,
+                                             double* red) {
+  const float* p = partials + (long long)l * nparts;
+  const int t = threadIdx.x;
   double s = 0.0;
-  for (int p = threadIdx.x; p < nparts; p += 256) s += (double)partials[(long long)l * nparts + p];
-  red[threadIdx.x] = s;
+  if ((nparts & 3) == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+    const f32x4_t* p4 = reinterpret_cast<const f32x4_t*>(p);
+    for (int q = t; q < nparts / 4; q += kFinThreads) {
+      const f32x4_t v = p4[q];
+      s += ((double)v.x + (double)v.y) + ((double)v.z + (double)v.w);
+    }
+  } else {
+    for (int q = t; q < nparts; q += kFinThreads) s += (double)p[q];
+  }
+  red[t] = s;
   __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+  for (int w = kFinThreads / 2; w > 0; w >>= 1) {
+    if (t < w) red[t] += red[t + w];
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(kFinThreads) void norm_finalize_kernel(const float* partials,
+                                                                    int nparts, float eps,
+                                                                    float* scale,
+                                                                    float* scale_sq) {
+  __shared__ double red[kFinThreads];
+  const int l = blockIdx.x;
+  sum_partials(partials, nparts, l, red);
   if (threadIdx.x == 0) {
     const float nrm = (float)sqrt(red[0]);
     const float sc = 1.0f / (nrm + eps);
@@ -288,19 +479,12 @@ __global__ __launch_bounds__(256) void muon_update_kernel(const UpdateArgs a) {
   }
 }
 
-__global__ __launch_bounds__(256) void norm_finalize_est_kernel(
+__global__ __launch_bounds__(kFinThreads) void norm_finalize_est_kernel(
     const float* partials, int nparts, float eps, float* scale, float* scale_sq,
     float* const* est_ptrs, float* ratio, float* ratio_sq, int* restage) {
-  __shared__ double red[256];
+  __shared__ double red[kFinThreads];
   const int l = blockIdx.x;
-  double s = 0.0;
-  for (int p = threadIdx.x; p < nparts; p += 256) s += (double)partials[(long long)l * nparts + p];
-  red[threadIdx.x] = s;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-    __syncthreads();
-  }
+  sum_partials(partials, nparts, l, red);
   if (threadIdx.x == 0) {
     const float nrm = (float)sqrt(red[0]);
     const float sc = 1.0f / (nrm + eps);
@@ -369,21 +553,38 @@ hipError_t launch_pad_copy(const uint16_t* src, long long lds, long long ss, uin
   return hipGetLastError();
 }
 
-int pre_blocks_per_mat(int Rp, int Cp) { return (Rp / kTile) * (Cp / kTile); }
+int pre_blocks_per_mat(int Rp, int Cp) { return (Rp / 32) * (Cp / 32); }
 
 hipError_t launch_pre(const PreArgs& a, hipStream_t stream) {
-  dim3 grid(a.Cp / kTile, a.Rp / kTile, a.L), block(256);
-  if (a.stage == PRE_NORM)
-    hipLaunchKernelGGL(muon_pre_kernel<PRE_NORM>, grid, block, 0, stream, a);
-  else if (a.stage == PRE_F16 && a.restage)
-    hipLaunchKernelGGL(muon_restage_kernel, dim3(std::min(pre_blocks_per_mat(a.Rp, a.Cp), 2048)),
-                       block, 0, stream, a);
-  else if (a.stage == PRE_F16)
-    hipLaunchKernelGGL(muon_pre_kernel<PRE_F16>, grid, block, 0, stream, a);
-  else if (a.stage == PRE_EST)
-    hipLaunchKernelGGL(muon_pre_kernel<PRE_EST>, grid, block, 0, stream, a);
-  else
-    hipLaunchKernelGGL(muon_pre_kernel<PRE_BF16>, grid, block, 0, stream, a);
+  dim3 block(256);
+  if (a.stage == PRE_F16 && a.restage) {
+    const int tiles = (a.Rp / kTile) * (a.Cp / kTile);
+    hipLaunchKernelGGL(muon_restage_kernel, dim3(std::min(tiles, 2048)), block, 0, stream, a);
+    return hipGetLastError();
+  }
+  // Which copy the launch writes: Y (the gradient's layout), YT (transposed), both or none
+  // (PRE_NORM writes none). Unpadded matrices with one copy take the contiguous-run kernels;
+  // everything else (padding, both copies) the 64x64 tiles. All three write the same partials
+  // layout size, (Rp / 32) * (Cp / 32) per matrix.
+  const bool y = a.stage != PRE_NORM && !a.skip_y, yt = a.stage != PRE_NORM && !a.skip_yt;
+  const bool unpadded = a.Rp == a.rows && a.Cp == a.cols;
+  const bool wide = unpadded && !yt && (!y || a.ldy == a.cols);
+  const bool tall = !wide && unpadded && !y && a.rows % 64 == 0 && a.cols % 256 == 0;
+#define DMUON_PRE(KERNEL, GRID)                                                                  \
+  do {                                                                                         \
+    if (a.stage == PRE_NORM) hipLaunchKernelGGL(KERNEL<PRE_NORM>, GRID, block, 0, stream, a);  \
+    else if (a.stage == PRE_F16) hipLaunchKernelGGL(KERNEL<PRE_F16>, GRID, block, 0, stream, a); \
+    else if (a.stage == PRE_EST) hipLaunchKernelGGL(KERNEL<PRE_EST>, GRID, block, 0, stream, a); \
+    else hipLaunchKernelGGL(KERNEL<PRE_BF16>, GRID, block, 0, stream, a);                      \
+  } while (0)
+  if (wide) {
+    DMUON_PRE(muon_pre_wide_kernel, dim3((unsigned)((long long)a.rows * a.cols / 1024), a.L));
+  } else if (tall) {
+    DMUON_PRE(muon_pre_tall_kernel, dim3(a.cols / 256, a.rows / 64, a.L));
+  } else {
+    DMUON_PRE(muon_pre_kernel, dim3(a.Cp / kTile, a.Rp / kTile, a.L));
+  }
+#undef DMUON_PRE
   return hipGetLastError();
 }
 
@@ -391,15 +592,15 @@ hipError_t launch_norm_finalize_est(const float* partials, int nparts, int L, fl
                                     float* scale, float* scale_sq, float* const* est_ptrs,
                                     float* ratio, float* ratio_sq, int* restage,
                                     hipStream_t stream) {
-  hipLaunchKernelGGL(norm_finalize_est_kernel, dim3(L), dim3(256), 0, stream, partials, nparts,
-                     eps, scale, scale_sq, est_ptrs, ratio, ratio_sq, restage);
+  hipLaunchKernelGGL(norm_finalize_est_kernel, dim3(L), dim3(kFinThreads), 0, stream, partials,
+                     nparts, eps, scale, scale_sq, est_ptrs, ratio, ratio_sq, restage);
   return hipGetLastError();
 }
 
 hipError_t launch_norm_finalize(const float* partials, int nparts, int L, float eps, float* scale,
                                 float* scale_sq, hipStream_t stream) {
-  hipLaunchKernelGGL(norm_finalize_kernel, dim3(L), dim3(256), 0, stream, partials, nparts, eps,
-                     scale, scale_sq);
+  hipLaunchKernelGGL(norm_finalize_kernel, dim3(L), dim3(kFinThreads), 0, stream, partials,
+                     nparts, eps, scale, scale_sq);
   return hipGetLastError();
 }
 

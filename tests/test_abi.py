@@ -201,7 +201,7 @@ def test_pre_and_final_validation_without_gpu():
     assert "needs w_ptrs" in _err(lib.dmuon_ns_gemm_final_bf16(
         p, 256, 0, p, 256, 0, p, 256, 0, 256, 256, 1, 1.0, 1.0, None, 256, 256, 0, p, 0, None,
         0, p, 1, 1.0, 0.0, 128, None))
-    assert lib.dmuon_muon_pre_partials(128, 256) == 8
+    assert lib.dmuon_muon_pre_partials(128, 256) == 32
     # NS-GEMM: X^T or X (read in place) must be given; X in place may not be overwritten
     assert "one of XT / X" in _err(lib.dmuon_ns_gemm_bf16(
         p, 256, 0, None, 256, 0, None, 256, 0, p, 256, 0, None, 256, 0, 256, 256, 1, 1.0, 1.0,
