@@ -785,11 +785,12 @@ def main():
                         "NS GEMM, final GEMM+update)")},
             **nt, traffic=traffic),
         "roofline_elementwise": {
-            "kernel": ("muon_pre_kernel: momentum + Nesterov + norm partials + fp16 staging of "
-                       "ns_in with the kept scale in one pass (a second pass only for matrices "
-                       "whose scale moved by more than 4x); one fp16 copy of ns_in" if single_pass else
-                       "muon_pre_kernel: momentum + Nesterov + norm partials, then fp16 "
-                       "staging of ns_in / ||ns_in|| (two passes)"),
+            "kernel": ("muon_pre_wide_kernel / muon_pre_tall_kernel: momentum + Nesterov + "
+                       "norm partials + fp16 staging of ns_in with the kept scale in one pass (a "
+                       "second pass only for matrices whose scale moved by more than 4x); one "
+                       "fp16 copy of ns_in, X^T of a tall matrix through LDS" if single_pass else
+                       "muon_pre_wide_kernel / muon_pre_tall_kernel: momentum + Nesterov + norm "
+                       "partials, then fp16 staging of ns_in / ||ns_in|| (two passes)"),
             "bound": "hbm", "achieved": None if pre_gbs is None else round(pre_gbs, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": None if pre_gbs is None else round(pre_gbs / HBM_PEAK_GBS, 4),

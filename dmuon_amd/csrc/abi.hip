@@ -1031,19 +1031,21 @@ int dmuon_muon_pre(void* const* g_ptrs, int g_dtype, float* const* buf_ptrs, voi
                    int nesterov, void* stream) {
   const char* who = "dmuon_muon_pre";
   if (batch == 0) return 0;
-  if (!g_ptrs || !Y || !YT || !partials) return fail("%s: NULL argument", who);
+  if (!g_ptrs || (!Y && !YT) || !partials) return fail("%s: NULL argument", who);
   if (g_dtype != DMUON_DTYPE_F32 && g_dtype != DMUON_DTYPE_BF16)
     return fail("%s: unsupported gradient dtype %d", who, g_dtype);
   if (rows <= 0 || cols <= 0 || batch < 0) return fail("%s: bad sizes", who);
   if (Rp % 64 || Cp % 64 || Rp < rows || Cp < cols)
     return fail("%s: padded extent %dx%d must be multiples of 64 covering %dx%d", who, Rp, Cp, rows, cols);
-  if (!aligned16(Y) || !aligned16(YT) || !ld_ok(ldy) || !ld_ok(ldyt) || ldy < Cp || ldyt < Rp ||
-      !stride_ok(strideY, batch) || !stride_ok(strideYT, batch))
+  if ((Y && (!aligned16(Y) || !ld_ok(ldy) || ldy < Cp || !stride_ok(strideY, batch))) ||
+      (YT && (!aligned16(YT) || !ld_ok(ldyt) || ldyt < Rp || !stride_ok(strideYT, batch))))
     return fail("%s: bad Y/YT layout", who);
   PreArgs p{};
   p.g_ptrs = g_ptrs; p.g_dtype = g_dtype; p.buf_ptrs = buf_ptrs;
   p.Y = static_cast<uint16_t*>(Y); p.ldy = ldy; p.sY = strideY;
   p.YT = static_cast<uint16_t*>(YT); p.ldyt = ldyt; p.sYT = strideYT;
+  p.skip_y = Y ? 0 : 1;
+  p.skip_yt = YT ? 0 : 1;
   p.partials = partials;
   p.rows = rows; p.cols = cols; p.Rp = Rp; p.Cp = Cp; p.L = batch;
   p.mu = mu; p.first_step = first_step; p.nesterov = nesterov;

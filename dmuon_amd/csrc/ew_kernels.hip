@@ -17,6 +17,7 @@
 //  finalize scale = 1/(||ns_in||_F + eps) per matrix, fixed-order (deterministic) reduction.
 //  update   W <- W*(1 - lr*wd) - lr*scale*U   for callers holding a materialised U.
 #include <algorithm>
+#include <type_traits>
 
 #include "dmuon_amd_internal.h"
 
@@ -256,25 +257,27 @@ __device__ __forceinline__ uint16_t pre_out(float ns, float sc) {
   return ST == PRE_BF16 ? f2bf(ns) : f2h(__fmul_rn(ns, sc));
 }
 
-// Four consecutive gradient values (and momentum values) at flat index i, one vector load each.
-__device__ __forceinline__ void pre_load4(const PreArgs& a, const void* g, const float* buf,
-                                          bool read_buf, long long i, float (&gv)[4],
-                                          float (&bv)[4]) {
-  if (a.g_dtype == DT_F32) {
-    const f32x4_t t = ldg_nt(reinterpret_cast<const f32x4_t*>(static_cast<const float*>(g) + i));
+// Raw words of four consecutive gradient values (GF: fp32, else bf16) at flat index i, one
+// vector load; unpacked by pre_unpack once every load of a batch has been issued.
+template <bool GF>
+using GradWords = typename std::conditional<GF, f32x4_t, u32x2_t>::type;
+template <bool GF>
+__device__ __forceinline__ GradWords<GF> pre_load_g(const void* g, long long i) {
+  if constexpr (GF)
+    return ldg_nt(reinterpret_cast<const f32x4_t*>(static_cast<const float*>(g) + i));
+  else
+    return ldg_nt(reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(g) + i));
+}
+template <bool GF>
+__device__ __forceinline__ void pre_unpack(const GradWords<GF>& t, const f32x4_t& b,
+                                           float (&gv)[4], float (&bv)[4]) {
+  if constexpr (GF) {
     gv[0] = t.x; gv[1] = t.y; gv[2] = t.z; gv[3] = t.w;
   } else {
-    const u32x2_t t =
-        ldg_nt(reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(g) + i));
     gv[0] = bf2f(t.x & 0xffff); gv[1] = bf2f(t.x >> 16);
     gv[2] = bf2f(t.y & 0xffff); gv[3] = bf2f(t.y >> 16);
   }
-  if (read_buf) {
-    const f32x4_t b = ldg_nt(reinterpret_cast<const f32x4_t*>(buf + i));
-    bv[0] = b.x; bv[1] = b.y; bv[2] = b.z; bv[3] = b.w;
-  } else {
-    bv[0] = bv[1] = bv[2] = bv[3] = 0.f;
-  }
+  bv[0] = b.x; bv[1] = b.y; bv[2] = b.z; bv[3] = b.w;
 }
 
 // Copy scale of this launch for matrix l (1 for PRE_BF16 / PRE_NORM), and whether it writes one
@@ -303,7 +306,7 @@ __device__ __forceinline__ void st_copy(V* p, V v) {
 // against 67% for the 64x64 tiles (whose wave instructions cover four 256-byte row pieces), and
 // 58-70% for 8 elements per thread or several pieces per block. The copy is stored non-temporal:
 // the products read it only after the whole batch is staged.
-template <int ST>
+template <int ST, bool GF>
 __global__ __launch_bounds__(256) void muon_pre_wide_kernel(const PreArgs a) {
   const int l = blockIdx.y;
   const long long i = (long long)blockIdx.x * 1024 + 4 * threadIdx.x;
@@ -312,8 +315,11 @@ __global__ __launch_bounds__(256) void muon_pre_wide_kernel(const PreArgs a) {
   const bool read_buf = buf && (ST == PRE_F16 || !a.first_step);
   bool copy;
   const float sc = pre_scale<ST>(a, l, copy);
+  const GradWords<GF> gw = pre_load_g<GF>(g, i);
+  const f32x4_t bw = read_buf ? ldg_nt(reinterpret_cast<const f32x4_t*>(buf + i))
+                              : f32x4_t{0.f, 0.f, 0.f, 0.f};
   float gv[4], bv[4], nb[4], ns[4];
-  pre_load4(a, g, buf, read_buf, i, gv, bv);
+  pre_unpack<GF>(gw, bw, gv, bv);
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -343,7 +349,7 @@ __global__ __launch_bounds__(256) void muon_pre_wide_kernel(const PreArgs a) {
 // in the wide kernel), eight rows' loads in flight; the copy goes through LDS and leaves as X rows
 // of 64 values (128-byte runs). Measured on a 32 x 14336x4096 batch: 76% of 8 TB/s against 65%
 // for the 64x64 tiles (128 x 256 tiles: 74%, four rows in flight: 75%).
-template <int ST>
+template <int ST, bool GF>
 __global__ __launch_bounds__(256) void muon_pre_tall_kernel(const PreArgs a) {
   constexpr int TR = 64, TC = 256, RB = 8;
   __shared__ __attribute__((aligned(16))) uint16_t tt[TC][TR + kPad];
@@ -359,17 +365,29 @@ __global__ __launch_bounds__(256) void muon_pre_tall_kernel(const PreArgs a) {
   float ss[TR / 16] = {0.f, 0.f, 0.f, 0.f};   // one per four rows of this wave
 #pragma unroll
   for (int rb = 0; rb < TR / 4; rb += RB) {
-    float gv[RB][4], bv[RB][4];
+    // every load of the batch issued before any is used
+    GradWords<GF> gw[RB];
+    f32x4_t bw[RB];
 #pragma unroll
     for (int q = 0; q < RB; ++q)
-      pre_load4(a, g, buf, read_buf, (r0 + w + 4 * (rb + q)) * a.cols + c0 + c, gv[q], bv[q]);
+      gw[q] = pre_load_g<GF>(g, (r0 + w + 4 * (rb + q)) * a.cols + c0 + c);
+    if (read_buf) {
+#pragma unroll
+      for (int q = 0; q < RB; ++q)
+        bw[q] = ldg_nt(reinterpret_cast<const f32x4_t*>(buf + (r0 + w + 4 * (rb + q)) * a.cols +
+                                                        c0 + c));
+    } else {
+#pragma unroll
+      for (int q = 0; q < RB; ++q) bw[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int q = 0; q < RB; ++q) {
       const int rl = w + 4 * (rb + q);
-      float nb[4], ns[4];
+      float gv[4], bv[4], nb[4], ns[4];
+      pre_unpack<GF>(gw[q], bw[q], gv, bv);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pre_elem<ST>(a, buf != nullptr, gv[q][e], bv[q][e], nb[e], ns[e]);
+        pre_elem<ST>(a, buf != nullptr, gv[e], bv[e], nb[e], ns[e]);
         ss[(rb + q) / 4] += ns[e] * ns[e];
       }
       if (ST != PRE_F16 && buf)
@@ -570,20 +588,25 @@ hipError_t launch_pre(const PreArgs& a, hipStream_t stream) {
   const bool unpadded = a.Rp == a.rows && a.Cp == a.cols;
   const bool wide = unpadded && !yt && (!y || a.ldy == a.cols);
   const bool tall = !wide && unpadded && !y && a.rows % 64 == 0 && a.cols % 256 == 0;
-#define DMUON_PRE(KERNEL, GRID)                                                                  \
+#define DMUON_PRE(KERNEL, GRID, ...)                                                           \
   do {                                                                                         \
-    if (a.stage == PRE_NORM) hipLaunchKernelGGL(KERNEL<PRE_NORM>, GRID, block, 0, stream, a);  \
-    else if (a.stage == PRE_F16) hipLaunchKernelGGL(KERNEL<PRE_F16>, GRID, block, 0, stream, a); \
-    else if (a.stage == PRE_EST) hipLaunchKernelGGL(KERNEL<PRE_EST>, GRID, block, 0, stream, a); \
-    else hipLaunchKernelGGL(KERNEL<PRE_BF16>, GRID, block, 0, stream, a);                      \
+    if (a.stage == PRE_NORM)                                                                   \
+      hipLaunchKernelGGL((KERNEL<PRE_NORM __VA_ARGS__>), GRID, block, 0, stream, a);           \
+    else if (a.stage == PRE_F16)                                                               \
+      hipLaunchKernelGGL((KERNEL<PRE_F16 __VA_ARGS__>), GRID, block, 0, stream, a);            \
+    else if (a.stage == PRE_EST)                                                               \
+      hipLaunchKernelGGL((KERNEL<PRE_EST __VA_ARGS__>), GRID, block, 0, stream, a);            \
+    else                                                                                       \
+      hipLaunchKernelGGL((KERNEL<PRE_BF16 __VA_ARGS__>), GRID, block, 0, stream, a);           \
   } while (0)
-  if (wide) {
-    DMUON_PRE(muon_pre_wide_kernel, dim3((unsigned)((long long)a.rows * a.cols / 1024), a.L));
-  } else if (tall) {
-    DMUON_PRE(muon_pre_tall_kernel, dim3(a.cols / 256, a.rows / 64, a.L));
-  } else {
-    DMUON_PRE(muon_pre_kernel, dim3(a.Cp / kTile, a.Rp / kTile, a.L));
-  }
+  const bool gf = a.g_dtype == DT_F32;
+  const dim3 gwide((unsigned)((long long)a.rows * a.cols / 1024), a.L);
+  const dim3 gtall(a.cols / 256, a.rows / 64, a.L);
+  if (wide && gf) DMUON_PRE(muon_pre_wide_kernel, gwide, , true);
+  else if (wide) DMUON_PRE(muon_pre_wide_kernel, gwide, , false);
+  else if (tall && gf) DMUON_PRE(muon_pre_tall_kernel, gtall, , true);
+  else if (tall) DMUON_PRE(muon_pre_tall_kernel, gtall, , false);
+  else DMUON_PRE(muon_pre_kernel, dim3(a.Cp / kTile, a.Rp / kTile, a.L));
 #undef DMUON_PRE
   return hipGetLastError();
 }

@@ -196,8 +196,9 @@ int dmuon_muon_pre_partials(int Rp, int Cp);
  * Momentum + Nesterov + NS-input staging for `batch` rows x cols matrices:
  *   buf <- g (first_step) | fp32(mu*buf) + g        (buf_ptrs may be NULL: ns_in = g)
  *   ns_in = g + mu*buf (nesterov) | buf
- *   Y[l]  <- bf16(ns_in)    [Rp][ldy]  zero outside rows x cols
- *   YT[l] <- bf16(ns_in)^T  [Cp][ldyt] zero outside cols x rows
+ *   Y[l]  <- bf16(ns_in)    [Rp][ldy]  zero outside rows x cols    (Y NULL: not written)
+ *   YT[l] <- bf16(ns_in)^T  [Cp][ldyt] zero outside cols x rows    (YT NULL: not written;
+ *                                                                   one of the two is needed)
  *   partials[l][p] <- partial sums of ns_in^2 (fp32), p < dmuon_muon_pre_partials(Rp, Cp)
  * g dtype: g_dtype; buf: fp32. Rp, Cp: multiples of 64, Rp >= rows, Cp >= cols.
  */

@@ -195,6 +195,11 @@ def test_pre_and_final_validation_without_gpu():
     p = ctypes.c_void_p(4096)
     assert "padded" in _err(lib.dmuon_muon_pre(p, 1, None, p, 128, 0, p, 128, 0, p, 100, 100, 96,
                                                128, 1, 0.95, 1, 1, None))
+    # one copy may be skipped (NULL), not both; a given copy's layout is still checked
+    assert "NULL argument" in _err(lib.dmuon_muon_pre(p, 1, None, None, 128, 0, None, 128, 0, p,
+                                                      100, 100, 128, 128, 1, 0.95, 1, 1, None))
+    assert "Y/YT layout" in _err(lib.dmuon_muon_pre(p, 1, None, None, 128, 0, p, 64, 0, p,
+                                                    100, 100, 128, 128, 1, 0.95, 1, 1, None))
     assert "nothing to write" in _err(lib.dmuon_ns_gemm_final_bf16(
         p, 256, 0, p, 256, 0, p, 256, 0, 256, 256, 1, 1.0, 1.0, None, 256, 256, 0, None, 0, None,
         0, None, 0, 1.0, 0.0, 128, None))

@@ -186,6 +186,58 @@ def test_pre_kernel_bit_exact(gpu, rows, cols, gdt, first):
         assert scale_sq[i].item() == pytest.approx(scale[i].item() ** 2, rel=1e-6)
 
 
+@pytest.mark.parametrize("rows,cols,which", [
+    (256, 512, "Y"),      # unpadded, copy in the gradient's layout: the flat wide kernel
+    (128, 192, "Y"),
+    (512, 256, "YT"),     # unpadded, transposed copy only, cols % 256 == 0: the 64 x 256 tiles
+    (640, 512, "YT"),
+    (512, 192, "YT"),     # transposed copy, cols not a multiple of 256: 64x64 tiles
+    (200, 300, "Y"),      # padded: 64x64 tiles
+])
+@pytest.mark.parametrize("gdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("first", [1, 0])
+def test_pre_kernel_single_copy_bit_exact(gpu, rows, cols, which, gdt, first):
+    """One copy (Y or YT NULL) selects the contiguous-run staging kernels where the shape allows:
+    momentum, the bf16 copy and the partial sums of ns_in^2 match the reference's ops bit for
+    bit (momentum, copy) and within fp32 summation error (partials); the other copy is left
+    untouched."""
+    L, mu = 3, 0.95
+    Rp, Cp = -(-rows // 64) * 64, -(-cols // 64) * 64
+    gs = [_rand((rows, cols), 50 + i, dtype=gdt, std=0.02).to(gpu) for i in range(L)]
+    bufs = [_rand((rows, cols), 60 + i, dtype=torch.float32, std=0.02).to(gpu) for i in range(L)]
+    buf0 = [b.clone() for b in bufs]
+    Y = torch.full((L, Rp, Cp), 7.0, dtype=torch.bfloat16, device=gpu)
+    YT = torch.full((L, Cp, Rp), 7.0, dtype=torch.bfloat16, device=gpu)
+    nparts = _C.lib().dmuon_muon_pre_partials(Rp, Cp)
+    assert nparts == Rp * Cp // 1024
+    parts = torch.full((L, nparts), float("nan"), dtype=torch.float32, device=gpu)
+    gp, bp = _ptrs(gs, gpu), _ptrs(bufs, gpu)
+    _C.call("dmuon_muon_pre", gp.data_ptr(), _C.DTYPE_F32 if gdt == torch.float32 else _C.DTYPE_BF16,
+            bp.data_ptr(), Y.data_ptr() if which == "Y" else None, Cp, Rp * Cp,
+            YT.data_ptr() if which == "YT" else None, Rp, Rp * Cp, parts.data_ptr(),
+            rows, cols, Rp, Cp, L, mu, first, 1, _stream())
+    untouched = torch.full((Cp, Rp) if which == "Y" else (Rp, Cp), 7.0, dtype=torch.bfloat16,
+                           device=gpu)
+    for i in range(L):
+        g = gs[i].float()
+        nb = g.clone() if first else (buf0[i] * mu + g)
+        ns = torch.from_numpy(o.fma_f32(np.float32(mu), nb.cpu().numpy(),
+                                        g.cpu().numpy())).to(gpu)
+        assert torch.equal(bufs[i], nb)
+        exp = torch.zeros(Rp, Cp, dtype=torch.bfloat16, device=gpu)
+        exp[:rows, :cols] = ns.to(torch.bfloat16)
+        if which == "Y":
+            assert torch.equal(Y[i], exp)
+            assert torch.equal(YT[i], untouched)
+        else:
+            assert torch.equal(YT[i], exp.t())
+            assert torch.equal(Y[i], untouched)
+        assert torch.isfinite(parts[i]).all()      # every partial written
+        ss = parts[i].double().sum().item()
+        ref = (ns.double() ** 2).sum().item()
+        assert abs(ss - ref) <= 1e-5 * ref
+
+
 @pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
 def test_update_kernel_bit_exact(gpu, wdt):
     L, shape = 2, (300, 500)
