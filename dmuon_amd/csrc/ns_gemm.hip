@@ -169,7 +169,7 @@ struct Tile {
   static constexpr int EPI_REGION = (EPI_REGION_RAW + 15) / 16 * 16;
   static constexpr int LDS_BYTES = (S * STAGE > NW * EPI_REGION ? S * STAGE : NW * EPI_REGION);
   static_assert(BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0, "tile rows vs DMA rows");
-  static_assert(S * LPT <= 63 && S <= 8, "vmcnt range (the prologue has S slices in flight)");
+  static_assert(S * LPT <= 63 && S <= 10, "vmcnt range (the prologue has S slices in flight)");
   // LDS slot of 16-byte chunk kc of row r. A ds_read_b128 serves 16 lanes (256 B, all 64
   // banks) per pass; a fragment read has those 16 lanes on 16 consecutive rows at one chunk,
   // so rows sharing a bank line (r % RPL) must take distinct slots along r / RPL.
@@ -248,13 +248,15 @@ __device__ __forceinline__ void sched_substeps() {
 }
 
 // Waves per SIMD: a 128x128 wave tile holds 256 accumulator registers, so its block runs one
-// wave per SIMD with the whole 512-entry register file; smaller wave tiles run two, unless the
-// block's LDS (more than half of the CU's 160 KiB) leaves room for one block per CU only.
+// wave per SIMD with the whole 512-entry register file; smaller wave tiles run two blocks per
+// CU, unless the block's LDS (more than half of the CU's 160 KiB) leaves room for one block per
+// CU only. A block of more than four waves puts NW / 4 of them on each SIMD.
 template <int BM, int BN, int BK, int S, int WM, int WN>
 struct Occupancy {
-  static constexpr int WPE =
+  static constexpr int BPC =
       (BM / WM) * (BN / WN) >= 128 * 128 || Tile<BM, BN, BK, S, WM, WN>::LDS_BYTES > 80 * 1024
           ? 1 : 2;
+  static constexpr int WPE = BPC * ((WM * WN + 3) / 4);
 };
 
 // First K slice of the tile's loop (see NtArgs::c_in): the slices that hold the tile's addend
@@ -1201,6 +1203,11 @@ int current_device_cus() {
 
 }  // namespace
 
+// 64x64 tiles of small launches: ring slots and waves (64 x 64 / kT64WN each)
+constexpr int kT64S = 8, kT64WN = 4;
+// 128x128 tiles of launches with at most one tile per CU: ring slots and waves (2 x kT128WN)
+constexpr int kT128S = 4, kT128WN = 4;
+
 hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   const long long nb = (long long)a.tiles_per_mat * a.L;
   if (nb <= 0) return hipSuccess;
@@ -1300,17 +1307,17 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
     s.tiles_per_mat = a.tri ? s.mt * (s.mt + 1) / 2 : s.mt * s.nt;
     const long long nb64 = (long long)s.tiles_per_mat * a.L;
     if (nb64 <= cus) {
-      dim3 g64((unsigned)nb64), b64(128);
+      dim3 g64((unsigned)nb64), b64(64 * kT64WN);
 #define DMUON_NT64K(E, KM)                                                                     \
   do {                                                                                         \
     if (s.mode == EPI_SYM)                                                                     \
-      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_SYM, E, KM>), g64, b64, 0,    \
+      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, kT64S, 1, kT64WN, EPI_SYM, E, KM>), g64, b64, 0,    \
                          stream, s);                                                           \
     else if (s.mode == EPI_NS)                                                                 \
-      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_NS, E, KM>), g64, b64, 0,     \
+      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, kT64S, 1, kT64WN, EPI_NS, E, KM>), g64, b64, 0,     \
                          stream, s);                                                           \
     else                                                                                       \
-      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, 7, 1, 2, EPI_FINAL, E, KM>), g64, b64, 0,  \
+      hipLaunchKernelGGL((nt_mfma_kernel<64, 64, 64, kT64S, 1, kT64WN, EPI_FINAL, E, KM>), g64, b64, 0,  \
                          stream, s);                                                           \
   } while (0)
 #define DMUON_NT64(E)                                                                          \
@@ -1328,11 +1335,11 @@ hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream) {
   const bool deep = tile != 256 && nb <= cus;
   if (a.elt == ELT_F16) {
     if (tile == 256) DMUON_PP(ELT_F16);
-    else if (deep) DMUON_NT(128, 64, 4, 2, 2, ELT_F16);
+    else if (deep) DMUON_NT(128, 64, kT128S, 2, kT128WN, ELT_F16);
     else DMUON_NT(128, 64, 2, 2, 2, ELT_F16);
   } else {
     if (tile == 256) DMUON_PP(ELT_BF16);
-    else if (deep) DMUON_NT(128, 64, 4, 2, 2, ELT_BF16);
+    else if (deep) DMUON_NT(128, 64, kT128S, 2, kT128WN, ELT_BF16);
     else DMUON_NT(128, 64, 2, 2, 2, ELT_BF16);
   }
 #undef DMUON_NT
