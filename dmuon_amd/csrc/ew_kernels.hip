@@ -48,9 +48,6 @@ __device__ __forceinline__ float wave_sum(float v) {
 __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
-__device__ __forceinline__ float h2f(uint16_t h) {
-  return static_cast<float>(__builtin_bit_cast(_Float16, h));
-}
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
@@ -291,14 +288,6 @@ __device__ __forceinline__ float pre_scale(const PreArgs& a, int l, bool& copy) 
   return sc;
 }
 
-// The contiguous-run kernels store the NS copy non-temporal (see above).
-constexpr bool kCopyNT = true;
-template <class V>
-__device__ __forceinline__ void st_copy(V* p, V v) {
-  if constexpr (kCopyNT) stg_nt(p, v);
-  else *(__attribute__((address_space(1))) V*)p = v;
-}
-
 // Wide orientation without padding (Rp == rows, Cp == cols, Y in the gradient's own layout, no
 // transposed copy): the matrix is one flat array, four consecutive elements per thread and 1024
 // per block over a grid of the whole matrix, so every wave instruction moves one contiguous run
@@ -332,7 +321,7 @@ __global__ __launch_bounds__(256) void muon_pre_wide_kernel(const PreArgs a) {
     u32x2_t p;
     p.x = (uint32_t)pre_out<ST>(ns[0], sc) | ((uint32_t)pre_out<ST>(ns[1], sc) << 16);
     p.y = (uint32_t)pre_out<ST>(ns[2], sc) | ((uint32_t)pre_out<ST>(ns[3], sc) << 16);
-    st_copy(reinterpret_cast<u32x2_t*>(a.Y + (long long)l * a.sY + i), p);
+    stg_nt(reinterpret_cast<u32x2_t*>(a.Y + (long long)l * a.sY + i), p);
   }
   if constexpr (ST == PRE_F16) return;
   __shared__ float red[4];
@@ -407,7 +396,7 @@ __global__ __launch_bounds__(256) void muon_pre_tall_kernel(const PreArgs a) {
     for (int pass = 0; pass < TC / 32; ++pass) {
       const int cr = pass * 32 + (threadIdx.x >> 3), pc = threadIdx.x & 7;
       const u32x4_copy_t v = *reinterpret_cast<const u32x4_copy_t*>(&tt[cr][pc * 8]);
-      st_copy(reinterpret_cast<u32x4_copy_t*>(X + (c0 + cr) * a.ldyt + r0 + pc * 8), v);
+      stg_nt(reinterpret_cast<u32x4_copy_t*>(X + (c0 + cr) * a.ldyt + r0 + pc * 8), v);
     }
   }
   if constexpr (ST == PRE_F16) return;
