@@ -27,7 +27,7 @@ NS_GRAM = 1
 # DMUON_ABI_VERSION of include/dmuon_amd.h: the argument lists below are those of this
 # version, and a library that reports another one is refused (its entry points would be
 # called with the wrong arguments).
-ABI_VERSION = 107
+ABI_VERSION = 108
 
 # name -> (restype, argtypes); mirrors include/dmuon_amd.h
 _SIGNATURES = {

@@ -72,7 +72,7 @@ extern "C" {
 const char* dmuon_last_error(void);
 
 /* ABI version (major*100 + minor): DMUON_ABI_VERSION of the header the library was built with. */
-#define DMUON_ABI_VERSION 107
+#define DMUON_ABI_VERSION 108
 int dmuon_abi_version(void);
 
 /*
