@@ -71,6 +71,9 @@ enum { C_NONE = 0, C_IS_A = 1, C_IS_B = 2 };
 
 // Launches the NT MFMA kernel; picks the tile configuration from args (tile = 256 or 128).
 hipError_t launch_nt(const NtArgs& a, int tile, hipStream_t stream);
+// The logical tile the NT kernels give hardware block b of a launch of nb blocks (host copy of
+// the device mapping, for tests: it must be a permutation of 0 .. nb - 1).
+int nt_block_tile(int b, int nb);
 
 // What one launch of the pre kernel does:
 //   PRE_BF16  momentum update, bf16 ns_in into Y / YT, norm partials (direct NS staging)

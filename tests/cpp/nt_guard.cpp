@@ -79,8 +79,27 @@ int main() {
   a.live_rows = 448;
   a.live_cols = 384;
   expect_refused("triangle with live_rows != live_cols", a);
-  if (bad) {
-    printf("%d case(s) not refused\n", bad);
+  // the block -> logical tile map of the NT kernels is a permutation of the launch's tiles
+  // (a tile computed twice, or one past the launch, would be a wrong result or an out-of-bounds
+  // access): launch sizes 1 .. 4096 and the c4 / c5 launch sizes
+  int map_bad = 0;
+  static int seen[1 << 16];
+  const int sizes[] = {2688, 4352, 4608, 6144, 8704, 16384, 28672, 57344};
+  for (int k = 0; k < 4096 + 8 && !map_bad; ++k) {
+    const int nb = k < 4096 ? k + 1 : sizes[k - 4096];
+    for (int t = 0; t < nb; ++t) seen[t] = 0;
+    for (int b = 0; b < nb; ++b) {
+      const int t = dmuon::nt_block_tile(b, nb);
+      if (t < 0 || t >= nb || seen[t]++) {
+        printf("block %d of %d maps to tile %d: not a permutation\n", b, nb, t);
+        map_bad = 1;
+        break;
+      }
+    }
+  }
+  printf("block -> tile map: %s\n", map_bad ? "NOT A PERMUTATION" : "permutation for every size");
+  if (bad || map_bad) {
+    if (bad) printf("%d case(s) not refused\n", bad);
     return 1;
   }
   printf("all refused\n");

@@ -335,7 +335,9 @@ def test_launch_nt_refuses_mismatched_addend_alias(tmp_path):
     """launch_nt itself (the one launcher every product goes through) refuses an addend named
     as an operand (C_IS_A / C_IS_B) unless it really is that operand of a square product with
     its layout. The harness tests/cpp/nt_guard.cpp calls the library's launch_nt on the host
-    with such arguments; every case must come back hipErrorInvalidValue without a device."""
+    with such arguments; every case must come back hipErrorInvalidValue without a device. The
+    same harness checks that the kernels' block -> logical tile map (XCD windows) is a
+    permutation of every launch's tiles."""
     import shutil
     import subprocess
     gxx = shutil.which("g++")
@@ -354,6 +356,7 @@ def test_launch_nt_refuses_mismatched_addend_alias(tmp_path):
     print(run.stdout)
     assert run.returncode == 0, run.stdout + run.stderr
     assert run.stdout.count("refused") >= 14 and "NOT REFUSED" not in run.stdout
+    assert "permutation for every size" in run.stdout
 
 
 def test_binding_refuses_a_library_of_another_abi_version():
