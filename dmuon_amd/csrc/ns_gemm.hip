@@ -288,6 +288,9 @@ struct TilePos {
   int l, bi, bj;
 };
 
+// tile rows per group of the walks (with the XCD windows, 4 or 16 rows for the triangle walk
+// and 4 or 16 for the rectangular one measured 0.3-0.9% slower per c5 step)
+constexpr int kTileGroupTri = 8, kTileGroupRect = 8;
 __device__ __forceinline__ TilePos decode_tile(const NtArgs& a, int hb, int nblocks) {
   const int lb = xcd_remap(hb, nblocks);
   const int l = lb / a.tiles_per_mat;
@@ -299,7 +302,7 @@ __device__ __forceinline__ TilePos decode_tile(const NtArgs& a, int hb, int nblo
     // that the tiles resident on one XCD at a time form compact blocks sharing panels in L2
     int g0 = 0, gs = 0;
     for (;;) {
-      gs = min(8, a.mt - g0);
+      gs = min(kTileGroupTri, a.mt - g0);
       const int cnt = gs * (gs + 1) / 2 + gs * (a.mt - g0 - gs);
       if (t < cnt) break;
       t -= cnt;
@@ -318,7 +321,7 @@ __device__ __forceinline__ TilePos decode_tile(const NtArgs& a, int hb, int nblo
     }
   } else {
     // groups of 8 tile-rows walked column-major so neighbouring blocks share B panels
-    const int group = 8;
+    const int group = kTileGroupRect;
     const int per_group = group * a.nt;
     const int g = t / per_group;
     const int first = g * group;
