@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: one full Muon optimizer step over the Llama-3-8B-shaped parameter set on one MI355X.
 
-Workload (BASELINE config c5): 32 layers x {q, o 4096x4096; k, v 1024x4096; gate, up
+Workload (benchmark config c5): 32 layers x {q, o 4096x4096; k, v 1024x4096; gate, up
 14336x4096; down 4096x14336} = 224 dedicated matrices, bf16 weights and gradients ~N(0, 0.02^2),
 fp32 momentum, all owned by the single rank, plus the AdamW-routed rest of Llama-3-8B
 (embeddings and lm_head 128256x4096, 65 RMSNorm weights of 4096, bf16); dmuon_amd.Muon(lr=0.02,
@@ -14,7 +14,7 @@ AdamW update of the rest. Synthetic data is generated on the GPU (values do not 
 Prints ONE JSON line. Besides the contract fields: the per-kernel-class breakdown from the
 library's hipEvent profiler (a second, separately timed pass), the roofline of the dominant
 kernel family (the MFMA NT kernels) and of the fused momentum kernel next to a plain device copy
-measured in the same run, the AdamW share of the step, the gradient clip, the other BASELINE
+measured in the same run, the AdamW share of the step, the gradient clip, the other benchmark
 configs (c2 single 4096^2 matrix x 100 steps, c3 aspect ratios one matrix each, c4 the MoE
 expert batch) each with ms / TFLOP/s / fraction of peak, and a CPU baseline: the numpy
 restatement of the reference math (fp16 cast points emulated) on the host cores, over a bounded
@@ -189,7 +189,7 @@ def _blas_threads():
 
 def cpu_config(shapes, ns: str, dtype: str, rounds: int, seed: int, scale: float = 1.0,
                sample: str = "") -> dict:
-    """One BASELINE config on the host (the per-config CPU baseline): the oracle's Muon step (momentum
+    """One benchmark config on the host (the per-config CPU baseline): the oracle's Muon step (momentum
     from a zero buffer, Nesterov, the NS of `ns` -- "direct" with Keller's coefficients or
     "gram" with Polar-Express and a restart at 2 --, weight decay 0.1 and the update) over
     `shapes`, with every tensor op rounded to `dtype` ("fp16": the reference's literal
@@ -375,7 +375,7 @@ def time_steps(torch, opt, warmup: int, steps: int) -> list:
 
 def config_leg(torch, dmuon, dev, shapes, ns, steps, warmup, seed, momentum_init=False,
                dtype=None):
-    """One BASELINE config on its own matrices (bf16 weights updated in place unless `dtype`
+    """One benchmark config on its own matrices (bf16 weights updated in place unless `dtype`
     -- then weights of that dtype, their own masters --, fp32 momentum): median ms per
     optimizer step and useful NS TFLOP/s."""
     from dmuon_amd.optim.newton_schulz import ns_useful_flops
@@ -454,7 +454,7 @@ def nt_roofline(prof: dict, prof_steps: int) -> dict:
 
 
 def run_config(torch, dmuon, dev, name: str, ns) -> dict:
-    """The GPU leg of BASELINE config `name` (c1: the literal fp32 plumbing config with Keller's
+    """The GPU leg of benchmark config `name` (c1: the literal fp32 plumbing config with Keller's
     direct NS; c2-c4 with the NS form `ns`)."""
     if name == "c1":
         keller = dmuon.NewtonSchulz("direct", coefficients=KELLER)
@@ -542,7 +542,7 @@ def main():
     ap.add_argument("--overlap-staging", action="store_true",
                     help="Muon(overlap_staging=True): stage the next chunk on a second stream")
     ap.add_argument("--config-only", choices=("c1", "c2", "c3", "c4"), default=None,
-                    help="only run that BASELINE config leg on the GPU (its own matrices) and "
+                    help="only run that benchmark config leg on the GPU (its own matrices) and "
                          "print its JSON line (for profiling one config)")
     ap.add_argument("--tile-cost", action="store_true",
                     help="only measure the triangle products' fixed cost per tile wave (a K "

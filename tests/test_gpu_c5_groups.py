@@ -1,4 +1,4 @@
-"""The headline workload's grouped path at its real batch sizes (BASELINE c5, the Llama-3-8B
+"""The headline workload's grouped path at its real batch sizes (benchmark config c5, the Llama-3-8B
 matrix set): Muon.step over the q/o bucket (64 x 4096^2, one chunk) and over the MLP bucket
 (32 down 4096 x 14336 and 64 gate/up 14336 x 4096 of 32 layers: three 32-matrix chunks, the
 first with n_transposed = 0, the other two with every member stored transposed), two optimizer

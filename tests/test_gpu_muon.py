@@ -1,6 +1,6 @@
 """GPU parity of the full Muon step through the drop-in API (dedicate_params + Muon.step).
 
-c1 (fp32 1024^2 weight, one step, lr 0.02, mu 0.95 Nesterov, wd 0.1,
+Benchmark configs: c1 (fp32 1024^2 weight, one step, lr 0.02, mu 0.95 Nesterov, wd 0.1,
 Keller x5) against the CPU oracle of muon.py:1683-1740; multi-step momentum bit-exact; c3/c4
 shapes at reduced size; and the c5 Llama-3-8B layer shapes at full size, where the weight
 update is checked bit-exactly against U from the stand-alone NS entry point and the momentum

@@ -6,7 +6,7 @@ Small sizes: against the CPU oracle on identical seeded inputs --
   * the reference's fp16 pipeline (direct_newton_schulz / gram_newton_schulz) within the
     north-star bf16 tolerance (relative Frobenius <= 2e-2),
   * the exact fp64 closed form.
-Full BASELINE sizes: size-independent properties -- transpose equivariance, scale invariance,
+Full benchmark sizes: size-independent properties -- transpose equivariance, scale invariance,
 bit-exact determinism, and the closed-form spectrum (singular values of U equal f(sigma(X))).
 """
 import zlib

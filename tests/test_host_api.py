@@ -94,7 +94,7 @@ def test_no_cpu_fallback():
 def test_useful_flops_formula():
     from dmuon_amd.optim.newton_schulz import ns_useful_flops
 
-    # BASELINE figures: c2 4096^2 -> 1.3746 TF, c5 set -> 471.81 TF
+    # the benchmark's FLOP figures: c2 4096^2 -> 1.3746 TF, c5 set -> 471.81 TF
     assert ns_useful_flops(4096, 4096) / 1e12 == pytest.approx(1.3746, abs=1e-4)
     c5 = 32 * (2 * ns_useful_flops(4096, 4096) + 2 * ns_useful_flops(1024, 4096)
                + 2 * ns_useful_flops(14336, 4096) + ns_useful_flops(4096, 14336))
